@@ -1,0 +1,292 @@
+"""Benchmark of the neighbourhood-search hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+
+North-star workload ("PointNet++ MSG layer"): B=32
+clouds of N=4096 points on 1-4 noisy spheres; one step is
+
+    FPS npoint=1024 -> ball_query(r, K) for (0.1,16), (0.2,32), (0.4,128)
+    -> knn(centres, cloud, 16)
+
+and the metric is points/s = B*N / (t_FPS + sum t_ball + t_kNN), inputs
+resident in HBM.  Prints one JSON line with the roofline of the dominant kernel
+(timed with HIP events on the launch stream) and the CPU baseline (this
+build's PyTorch-CPU port of the reference's algorithms, oracle/torch_port.py,
+on a bounded sample of the same workload).
+
+The input generators for all five BASELINE.json configs live here so the
+tests build exactly the benchmarked data.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import subprocess
+import sys
+import time
+from pathlib import Path
+
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT / "mps-pointops_amd"))
+
+# ------------------------------------------------------------- workloads
+
+
+def make_c1(seed: int = 1) -> torch.Tensor:
+    """Config 1: B=16, N=1024 uniform in [-1,1]^3."""
+    g = torch.Generator().manual_seed(seed)
+    return 2 * torch.rand(16, 1024, 3, generator=g) - 1
+
+
+def make_c2(seed: int = 2, B: int = 32, N: int = 4096) -> torch.Tensor:
+    """Config 2: per cloud 1-4 spheres (radius U[0.2,0.8], centre U[-0.5,0.5]^3),
+    points split evenly over the spheres, on-sphere by normalised randn, plus
+    N(0, 0.01) noise."""
+    g = torch.Generator().manual_seed(seed)
+    clouds = []
+    for _ in range(B):
+        ns = int(torch.randint(1, 5, (1,), generator=g))
+        radii = 0.2 + 0.6 * torch.rand(ns, generator=g)
+        centres = torch.rand(ns, 3, generator=g) - 0.5
+        counts = [N // ns + (1 if i < N % ns else 0) for i in range(ns)]
+        parts = []
+        for s in range(ns):
+            d = torch.randn(counts[s], 3, generator=g)
+            d = d / d.norm(dim=1, keepdim=True).clamp_min(1e-12)
+            parts.append(centres[s] + radii[s] * d)
+        cloud = torch.cat(parts) + 0.01 * torch.randn(N, 3, generator=g)
+        clouds.append(cloud)
+    return torch.stack(clouds).float().contiguous()
+
+
+def make_c3(seed: int = 3, N: int = 1 << 20) -> torch.Tensor:
+    """Config 3: one LiDAR-like slab, x,y in [-50,50]^2 accepted with
+    probability 1/(1+r^2), z U[0,4]."""
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    have = 0
+    while have < N:
+        xy = torch.rand(1 << 22, 2, generator=g, dtype=torch.float64) * 100 - 50
+        r2 = (xy * xy).sum(1)
+        keep = torch.rand(1 << 22, generator=g, dtype=torch.float64) < 1.0 / (1.0 + r2)
+        xy = xy[keep]
+        out.append(xy)
+        have += len(xy)
+    xy = torch.cat(out)[:N]
+    z = torch.rand(N, 1, generator=g, dtype=torch.float64) * 4
+    return torch.cat([xy, z], 1).float().unsqueeze(0).contiguous()
+
+
+def make_c4(seed: int = 4) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Config 4: ref 1,048,576 and 131,072 queries uniform in [0,10]^3, plus
+    DGCNN features randn(8, 2048, 64)."""
+    g = torch.Generator().manual_seed(seed)
+    ref = torch.rand(1, 1 << 20, 3, generator=g) * 10
+    query = torch.rand(1, 131072, 3, generator=g) * 10
+    feat = torch.randn(8, 2048, 64, generator=g)
+    return ref, query, feat
+
+
+def make_c5(seed: int = 5, B: int = 32, P: int = 8192) -> tuple[torch.Tensor, torch.Tensor]:
+    """Config 5: y1 on the unit sphere, y2 = y1 + N(0,0.02) with 10% of points
+    (first floor(0.1P) of a seeded permutation) replaced by U[-1,1]^3."""
+    g = torch.Generator().manual_seed(seed)
+    y1 = torch.randn(B, P, 3, generator=g)
+    y1 = y1 / y1.norm(dim=-1, keepdim=True).clamp_min(1e-12)
+    y2 = y1 + 0.02 * torch.randn(B, P, 3, generator=g)
+    m = P // 10
+    for b in range(B):
+        sel = torch.randperm(P, generator=g)[:m]
+        y2[b, sel] = torch.rand(m, 3, generator=g) * 2 - 1
+    return y1.contiguous(), y2.contiguous()
+
+
+C2_RADII = ((0.1, 16), (0.2, 32), (0.4, 128))
+C2_NPOINT = 1024
+C2_KNN_K = 16
+
+# ---------------------------------------------------------------- timing
+
+MI355X_HBM_BYTES_PER_S = 8.0e12
+# FP32 VALU without packed math or FMA: 256 CUs x 64 lanes x 2.4 GHz op/s is
+# the issue-rate ceiling of this build; the published vector-FP32 peak
+# (157.3 TFLOP/s) counts packed FMA (4 flops per lane-cycle).
+MI355X_FP32_PEAK = 157.3e12
+
+
+class KernelTimer:
+    """HIP-event timing on the stream the kernels are launched on."""
+
+    def __init__(self, stream):
+        self.stream = stream
+
+    def time(self, fn, reps: int) -> float:
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(self.stream)
+        for _ in range(reps):
+            fn()
+        end.record(self.stream)
+        end.synchronize()
+        return start.elapsed_time(end) / 1e3 / reps
+
+
+def cpu_info() -> dict:
+    model = platform.processor() or ""
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except (OSError, subprocess.SubprocessError):
+        pass
+    return {"model": model, "os_cpu_count": os.cpu_count()}
+
+
+def cpu_baseline(xyz_cpu: torch.Tensor, clouds: int) -> dict:
+    """The reference's CPU algorithms (PyTorch-CPU port) on the first
+    `clouds` clouds of the config-2 input, scaled to points/s."""
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_port
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = xyz_cpu[:clouds].contiguous()
+    t0 = time.perf_counter()
+    idx = torch_port.furthest_point_sample(x, C2_NPOINT)
+    t1 = time.perf_counter()
+    centres = x.gather(1, idx[..., None].expand(-1, -1, 3))
+    t_ball = 0.0
+    for radius, k in C2_RADII:
+        s = time.perf_counter()
+        torch_port.ball_query(centres, x, radius, k)
+        t_ball += time.perf_counter() - s
+    s = time.perf_counter()
+    torch_port.knn(centres, x, C2_KNN_K)
+    t_knn = time.perf_counter() - s
+    total = (t1 - t0) + t_ball + t_knn
+    return {
+        "value": clouds * x.shape[1] / total,
+        "unit": "points/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"{clouds} of 32 clouds of config 2 (N=4096): FPS 1024 + 3 ball queries + kNN16, "
+                  f"PyTorch-CPU port of reference.py; fps {t1 - t0:.3f}s ball {t_ball:.3f}s "
+                  f"knn {t_knn:.3f}s",
+        "cpu": cpu_info(),
+    }
+
+
+def run(args) -> dict:
+    import mps_pointops as mp
+
+    device = torch.device("cuda", 0)
+    xyz_cpu = make_c2()
+    xyz = xyz_cpu.to(device)
+    B, N, _ = xyz.shape
+    stream = torch.cuda.current_stream(device)
+    timer = KernelTimer(stream)
+
+    state = {}
+
+    def fps():
+        state["idx"] = mp.furthest_point_sample(xyz, C2_NPOINT)
+
+    fps()
+    torch.cuda.synchronize()
+    centres = xyz.gather(1, state["idx"][..., None].expand(-1, -1, 3)).contiguous()
+
+    def balls():
+        for radius, k in C2_RADII:
+            mp.ball_query(centres, xyz, radius, k)
+
+    def knn():
+        mp.knn(centres, xyz, C2_KNN_K)
+
+    def step():
+        fps()
+        balls()
+        knn()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    # Whole-step wall time over exactly K steps.
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / args.steps
+
+    # Per-op kernel time on the launch stream (HIP events).
+    reps = max(5, args.steps)
+    t_fps = timer.time(fps, reps)
+    t_ball = timer.time(balls, reps)
+    t_knn = timer.time(knn, reps)
+    t_sum = t_fps + t_ball + t_knn
+    value = B * N / t_sum
+
+    # Roofline of the dominant kernel (FPS): 9 FP32 ops per point per step
+    # (3 sub, 3 mul, 2 add, 1 min) over B*npoint*N point-steps.
+    fps_ops = 9.0 * B * C2_NPOINT * N
+    achieved = fps_ops / t_fps
+    result = {
+        "metric": "points/sec for FPS+ball_query+kNN at B=32,N=4096; % of HBM/FP32 roofline",
+        "value": value,
+        "unit": "points/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": wall * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (BASELINE.json config 2 generator, seed 2)",
+        "config": {
+            "workload": "c2 PointNet++ MSG layer: B=32 N=4096 FPS1024 + ball(0.1,16)(0.2,32)"
+                        "(0.4,128) + kNN16",
+            "B": B, "N": N, "npoint": C2_NPOINT,
+        },
+        "breakdown_ms": {"fps": t_fps * 1e3, "ball_query_x3": t_ball * 1e3, "knn": t_knn * 1e3},
+        "roofline": {
+            "kernel": "fps_regs_kernel<16,256>",
+            "bound": "valu",
+            "achieved": achieved / 1e12,
+            "peak": MI355X_FP32_PEAK / 1e12,
+            "unit": "TFLOP/s",
+            "frac": achieved / MI355X_FP32_PEAK,
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(xyz_cpu, args.cpu_clouds)
+    return result
+
+
+def main() -> None:
+    parser = argparse.ArgumentParser()
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--cpu-clouds", type=int, default=32)
+    args = parser.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build measures one MI355X; every workload here runs on one "
+                          "GPU (batch sharding across GPUs is described in DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    result = run(args)
+    print(json.dumps(result))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,185 @@
+/*
+ * C ABI of libpointops_hip.so: MI355X (gfx950) kernels for the
+ * neighbourhood-search hot path of mps_pointops.
+ *
+ * Conventions (every entry point):
+ *   - All pointers are DEVICE pointers to contiguous row-major arrays owned by
+ *     the caller.  The library never allocates, frees or synchronises; scratch
+ *     and workspace buffers are passed in (their size comes from the
+ *     matching *_bytes query).
+ *   - Sizes are int64_t element counts; float arithmetic is IEEE binary32
+ *     (binary64 for the *_f64 entries) with no contraction and no fast-math.
+ *   - Work is enqueued on `stream`; the return value is hipSuccess or the
+ *     error of the launch.  Argument errors return hipErrorInvalidValue
+ *     before anything is enqueued.
+ *
+ * Each entry point replaces one `lib.<kernel>(...)` enqueue of the reference
+ * (/root/reference/mps_pointops), cited below as file:line.
+ */
+#ifndef POINTOPS_HIP_H
+#define POINTOPS_HIP_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ABI version of this header (bumped on any signature change). */
+int pointops_abi_version(void);
+
+/* Non-zero when `device` is a gfx950 agent this library was built for. */
+int pointops_device_supported(int device);
+
+/* ------------------------------------------------------------------ FPS */
+
+/* Dense batched farthest point sampling.  Replaces ops.py:271-274
+ * (`_library("fps").furthest_point_sample`, kernels/fps.metal:19-107).
+ * xyz (B,N,3) f32 -> out (B,npoint) int64; ties go to the smaller index; once
+ * every point is taken the rest repeat the first maximum (index 0).
+ * `scratch` must hold pointops_fps_dense_scratch_bytes(B, N) bytes (0 means
+ * it may be NULL: the running distances then live on chip). */
+size_t pointops_fps_dense_scratch_bytes(int64_t B, int64_t N);
+hipError_t pointops_fps_dense(const float *xyz, int64_t *out, void *scratch, int64_t B,
+                              int64_t N, int64_t npoint, int64_t start_idx,
+                              int32_t skip_near_origin, hipStream_t stream);
+
+/* Large single-cloud FPS (B = 1): one persistent cooperative launch over all
+ * CUs with a per-step device-wide argmax.  Replaces the 2*(npoint-1)
+ * dispatch loop of ops.py:253-270 (kernels/fps_multigroup.metal:10-133).
+ * `workspace` must hold pointops_fps_large_workspace_bytes(N, npoint) bytes
+ * and be zero-filled by the caller before every call. */
+size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint);
+hipError_t pointops_fps_large(const float *xyz, int64_t *out, void *workspace, int64_t N,
+                              int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
+                              hipStream_t stream);
+
+/* Ragged FPS (torch_cluster layout).  Replaces _flat_fps_mps.py:86-95
+ * (kernels/fps_flat.metal:7-96).  Cloud b is x[ptr[b]:ptr[b+1]]; its samples
+ * go to out[out_ptr[b]:out_ptr[b+1]] as global indices starting from the
+ * local index starts[b].  `max_len` is max_b(ptr[b+1]-ptr[b]); `scratch` must
+ * hold pointops_fps_flat_scratch_bytes(total_n, max_len) bytes. */
+size_t pointops_fps_flat_scratch_bytes(int64_t total_n, int64_t max_len);
+hipError_t pointops_fps_flat(const float *x, const int64_t *ptr, const int64_t *out_ptr,
+                             const int64_t *starts, int64_t *out, void *scratch,
+                             int64_t batch, int64_t total_n, int64_t max_len,
+                             hipStream_t stream);
+
+/* ------------------------------------------------------------------ kNN */
+
+/* Dense exact kNN, D = 3.  Replaces ops.py:329-333 (kernels/knn.metal:32-140).
+ * query (B,M,3), ref (B,N,3) -> dist (B,M,K) Euclidean, idx (B,M,K) int64,
+ * sorted by (fl32 squared distance, index).  NaN distances never match;
+ * unfilled slots are (inf, 4294967295).  1 <= K <= 256. */
+hipError_t pointops_knn3(const float *query, const float *ref, float *dist, int64_t *idx,
+                         int64_t B, int64_t M, int64_t N, int64_t K, hipStream_t stream);
+
+/* Dense exact kNN in D dimensions (sequential per-dimension accumulation).
+ * Replaces ops.py:334-338 (kernels/feature_knn.metal:133-164).  Non-finite
+ * queries and non-finite distances never match; unfilled slots are (inf, -1). */
+hipError_t pointops_knn_feat(const float *query, const float *ref, float *dist, int64_t *idx,
+                             int64_t B, int64_t M, int64_t N, int64_t D, int64_t K,
+                             hipStream_t stream);
+
+/* Flat (ragged) kNN, global x indices padded with -1, (Q,K).  Replaces
+ * _flat_search_mps.py:192-203 (kernels/flat_search.metal:140-250 for D = 3,
+ * kernels/feature_knn.metal:166-199 otherwise).  y (Q,D) queries, x (Nx,D)
+ * references, ptr_y/ptr_x (batch+1,) segment offsets. */
+hipError_t pointops_knn_flat(const float *y, const float *x, const int64_t *ptr_y,
+                             const int64_t *ptr_x, int64_t *out, int64_t Q, int64_t batch,
+                             int64_t D, int64_t K, hipStream_t stream);
+
+/* ----------------------------------------------------------- ball query */
+
+/* Dense first-K ball query (PyTorch3D convention).  Replaces
+ * _ball_query_mps.py:139-162 (kernels/ball_query.metal:126-166).  The first K
+ * points j in input order with fl32((dx^2+dy^2)+dz^2) < radius_sq; empty
+ * slots are (idx -1, dist2 0).  Queries at or beyond query_lengths[b] are
+ * padding; only points below point_lengths[b] are scanned.  The _f16 entry
+ * takes IEEE half coordinates (uint16 bit patterns) widened exactly. */
+hipError_t pointops_ball_query_f32(const float *queries, const float *points,
+                                   const int64_t *query_lengths, const int64_t *point_lengths,
+                                   int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
+                                   int64_t K, float radius_sq, hipStream_t stream);
+hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *points,
+                                   const int64_t *query_lengths, const int64_t *point_lengths,
+                                   int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
+                                   int64_t K, float radius_sq, hipStream_t stream);
+
+/* Flat radius search (torch_cluster convention): first K global x indices
+ * with squared distance < radius_sq, padded with -1, (Q,K); optional
+ * exclusion of x index == y index before the cap.  Replaces
+ * _flat_search_mps.py:230-242 (kernels/flat_search.metal:229-275). */
+hipError_t pointops_radius_flat_f32(const float *y, const float *x, const int64_t *ptr_y,
+                                    const int64_t *ptr_x, int64_t *out, int64_t Q,
+                                    int64_t batch, int64_t K, float radius_sq,
+                                    int32_t ignore_same_index, hipStream_t stream);
+hipError_t pointops_radius_flat_f16(const uint16_t *y, const uint16_t *x, const int64_t *ptr_y,
+                                    const int64_t *ptr_x, int64_t *out, int64_t Q,
+                                    int64_t batch, int64_t K, float radius_sq,
+                                    int32_t ignore_same_index, hipStream_t stream);
+
+/* ------------------------------------------------- PointNet++ propagation */
+
+/* Three nearest known points per unknown point (stable index order on equal
+ * squared distance, NaN last).  Replaces pointnet2.py:94-99
+ * (kernels/pointnet2.metal:8-50).  unknown (B,N,3), known (B,M,3), M >= 3 ->
+ * dist (B,N,3) Euclidean, idx (B,N,3) int32. */
+hipError_t pointops_three_nn(const float *unknown, const float *known, float *dist,
+                             int32_t *idx, int64_t B, int64_t N, int64_t M, hipStream_t stream);
+
+/* out[b,c,n] = (f[b,c,i0]*w0 + f[b,c,i1]*w1) + f[b,c,i2]*w2.  Replaces
+ * pointnet2.py:156-162 (kernels/pointnet2.metal:52-71).  features (B,C,M),
+ * idx (B,N,3) int32 in [0,M), weights (B,N,3) -> out (B,C,N). */
+hipError_t pointops_three_interpolate(const float *features, const int32_t *idx,
+                                      const float *weights, float *out, int64_t B, int64_t C,
+                                      int64_t M, int64_t N, hipStream_t stream);
+
+/* grad_features[b,c,i_t] += grad_out[b,c,n] * w[b,n,t] (float atomics;
+ * summation order, hence the last bits, is not deterministic).  The caller
+ * zero-fills grad_features.  Replaces pointnet2.py:179-186
+ * (kernels/pointnet2.metal:85-103). */
+hipError_t pointops_three_interpolate_backward(const float *grad_out, const int32_t *idx,
+                                               const float *weights, float *grad_features,
+                                               int64_t B, int64_t C, int64_t M, int64_t N,
+                                               hipStream_t stream);
+
+/* -------------------------------------------------------------- Chamfer */
+
+/* Nearest reference per query (K = 1), first minimum index on ties, under
+ * squared L2 (norm 2) or L1 (norm 1) in D dimensions.  Replaces
+ * chamfer.py:136-157 (kernels/chamfer_nn.metal:13-226).  Rows at or beyond
+ * query_lengths[b] and rows of an empty reference cloud are (0, -1). */
+hipError_t pointops_chamfer_nearest_f32(const float *query, const float *ref,
+                                        const int64_t *query_lengths,
+                                        const int64_t *ref_lengths, float *dist, int64_t *idx,
+                                        int64_t B, int64_t Q, int64_t R, int64_t D,
+                                        int32_t norm, hipStream_t stream);
+hipError_t pointops_chamfer_nearest_f64(const double *query, const double *ref,
+                                        const int64_t *query_lengths,
+                                        const int64_t *ref_lengths, double *dist, int64_t *idx,
+                                        int64_t B, int64_t Q, int64_t R, int64_t D,
+                                        int32_t norm, hipStream_t stream);
+
+/* Chamfer backward for selected pairs.  norm 2: gq = (q - ref[idx]) * (2 g);
+ * norm 1: gq = (q > ref[idx] ? 1 : -1) * g; grad_ref[idx] -= gq (float
+ * atomics).  Rows with idx < 0 get 0.  The caller zero-fills grad_ref.
+ * Replaces the PyTorch gather/scatter_add_ of chamfer.py:227-294. */
+hipError_t pointops_chamfer_backward_f32(const float *query, const float *ref,
+                                         const int64_t *idx, const float *grad_dist,
+                                         float *grad_query, float *grad_ref, int64_t B,
+                                         int64_t Q, int64_t R, int64_t D, int32_t norm,
+                                         hipStream_t stream);
+hipError_t pointops_chamfer_backward_f64(const double *query, const double *ref,
+                                         const int64_t *idx, const double *grad_dist,
+                                         double *grad_query, double *grad_ref, int64_t B,
+                                         int64_t Q, int64_t R, int64_t D, int32_t norm,
+                                         hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* POINTOPS_HIP_H */

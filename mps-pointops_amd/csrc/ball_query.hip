@@ -1,0 +1,200 @@
+// First-K radius search for gfx950.
+//
+// One wave per query scans the candidate points in input order, 64 per block
+// (lane l <-> point base + l).  A hit is fl32((dx^2 + dy^2) + dz^2) < r2 with
+// the reference's separately rounded arithmetic (reference.py:96-134); NaN and
+// overflowed distances never satisfy `<`.  The hits of a block take output
+// slots found + rank, where rank is the number of hit lanes below (ballot +
+// mbcnt), which keeps the first K hits in index order without atomics; the
+// scan stops as soon as K hits are found and the remaining slots are padded.
+//
+//   dense: _ball_query_mps.py:122-166 / kernels/ball_query.metal:30-166
+//          (query/point lengths, (idx -1, dist2 0) padding, f32 or f16 input)
+//   flat:  _flat_search_mps.py:207-243 / kernels/flat_search.metal:171-275
+//          (segments by ptr, global indices, -1 padding, optional exclusion of
+//          index == query index before the cap)
+#include <hip/hip_fp16.h>
+
+#include "pointops_common.hpp"
+#include "pointops_hip.h"
+
+namespace pointops {
+namespace {
+
+constexpr int kBqThreads = 256;
+constexpr int kBqWaves = kBqThreads / kWave;
+
+template <typename S>
+__device__ __forceinline__ float widen(S v);
+template <>
+__device__ __forceinline__ float widen<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float widen<uint16_t>(uint16_t v) {
+    return __half2float(__ushort_as_half(v));
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
+    const S* __restrict__ queries, const S* __restrict__ points,
+    const int64_t* __restrict__ query_lengths, const int64_t* __restrict__ point_lengths,
+    int64_t* __restrict__ out_idx, float* __restrict__ out_dist, int64_t B, int64_t Q, int64_t P,
+    int K, float r2) {
+    const int lane = lane_id();
+    const uint32_t blk = xcd_local_block(blockIdx.x, gridDim.x);
+    const int64_t row = static_cast<int64_t>(blk) * kBqWaves + uniform(threadIdx.x / kWave);
+    if (row >= B * Q) return;
+    const int64_t b = row / Q;
+    const int64_t qi = row - b * Q;
+    int64_t* oi = out_idx + row * K;
+    float* od = out_dist + row * K;
+    int found = 0;
+    if (qi < query_lengths[b]) {
+        const int64_t plen = point_lengths[b];
+        const int n = static_cast<int>(plen < P ? plen : P);
+        const S* qp = queries + 3 * row;
+        const float qx = widen(qp[0]), qy = widen(qp[1]), qz = widen(qp[2]);
+        const S* pp = points + 3 * b * P;
+        for (int base = 0; base < n; base += kWave) {
+            const int j = base + lane;
+            bool hit = false;
+            float d = 0.f;
+            if (j < n) {
+                const S* pt = pp + 3 * static_cast<int64_t>(j);
+                d = sqdist3(qx, qy, qz, widen(pt[0]), widen(pt[1]), widen(pt[2]));
+                hit = d < r2;
+            }
+            const uint64_t mask = ballot(hit);
+            if (mask == 0) continue;
+            const int slot = found + lanes_below(mask);
+            if (hit && slot < K) {
+                oi[slot] = j;
+                od[slot] = d;
+            }
+            found += __popcll(mask);
+            if (found >= K) {
+                found = K;
+                break;
+            }
+        }
+    }
+    for (int s = found + lane; s < K; s += kWave) {
+        oi[s] = -1;
+        od[s] = 0.f;
+    }
+}
+
+__device__ __forceinline__ int64_t segment_of(const int64_t* __restrict__ ptr, int64_t batch,
+                                              int64_t q) {
+    int64_t lo = 0, hi = batch;
+    while (lo < hi) {
+        const int64_t mid = lo + (hi - lo) / 2;
+        if (ptr[mid + 1] <= q) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+template <typename S>
+__global__ __launch_bounds__(kBqThreads) void radius_flat_kernel(
+    const S* __restrict__ y, const S* __restrict__ x, const int64_t* __restrict__ ptr_y,
+    const int64_t* __restrict__ ptr_x, int64_t* __restrict__ out, int64_t Q, int64_t batch, int K,
+    float r2, int ignore_same_index) {
+    const int lane = lane_id();
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * kBqWaves + uniform(threadIdx.x / kWave);
+    if (q >= Q) return;
+    const int64_t b = segment_of(ptr_y, batch, q);
+    const int64_t lo = ptr_x[b], hi = ptr_x[b + 1];
+    int64_t* o = out + q * K;
+    int found = 0;
+    if (r2 > 0.f) {
+        const float qx = widen(y[3 * q]), qy = widen(y[3 * q + 1]), qz = widen(y[3 * q + 2]);
+        for (int64_t base = lo; base < hi; base += kWave) {
+            const int64_t j = base + lane;
+            bool hit = false;
+            if (j < hi && !(ignore_same_index && j == q)) {
+                const S* pt = x + 3 * j;
+                const float d = sqdist3(widen(pt[0]), widen(pt[1]), widen(pt[2]), qx, qy, qz);
+                hit = d < r2;
+            }
+            const uint64_t mask = ballot(hit);
+            if (mask == 0) continue;
+            const int slot = found + lanes_below(mask);
+            if (hit && slot < K) o[slot] = j;
+            found += __popcll(mask);
+            if (found >= K) {
+                found = K;
+                break;
+            }
+        }
+    }
+    for (int s = found + lane; s < K; s += kWave) o[s] = -1;
+}
+
+template <typename S>
+hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t* pl, int64_t* idx,
+                       float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K, float r2,
+                       hipStream_t stream) {
+    if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kWave)
+        return hipErrorInvalidValue;
+    if (B == 0 || Q == 0 || K == 0) return hipSuccess;
+    const int64_t blocks = (B * Q + kBqWaves - 1) / kBqWaves;
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((ball_query_kernel<S>), dim3(static_cast<uint32_t>(blocks)), dim3(kBqThreads),
+                       0, stream, q, p, ql, pl, idx, dist2, B, Q, P, static_cast<int>(K), r2);
+    return hipGetLastError();
+}
+
+template <typename S>
+hipError_t launch_radius(const S* y, const S* x, const int64_t* ptr_y, const int64_t* ptr_x,
+                         int64_t* out, int64_t Q, int64_t batch, int64_t K, float r2, int ignore,
+                         hipStream_t stream) {
+    if (Q < 0 || batch < 0 || K < 0 || K > INT32_MAX) return hipErrorInvalidValue;
+    if (Q == 0 || K == 0) return hipSuccess;
+    const int64_t blocks = (Q + kBqWaves - 1) / kBqWaves;
+    if (batch == 0 || blocks > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((radius_flat_kernel<S>), dim3(static_cast<uint32_t>(blocks)), dim3(kBqThreads),
+                       0, stream, y, x, ptr_y, ptr_x, out, Q, batch, static_cast<int>(K), r2,
+                       ignore ? 1 : 0);
+    return hipGetLastError();
+}
+
+}  // namespace
+}  // namespace pointops
+
+using namespace pointops;
+
+extern "C" {
+
+hipError_t pointops_ball_query_f32(const float* queries, const float* points,
+                                   const int64_t* query_lengths, const int64_t* point_lengths,
+                                   int64_t* idx, float* dist2, int64_t B, int64_t Q, int64_t P,
+                                   int64_t K, float radius_sq, hipStream_t stream) {
+    return launch_ball<float>(queries, points, query_lengths, point_lengths, idx, dist2, B, Q, P, K,
+                              radius_sq, stream);
+}
+
+hipError_t pointops_ball_query_f16(const uint16_t* queries, const uint16_t* points,
+                                   const int64_t* query_lengths, const int64_t* point_lengths,
+                                   int64_t* idx, float* dist2, int64_t B, int64_t Q, int64_t P,
+                                   int64_t K, float radius_sq, hipStream_t stream) {
+    return launch_ball<uint16_t>(queries, points, query_lengths, point_lengths, idx, dist2, B, Q, P,
+                                 K, radius_sq, stream);
+}
+
+hipError_t pointops_radius_flat_f32(const float* y, const float* x, const int64_t* ptr_y,
+                                    const int64_t* ptr_x, int64_t* out, int64_t Q, int64_t batch,
+                                    int64_t K, float radius_sq, int32_t ignore_same_index,
+                                    hipStream_t stream) {
+    return launch_radius<float>(y, x, ptr_y, ptr_x, out, Q, batch, K, radius_sq, ignore_same_index,
+                                stream);
+}
+
+hipError_t pointops_radius_flat_f16(const uint16_t* y, const uint16_t* x, const int64_t* ptr_y,
+                                    const int64_t* ptr_x, int64_t* out, int64_t Q, int64_t batch,
+                                    int64_t K, float radius_sq, int32_t ignore_same_index,
+                                    hipStream_t stream) {
+    return launch_radius<uint16_t>(y, x, ptr_y, ptr_x, out, Q, batch, K, radius_sq,
+                                   ignore_same_index, stream);
+}
+
+}  // extern "C"

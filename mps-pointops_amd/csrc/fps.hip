@@ -1,0 +1,567 @@
+// Farthest point sampling for gfx950.
+//
+// Semantics (reference.py:40-71, kernels/fps.metal:19-107): sampling starts at
+// `start`; each step takes the point whose running minimum squared distance
+// to the sampled set is largest, ties to the smaller index; points with
+// ((x*x + y*y) + z*z) < fl32(1e-3) are never picked when skip_near_origin is
+// set (their running distance is -inf); if no point can be picked the step
+// takes index 0.
+//
+// Kernels:
+//   fps_regs_kernel<P,T>    one workgroup per cloud, the cloud's points and
+//                           running distances in VGPRs (P per thread), a
+//                           float4 copy in LDS for the centroid broadcast,
+//                           one barrier per step (double-buffered slots).
+//   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
+//                           LDS: points re-read from L2, running distances in
+//                           a caller-provided scratch array.
+//   fps_large_kernel<P,T>   one cloud over every CU (cooperative launch): each
+//                           workgroup keeps its chunk on chip and publishes a
+//                           tagged (distance, index, xyz) record per step;
+//                           every workgroup polls all records and reduces them.
+#include <hip/hip_cooperative_groups.h>
+
+#include "pointops_common.hpp"
+#include "pointops_hip.h"
+
+namespace pointops {
+namespace {
+
+constexpr float kSkipThreshold = 1e-3f;  // torch.tensor(1e-3, dtype=float32)
+
+__device__ __forceinline__ bool near_origin(float x, float y, float z) {
+    float mag = x * x;
+    mag = mag + y * y;
+    mag = mag + z * z;
+    return mag < kSkipThreshold;
+}
+
+// Segment of workgroup b: dense clouds (ptr == nullptr) or ragged ones.
+struct Segment {
+    int64_t in_lo;   // first point of the cloud
+    int64_t n;       // points in the cloud
+    int64_t out_lo;  // first output slot
+    int64_t cnt;     // samples to take
+    int64_t start;   // local start index
+    int64_t base;    // added to every emitted local index
+};
+
+__device__ __forceinline__ Segment segment_of(int b, const int64_t* ptr, const int64_t* out_ptr,
+                                              const int64_t* starts, int64_t N, int64_t npoint,
+                                              int64_t start) {
+    Segment s;
+    if (ptr != nullptr) {
+        s.in_lo = ptr[b];
+        s.n = ptr[b + 1] - s.in_lo;
+        s.out_lo = out_ptr[b];
+        s.cnt = out_ptr[b + 1] - s.out_lo;
+        s.start = starts[b];
+        s.base = s.in_lo;
+    } else {
+        s.in_lo = static_cast<int64_t>(b) * N;
+        s.n = N;
+        s.out_lo = static_cast<int64_t>(b) * npoint;
+        s.cnt = npoint;
+        s.start = start;
+        s.base = 0;
+    }
+    return s;
+}
+
+// Block-wide argmax of (value, index) pairs held one per wave in `slots`:
+// largest value, then smallest index.  Every thread gets the result.
+template <int NW>
+__device__ __forceinline__ int block_argmax(const int2* slots) {
+    float best = i2f(slots[0].x);
+    int bidx = slots[0].y;
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+        const float v = i2f(slots[w].x);
+        const int i = slots[w].y;
+        if (v > best || (v == best && i < bidx)) {
+            best = v;
+            bidx = i;
+        }
+    }
+    return bidx;
+}
+
+template <int P, int T>
+__global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ xyz,
+                                                     const int64_t* __restrict__ ptr,
+                                                     const int64_t* __restrict__ out_ptr,
+                                                     const int64_t* __restrict__ starts,
+                                                     int64_t* __restrict__ out, int64_t N,
+                                                     int64_t npoint, int64_t start, int skip) {
+    constexpr int NW = T / kWave;
+    __shared__ float4 spts[P * T];
+    __shared__ int2 slots[2][NW];
+
+    const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
+    if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
+    const float* p = xyz + 3 * seg.in_lo;
+    int64_t* o = out + seg.out_lo;
+    const int n = static_cast<int>(seg.n);
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+
+    float px[P], py[P], pz[P], md[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid + k * T;
+        if (j < n) {
+            const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
+            px[k] = x;
+            py[k] = y;
+            pz[k] = z;
+            md[k] = (skip && near_origin(x, y, z)) ? -INFINITY : INFINITY;
+            spts[j] = make_float4(x, y, z, 0.f);
+        } else {
+            px[k] = py[k] = pz[k] = 0.f;
+            md[k] = -INFINITY;  // never a candidate
+        }
+    }
+    __syncthreads();
+
+    int far = static_cast<int>(seg.start);
+    for (int64_t step = 0; step < seg.cnt; ++step) {
+        if (tid == 0) o[step] = seg.base + far;
+        if (step + 1 == seg.cnt) break;
+        const float4 c = spts[far];
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const float d = sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z);
+            const float m = fminf(md[k], d);
+            md[k] = m;
+            // k grows with the index inside a thread: strict > keeps the smaller one.
+            if (m > bv) {
+                bv = m;
+                bi = tid + k * T;
+            }
+        }
+        const float wv = wave_max(bv);
+        const int wi = wave_min(bv == wv ? bi : INT_MAX);
+        int2* buf = slots[step & 1];
+        if (lane == 0) buf[wave] = make_int2(f2i(wv), wi);
+        __syncthreads();
+        const int win = block_argmax<NW>(buf);
+        far = (win == INT_MAX) ? 0 : win;
+    }
+}
+
+template <int T>
+__global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__ xyz,
+                                                       const int64_t* __restrict__ ptr,
+                                                       const int64_t* __restrict__ out_ptr,
+                                                       const int64_t* __restrict__ starts,
+                                                       int64_t* __restrict__ out,
+                                                       float* __restrict__ scratch, int64_t N,
+                                                       int64_t npoint, int64_t start, int skip) {
+    constexpr int NW = T / kWave;
+    __shared__ int2 slots[2][NW];
+    const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
+    if (seg.cnt <= 0) return;
+    const float* p = xyz + 3 * seg.in_lo;
+    float* md = scratch + seg.in_lo;
+    int64_t* o = out + seg.out_lo;
+    const int64_t n = seg.n;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+
+    for (int64_t j = tid; j < n; j += T) {
+        md[j] = (skip && near_origin(p[3 * j], p[3 * j + 1], p[3 * j + 2])) ? -INFINITY : INFINITY;
+    }
+    int64_t far = seg.start;
+    for (int64_t step = 0; step < seg.cnt; ++step) {
+        if (tid == 0) o[step] = seg.base + far;
+        if (step + 1 == seg.cnt) break;
+        const float cx = p[3 * far], cy = p[3 * far + 1], cz = p[3 * far + 2];
+        float bv = -INFINITY;
+        int bi = INT_MAX;
+        for (int64_t j = tid; j < n; j += T) {
+            const float d = sqdist3(p[3 * j], p[3 * j + 1], p[3 * j + 2], cx, cy, cz);
+            const float m = fminf(md[j], d);
+            md[j] = m;
+            if (m > bv) {
+                bv = m;
+                bi = static_cast<int>(j);
+            }
+        }
+        const float wv = wave_max(bv);
+        const int wi = wave_min(bv == wv ? bi : INT_MAX);
+        int2* buf = slots[step & 1];
+        if (lane == 0) buf[wave] = make_int2(f2i(wv), wi);
+        __syncthreads();
+        const int win = block_argmax<NW>(buf);
+        far = (win == INT_MAX) ? 0 : win;
+    }
+}
+
+// ------------------------------------------------------------ large cloud
+
+// Per-step record published by each workgroup: four 64-bit words written with
+// agent-scope atomic stores, each carrying the step tag so that a reader can
+// tell a complete record of this step from a stale one two steps back
+// (records are double-buffered by step parity).
+//   w0 = vkey << 32 | tag << 21 | (~idx & 0x1FFFFF)
+//   w1 = x_bits << 32 | tag,  w2 = y_bits << 32 | tag,  w3 = z_bits << 32 | tag
+// vkey = 0 when the workgroup has no candidate, else float bits + 1 (running
+// distances are >= +0 for candidates, so the bits order like the values).
+constexpr int kLargeIdxBits = 21;
+constexpr uint32_t kLargeIdxMask = (1u << kLargeIdxBits) - 1u;
+constexpr int64_t kLargeMaxN = int64_t(1) << kLargeIdxBits;
+constexpr uint32_t kSpinLimit = 1u << 22;
+
+__device__ __forceinline__ uint32_t step_tag(int64_t step) {
+    return (static_cast<uint32_t>(step >> 1) & 0x3FFu) | 0x400u;  // never 0
+}
+
+template <int P, int T>
+__global__ __launch_bounds__(T) void fps_large_kernel(const float* __restrict__ xyz,
+                                                      int64_t* __restrict__ out,
+                                                      uint64_t* __restrict__ records,
+                                                      uint32_t* __restrict__ status, int N,
+                                                      int64_t npoint, int start, int skip,
+                                                      int chunk) {
+    constexpr int NW = T / kWave;
+    __shared__ int2 slots[2][NW];
+    __shared__ uint64_t red_key[NW];
+    __shared__ int red_src[NW];
+    __shared__ float4 centroid;
+    __shared__ int abort_flag;
+
+    const int G = gridDim.x;
+    const int g = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int lo = g * chunk;
+    const int n = max(0, min(chunk, N - lo));
+    const float* p = xyz + 3 * static_cast<int64_t>(lo);
+
+    float px[P], py[P], pz[P], md[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid + k * T;
+        if (j < n) {
+            const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
+            px[k] = x;
+            py[k] = y;
+            pz[k] = z;
+            md[k] = (skip && near_origin(x, y, z)) ? -INFINITY : INFINITY;
+        } else {
+            px[k] = py[k] = pz[k] = 0.f;
+            md[k] = -INFINITY;
+        }
+    }
+    if (tid == 0) abort_flag = 0;
+
+    int far = start;
+    float cx = xyz[3 * static_cast<int64_t>(far)];
+    float cy = xyz[3 * static_cast<int64_t>(far) + 1];
+    float cz = xyz[3 * static_cast<int64_t>(far) + 2];
+    for (int64_t step = 0; step < npoint; ++step) {
+        if (g == 0 && tid == 0) out[step] = far;
+        if (step + 1 == npoint) break;
+
+        // Local (value, index) argmax of this workgroup's chunk.
+        float bv = -INFINITY;
+        int bk = -1;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const float d = sqdist3(px[k], py[k], pz[k], cx, cy, cz);
+            const float m = fminf(md[k], d);
+            md[k] = m;
+            if (m > bv) {
+                bv = m;
+                bk = k;
+            }
+        }
+        const int bi = bk < 0 ? INT_MAX : lo + tid + bk * T;
+        const float wv = wave_max(bv);
+        const int wi = wave_min(bv == wv ? bi : INT_MAX);
+        int2* buf = slots[step & 1];
+        if (lane == 0) buf[wave] = make_int2(f2i(wv), wi);
+        __syncthreads();
+        const int win = block_argmax<NW>(buf);
+        float winv = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w)
+            if (buf[w].y == win) winv = i2f(buf[w].x);
+
+        // The owner of the local winner publishes the record.
+        const uint32_t tag = step_tag(step);
+        uint64_t* rec = records + ((step & 1) * static_cast<int64_t>(G) + g) * 4;
+        const int owner = (win == INT_MAX) ? 0 : ((win - lo) % T);
+        if (tid == owner) {
+            uint32_t vkey = 0;
+            float wx = 0.f, wy = 0.f, wz = 0.f;
+            if (win != INT_MAX) {
+                vkey = static_cast<uint32_t>(f2i(winv)) + 1u;
+                const int kk = (win - lo) / T;
+#pragma unroll
+                for (int k = 0; k < P; ++k) {
+                    if (k == kk) {
+                        wx = px[k];
+                        wy = py[k];
+                        wz = pz[k];
+                    }
+                }
+            }
+            const uint64_t w0 = (static_cast<uint64_t>(vkey) << 32) |
+                                (static_cast<uint64_t>(tag) << kLargeIdxBits) |
+                                (~static_cast<uint32_t>(win) & kLargeIdxMask);
+            __hip_atomic_store(rec + 1, (static_cast<uint64_t>(f2i(wx)) << 32) | tag,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(rec + 2, (static_cast<uint64_t>(f2i(wy)) << 32) | tag,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(rec + 3, (static_cast<uint64_t>(f2i(wz)) << 32) | tag,
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(rec + 0, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+
+        // Poll every workgroup's record of this step (thread t reads records
+        // t, t+T, ...), keep the best complete one.
+        uint64_t best = 0;
+        int best_src = -1;
+        const uint64_t* base = records + (step & 1) * static_cast<int64_t>(G) * 4;
+        for (int r = tid; r < G; r += T) {
+            const uint64_t* q = base + 4 * r;
+            uint32_t spins = 0;
+            uint64_t w0, w1, w2, w3;
+            while (true) {
+                w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const bool ready = ((w0 >> kLargeIdxBits) & 0x7FFu) == tag &&
+                                   static_cast<uint32_t>(w1) == tag &&
+                                   static_cast<uint32_t>(w2) == tag &&
+                                   static_cast<uint32_t>(w3) == tag;
+                if (ready) break;
+                if (++spins > kSpinLimit || __hip_atomic_load(status, __ATOMIC_RELAXED,
+                                                              __HIP_MEMORY_SCOPE_AGENT)) {
+                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    abort_flag = 1;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            // Order: vkey, then ~idx (tag bits are equal for every record).
+            const uint64_t key = (w0 & 0xFFFFFFFF00000000ull) | (w0 & kLargeIdxMask);
+            if (best_src < 0 || key > best) {
+                best = key;
+                best_src = r;
+            }
+            (void)w1;
+            (void)w2;
+            (void)w3;
+        }
+        // Wave reduction of (key, src) with shuffles (one per step), then a
+        // block reduction through LDS.
+        uint64_t k64 = best_src < 0 ? 0 : best;
+        int s64 = best_src;
+        for (int off = 32; off >= 1; off >>= 1) {
+            const uint64_t ok = __shfl_xor(k64, off);
+            const int os = __shfl_xor(s64, off);
+            if (os >= 0 && (s64 < 0 || ok > k64)) {
+                k64 = ok;
+                s64 = os;
+            }
+        }
+        if (lane == 0) {
+            red_key[wave] = k64;
+            red_src[wave] = s64;
+        }
+        __syncthreads();
+        if (abort_flag) return;  // uniform: read after the barrier
+        uint64_t gk = red_key[0];
+        int gs = red_src[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            if (red_src[w] >= 0 && (gs < 0 || red_key[w] > gk)) {
+                gk = red_key[w];
+                gs = red_src[w];
+            }
+        }
+        const uint32_t vk = static_cast<uint32_t>(gk >> 32);
+        const int idx = static_cast<int>(~static_cast<uint32_t>(gk) & kLargeIdxMask);
+        far = (vk == 0) ? 0 : idx;
+        if (tid == 0) {
+            if (vk == 0) {
+                centroid = make_float4(xyz[0], xyz[1], xyz[2], 0.f);
+            } else {
+                const uint64_t* q = base + 4 * gs;
+                const uint64_t w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                centroid = make_float4(i2f(static_cast<int>(w1 >> 32)), i2f(static_cast<int>(w2 >> 32)),
+                                       i2f(static_cast<int>(w3 >> 32)), 0.f);
+            }
+        }
+        __syncthreads();
+        cx = centroid.x;
+        cy = centroid.y;
+        cz = centroid.z;
+    }
+}
+
+// ------------------------------------------------------------ dispatch
+
+constexpr int kRegsThreads = 256;
+constexpr int kRegsMaxPoints = 32 * kRegsThreads;  // 8192 points, 128 KiB of LDS
+constexpr int kGlobalThreads = 1024;
+
+template <int P>
+hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
+                       const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
+                       int64_t npoint, int64_t start, int skip, hipStream_t stream) {
+    hipLaunchKernelGGL((fps_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                       start, skip);
+    return hipGetLastError();
+}
+
+hipError_t launch_fps(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
+                      const int64_t* starts, int64_t* out, float* scratch, int64_t blocks,
+                      int64_t max_len, int64_t N, int64_t npoint, int64_t start, int skip,
+                      hipStream_t stream) {
+    if (max_len <= 1 * kRegsThreads)
+        return launch_regs<1>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (max_len <= 2 * kRegsThreads)
+        return launch_regs<2>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (max_len <= 4 * kRegsThreads)
+        return launch_regs<4>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (max_len <= 8 * kRegsThreads)
+        return launch_regs<8>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (max_len <= 16 * kRegsThreads)
+        return launch_regs<16>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (max_len <= 32 * kRegsThreads)
+        return launch_regs<32>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
+    if (scratch == nullptr) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((fps_global_kernel<kGlobalThreads>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kGlobalThreads), 0, stream, xyz, ptr, out_ptr, starts, out, scratch,
+                       N, npoint, start, skip);
+    return hipGetLastError();
+}
+
+constexpr int kLargeThreads = 256;
+
+template <int P>
+hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint32_t* status,
+                        int N, int64_t npoint, int start, int skip, int chunk, int grid,
+                        hipStream_t stream) {
+    void* args[] = {(void*)&xyz, (void*)&out, (void*)&records, (void*)&status, (void*)&N,
+                    (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk};
+    return hipLaunchCooperativeKernel(
+        reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>), dim3(grid),
+        dim3(kLargeThreads), args, 0, stream);
+}
+
+template <int P>
+int large_capacity(int device) {
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>),
+            kLargeThreads, 0) != hipSuccess)
+        return 0;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        return 0;
+    return per_cu * cus;
+}
+
+}  // namespace
+}  // namespace pointops
+
+using namespace pointops;
+
+extern "C" {
+
+size_t pointops_fps_dense_scratch_bytes(int64_t B, int64_t N) {
+    if (B <= 0 || N <= kRegsMaxPoints) return 0;
+    return static_cast<size_t>(B) * static_cast<size_t>(N) * sizeof(float);
+}
+
+hipError_t pointops_fps_dense(const float* xyz, int64_t* out, void* scratch, int64_t B, int64_t N,
+                              int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
+                              hipStream_t stream) {
+    if (B < 0 || N < 0 || npoint < 0) return hipErrorInvalidValue;
+    if (B == 0 || npoint == 0) return hipSuccess;
+    if (N == 0 || start_idx < 0 || start_idx >= N || N > INT32_MAX - 1 || B > INT32_MAX)
+        return hipErrorInvalidValue;
+    if (xyz == nullptr || out == nullptr) return hipErrorInvalidValue;
+    return launch_fps(xyz, nullptr, nullptr, nullptr, out, static_cast<float*>(scratch), B, N, N,
+                      npoint, start_idx, skip_near_origin ? 1 : 0, stream);
+}
+
+size_t pointops_fps_flat_scratch_bytes(int64_t total_n, int64_t max_len) {
+    if (max_len <= kRegsMaxPoints || total_n <= 0) return 0;
+    return static_cast<size_t>(total_n) * sizeof(float);
+}
+
+hipError_t pointops_fps_flat(const float* x, const int64_t* ptr, const int64_t* out_ptr,
+                             const int64_t* starts, int64_t* out, void* scratch, int64_t batch,
+                             int64_t total_n, int64_t max_len, hipStream_t stream) {
+    if (batch < 0 || total_n < 0 || max_len < 0 || max_len > INT32_MAX - 1 || batch > INT32_MAX)
+        return hipErrorInvalidValue;
+    if (batch == 0) return hipSuccess;
+    if (ptr == nullptr || out_ptr == nullptr || starts == nullptr) return hipErrorInvalidValue;
+    return launch_fps(x, ptr, out_ptr, starts, out, static_cast<float*>(scratch), batch, max_len, 0,
+                      0, 0, 0, stream);
+}
+
+size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
+    (void)npoint;
+    if (N <= 0) return 0;
+    // status word (padded to 256 B) + 2 parities x grid x 4 words
+    const int64_t max_grid = 4096;
+    return 256 + static_cast<size_t>(2 * max_grid * 4) * sizeof(uint64_t);
+}
+
+hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,
+                              int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
+                              hipStream_t stream) {
+    if (N < 0 || npoint < 0) return hipErrorInvalidValue;
+    if (npoint == 0) return hipSuccess;
+    if (N == 0 || N > kLargeMaxN || start_idx < 0 || start_idx >= N) return hipErrorInvalidValue;
+    if (xyz == nullptr || out == nullptr || workspace == nullptr) return hipErrorInvalidValue;
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    // Choose points per thread so that the cloud fits the co-resident grid.
+    const int choices[] = {4, 8, 16, 32};
+    for (int P : choices) {
+        int cap = 0;
+        switch (P) {
+            case 4: cap = large_capacity<4>(device); break;
+            case 8: cap = large_capacity<8>(device); break;
+            case 16: cap = large_capacity<16>(device); break;
+            default: cap = large_capacity<32>(device); break;
+        }
+        cap = cap < 4096 ? cap : 4096;
+        const int64_t per_block = static_cast<int64_t>(P) * kLargeThreads;
+        const int64_t need = (N + per_block - 1) / per_block;
+        if (cap <= 0 || need > cap) continue;
+        const int grid = static_cast<int>(need);
+        const int chunk = static_cast<int>(per_block);
+        auto* status = static_cast<uint32_t*>(workspace);
+        auto* records = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + 256);
+        const int n32 = static_cast<int>(N);
+        const int s32 = static_cast<int>(start_idx);
+        const int skip = skip_near_origin ? 1 : 0;
+        switch (P) {
+            case 4: return launch_large<4>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
+            case 8: return launch_large<8>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
+            case 16: return launch_large<16>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
+            default: return launch_large<32>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
+        }
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // extern "C"

@@ -1,0 +1,305 @@
+// Exact k-nearest-neighbour search for gfx950.
+//
+// One wave per query.  Lane l scans reference j = 64*c + l of chunk c; the
+// current best K keys (squared distance, index) form a sorted list spread
+// over the wave: slot s lives in lane s % 64 of register s / 64 (K <= 256).
+// A reference is a candidate when its key is before the K-th entry; the wave
+// ballots the candidates and inserts them one by one (rank by ballot
+// popcount, shift by one lane with DPP wave_shr).  Keys order by distance then
+// index, so the result is independent of visit order; chunks are visited with
+// a stride coprime to the chunk count (as kernels/knn.metal:12-17 does) so
+// that spatially sorted clouds do not insert on every chunk.
+//
+// Variants (template DIM3 / FLAT):
+//   dense 3-D   kernels/knn.metal:32-140 semantics: NaN distances never match,
+//               unfilled slots are (inf, 2^32-1);
+//   dense D-dim kernels/feature_knn.metal:51-164: non-finite queries and
+//               distances never match, unfilled slots (inf, -1);
+//   flat        kernels/flat_search.metal:140-250 and feature_knn.metal:166-199:
+//               segment by binary search on ptr_y, global indices, -1 padding.
+#include "pointops_common.hpp"
+#include "pointops_hip.h"
+
+namespace pointops {
+namespace {
+
+constexpr int kKnnThreads = 256;
+constexpr int kKnnWaves = kKnnThreads / kWave;
+constexpr int kMaxK = 256;
+
+// Sequential squared L2 in D dimensions: s = d0^2; s = s + dt^2 (dt = r - q).
+__device__ __forceinline__ float sqdist_nd(const float* __restrict__ r, const float* __restrict__ q,
+                                           int D) {
+    const float first = r[0] - q[0];
+    float s = first * first;
+    for (int t = 1; t < D; ++t) {
+        const float delta = r[t] - q[t];
+        const float term = delta * delta;
+        s = s + term;
+    }
+    return s;
+}
+
+__device__ __forceinline__ int64_t segment_of(const int64_t* __restrict__ ptr, int64_t batch,
+                                              int64_t q) {
+    int64_t lo = 0, hi = batch;
+    while (lo < hi) {
+        const int64_t mid = lo + (hi - lo) / 2;
+        if (ptr[mid + 1] <= q) lo = mid + 1;
+        else hi = mid;
+    }
+    return lo;
+}
+
+__device__ __forceinline__ uint32_t gcd_u32(uint32_t a, uint32_t b) {
+    while (b != 0) {
+        const uint32_t t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
+
+// Chunk stride ~ golden ratio * chunks, bumped until coprime to chunks.
+__device__ __forceinline__ uint32_t visit_stride(uint32_t chunks) {
+    if (chunks <= 2) return 1;
+    uint32_t s = static_cast<uint32_t>(static_cast<double>(chunks) * 0.6180339887498949 + 0.5) % chunks;
+    if (s == 0) s = 1;
+    while (gcd_u32(s, chunks) != 1) {
+        s = (s + 1) % chunks;
+        if (s == 0) s = 1;
+    }
+    return s;
+}
+
+// Insert candidate (cd, ci) into the wave-distributed sorted list.
+template <int SLOTS>
+__device__ __forceinline__ void list_insert(float (&ld)[SLOTS], int (&li)[SLOTS], int K, int lane,
+                                            float cd, int ci) {
+    int pos = 0;
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        const int s = r * kWave + lane;
+        pos += __popcll(ballot(s < K && before(ld[r], li[r], cd, ci)));
+    }
+    int carry_d = 0, carry_i = 0;
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        const int s = r * kWave + lane;
+        // Lane 63 of the previous register moves to lane 0 of this one.
+        const int next_carry_d = readlane(f2i(ld[r]), kWave - 1);
+        const int next_carry_i = readlane(li[r], kWave - 1);
+        const float shifted_d = i2f(wave_shr1(f2i(ld[r]), carry_d));
+        const int shifted_i = wave_shr1(li[r], carry_i);
+        if (s > pos) {
+            ld[r] = shifted_d;
+            li[r] = shifted_i;
+        } else if (s == pos) {
+            ld[r] = cd;
+            li[r] = ci;
+        }
+        carry_d = next_carry_d;
+        carry_i = next_carry_i;
+    }
+}
+
+template <int SLOTS>
+__device__ __forceinline__ void list_tail(const float (&ld)[SLOTS], const int (&li)[SLOTS], int K,
+                                          float& td, int& ti) {
+    const int r_last = (K - 1) / kWave;
+    const int l_last = (K - 1) % kWave;
+    int d = 0, i = 0;
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        if (r == r_last) {
+            d = readlane(f2i(ld[r]), l_last);
+            i = readlane(li[r], l_last);
+        }
+    }
+    td = i2f(d);
+    ti = i;
+}
+
+// One wave: scan n references and keep the K best keys.
+template <int SLOTS, bool DIM3, bool FINITE_ONLY>
+__device__ __forceinline__ void scan_refs(const float* __restrict__ qp, const float* __restrict__ rp,
+                                          int n, int D, int K, int lane, float (&ld)[SLOTS],
+                                          int (&li)[SLOTS]) {
+    float td = INFINITY;
+    int ti = -1;  // 0xFFFFFFFF: every real index is before it
+    const uint32_t chunks = (static_cast<uint32_t>(n) + kWave - 1) / kWave;
+    if (chunks == 0) return;
+    float qx = 0.f, qy = 0.f, qz = 0.f;
+    if (DIM3) {
+        qx = qp[0];
+        qy = qp[1];
+        qz = qp[2];
+    }
+    const uint32_t stride = visit_stride(chunks);
+    uint32_t chunk = 0;
+    for (uint32_t c = 0; c < chunks; ++c) {
+        const int j = static_cast<int>(chunk * kWave) + lane;
+        chunk += stride;
+        if (chunk >= chunks) chunk -= chunks;
+        float d = INFINITY;
+        bool valid = j < n;
+        if (valid) {
+            if (DIM3) {
+                const float* r = rp + 3 * static_cast<int64_t>(j);
+                d = sqdist3(r[0], r[1], r[2], qx, qy, qz);
+            } else {
+                d = sqdist_nd(rp + static_cast<int64_t>(j) * D, qp, D);
+            }
+            if (FINITE_ONLY) valid = isfinite(d);
+        }
+        uint64_t pending = ballot(valid && before(d, j, td, ti));
+        while (pending != 0) {
+            const int src = __builtin_ctzll(pending);
+            pending &= pending - 1;
+            const float cd = i2f(readlane(f2i(d), src));
+            const int ci = readlane(j, src);
+            if (!before(cd, ci, td, ti)) continue;  // an earlier insert raised the bar
+            list_insert<SLOTS>(ld, li, K, lane, cd, ci);
+            list_tail<SLOTS>(ld, li, K, td, ti);
+        }
+    }
+}
+
+template <int SLOTS, bool DIM3>
+__global__ __launch_bounds__(kKnnThreads) void knn_dense_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
+    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int D, int K) {
+    const int lane = lane_id();
+    const int64_t row = static_cast<int64_t>(blockIdx.x) * kKnnWaves + uniform(threadIdx.x / kWave);
+    if (row >= B * M) return;  // whole wave leaves; only wave-level sync below
+    const int64_t b = row / M;
+    const float* qp = query + row * D;
+    const float* rp = ref + b * N * D;
+    float ld[SLOTS];
+    int li[SLOTS];
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        ld[r] = INFINITY;
+        li[r] = -1;
+    }
+    bool query_ok = true;
+    if (!DIM3) {
+        for (int t = 0; t < D; ++t) query_ok = query_ok && isfinite(qp[t]);
+    }
+    if (query_ok) scan_refs<SLOTS, DIM3, !DIM3>(qp, rp, static_cast<int>(N), D, K, lane, ld, li);
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        const int s = r * kWave + lane;
+        if (s < K) {
+            out_dist[row * K + s] = sqrtf(ld[r]);
+            // 3-D keeps the reference kernel's (inf, UINT_MAX) padding.
+            out_idx[row * K + s] = DIM3 ? static_cast<int64_t>(static_cast<uint32_t>(li[r]))
+                                        : (li[r] < 0 ? int64_t(-1) : int64_t(li[r]));
+        }
+    }
+}
+
+template <int SLOTS, bool DIM3>
+__global__ __launch_bounds__(kKnnThreads) void knn_flat_kernel(
+    const float* __restrict__ y, const float* __restrict__ x, const int64_t* __restrict__ ptr_y,
+    const int64_t* __restrict__ ptr_x, int64_t* __restrict__ out, int64_t Q, int64_t batch, int D,
+    int K) {
+    const int lane = lane_id();
+    const int64_t q = static_cast<int64_t>(blockIdx.x) * kKnnWaves + uniform(threadIdx.x / kWave);
+    if (q >= Q) return;
+    const int64_t b = segment_of(ptr_y, batch, q);
+    const int64_t lo = ptr_x[b];
+    const int n = static_cast<int>(ptr_x[b + 1] - lo);
+    const float* qp = y + q * D;
+    float ld[SLOTS];
+    int li[SLOTS];
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        ld[r] = INFINITY;
+        li[r] = -1;
+    }
+    bool query_ok = true;
+    for (int t = 0; t < D; ++t) query_ok = query_ok && isfinite(qp[t]);
+    if (query_ok) scan_refs<SLOTS, DIM3, true>(qp, x + lo * D, n, D, K, lane, ld, li);
+#pragma unroll
+    for (int r = 0; r < SLOTS; ++r) {
+        const int s = r * kWave + lane;
+        if (s < K) out[q * K + s] = li[r] < 0 ? int64_t(-1) : lo + li[r];
+    }
+}
+
+template <bool DIM3>
+hipError_t launch_dense(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
+                        int64_t M, int64_t N, int D, int K, hipStream_t stream) {
+    const int64_t rows = B * M;
+    const dim3 grid(static_cast<uint32_t>((rows + kKnnWaves - 1) / kKnnWaves));
+    const dim3 block(kKnnThreads);
+    if (K <= 64)
+        hipLaunchKernelGGL((knn_dense_kernel<1, DIM3>), grid, block, 0, stream, query, ref, dist, idx,
+                           B, M, N, D, K);
+    else if (K <= 128)
+        hipLaunchKernelGGL((knn_dense_kernel<2, DIM3>), grid, block, 0, stream, query, ref, dist, idx,
+                           B, M, N, D, K);
+    else
+        hipLaunchKernelGGL((knn_dense_kernel<4, DIM3>), grid, block, 0, stream, query, ref, dist, idx,
+                           B, M, N, D, K);
+    return hipGetLastError();
+}
+
+template <bool DIM3>
+hipError_t launch_flat(const float* y, const float* x, const int64_t* ptr_y, const int64_t* ptr_x,
+                       int64_t* out, int64_t Q, int64_t batch, int D, int K, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>((Q + kKnnWaves - 1) / kKnnWaves));
+    const dim3 block(kKnnThreads);
+    if (K <= 64)
+        hipLaunchKernelGGL((knn_flat_kernel<1, DIM3>), grid, block, 0, stream, y, x, ptr_y, ptr_x, out,
+                           Q, batch, D, K);
+    else if (K <= 128)
+        hipLaunchKernelGGL((knn_flat_kernel<2, DIM3>), grid, block, 0, stream, y, x, ptr_y, ptr_x, out,
+                           Q, batch, D, K);
+    else
+        hipLaunchKernelGGL((knn_flat_kernel<4, DIM3>), grid, block, 0, stream, y, x, ptr_y, ptr_x, out,
+                           Q, batch, D, K);
+    return hipGetLastError();
+}
+
+bool grid_ok(int64_t rows) { return (rows + kKnnWaves - 1) / kKnnWaves <= INT32_MAX; }
+
+}  // namespace
+}  // namespace pointops
+
+using namespace pointops;
+
+extern "C" {
+
+hipError_t pointops_knn3(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
+                         int64_t M, int64_t N, int64_t K, hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0 || K < 0 || K > kMaxK || K > N) return hipErrorInvalidValue;
+    if (B == 0 || M == 0 || K == 0) return hipSuccess;
+    if (N > INT32_MAX - kWave || !grid_ok(B * M)) return hipErrorInvalidValue;
+    return launch_dense<true>(query, ref, dist, idx, B, M, N, 3, static_cast<int>(K), stream);
+}
+
+hipError_t pointops_knn_feat(const float* query, const float* ref, float* dist, int64_t* idx,
+                             int64_t B, int64_t M, int64_t N, int64_t D, int64_t K,
+                             hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0 || D < 1 || K < 0 || K > kMaxK || K > N) return hipErrorInvalidValue;
+    if (B == 0 || M == 0 || K == 0) return hipSuccess;
+    if (N > INT32_MAX - kWave || D > INT32_MAX || !grid_ok(B * M)) return hipErrorInvalidValue;
+    return launch_dense<false>(query, ref, dist, idx, B, M, N, static_cast<int>(D),
+                               static_cast<int>(K), stream);
+}
+
+hipError_t pointops_knn_flat(const float* y, const float* x, const int64_t* ptr_y,
+                             const int64_t* ptr_x, int64_t* out, int64_t Q, int64_t batch,
+                             int64_t D, int64_t K, hipStream_t stream) {
+    if (Q < 0 || batch < 0 || D < 1 || K < 0 || K > kMaxK) return hipErrorInvalidValue;
+    if (Q == 0 || K == 0) return hipSuccess;
+    if (batch == 0 || D > INT32_MAX || !grid_ok(Q)) return hipErrorInvalidValue;
+    if (D == 3)
+        return launch_flat<true>(y, x, ptr_y, ptr_x, out, Q, batch, 3, static_cast<int>(K), stream);
+    return launch_flat<false>(y, x, ptr_y, ptr_x, out, Q, batch, static_cast<int>(D),
+                              static_cast<int>(K), stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,112 @@
+// Shared device helpers for the gfx950 neighbourhood-search kernels.
+//
+// Every kernel is compiled with -ffp-contract=off and without fast-math, so
+// each float expression below is one IEEE binary32 operation rounded to
+// nearest-even in the written order; denormals are preserved (no FTZ).  The
+// squared distance is therefore bit-identical to the reference's separately
+// rounded tensor ops ((dx*dx + dy*dy) + dz*dz), reference.py:34-37.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pointops {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float sqdist3(float ax, float ay, float az, float bx, float by,
+                                         float bz) {
+    const float dx = ax - bx;
+    const float dy = ay - by;
+    const float dz = az - bz;
+    float d = dx * dx;
+    d = d + dy * dy;
+    d = d + dz * dz;
+    return d;
+}
+
+__device__ __forceinline__ int f2i(float v) { return __float_as_int(v); }
+__device__ __forceinline__ float i2f(int v) { return __int_as_float(v); }
+
+// ---------------------------------------------------------------- DPP / SALU
+// GFX9 DPP controls (row = 16 lanes).
+constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
+constexpr int kDppQuadXor2 = 0x4E;      // quad_perm [2,3,0,1]
+constexpr int kDppRowHalfMirror = 0x141;
+constexpr int kDppRowMirror = 0x140;
+constexpr int kDppWaveShr1 = 0x138;     // lane l <- lane l-1; lane 0 keeps `old`
+
+template <int CTRL>
+__device__ __forceinline__ int dpp(int v) {
+    return __builtin_amdgcn_update_dpp(v, v, CTRL, 0xF, 0xF, false);
+}
+
+// Shift the wave right by one lane: lane l gets v[l-1], lane 0 gets `fill`.
+__device__ __forceinline__ int wave_shr1(int v, int fill) {
+    return __builtin_amdgcn_update_dpp(fill, v, kDppWaveShr1, 0xF, 0xF, false);
+}
+
+__device__ __forceinline__ int readlane(int v, int lane) {
+    return __builtin_amdgcn_readlane(v, lane);
+}
+
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+__device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
+
+// Lanes strictly below this lane whose bit is set in `mask`.
+__device__ __forceinline__ int lanes_below(uint64_t mask) {
+    return __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                     __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+}
+
+__device__ __forceinline__ int lane_id() { return __lane_id(); }
+
+// Maximum over the wave of a float with no NaN; every lane gets the result.
+__device__ __forceinline__ float wave_max(float v) {
+    v = fmaxf(v, i2f(dpp<kDppQuadXor1>(f2i(v))));
+    v = fmaxf(v, i2f(dpp<kDppQuadXor2>(f2i(v))));
+    v = fmaxf(v, i2f(dpp<kDppRowHalfMirror>(f2i(v))));
+    v = fmaxf(v, i2f(dpp<kDppRowMirror>(f2i(v))));
+    const float a = i2f(readlane(f2i(v), 0));
+    const float b = i2f(readlane(f2i(v), 16));
+    const float c = i2f(readlane(f2i(v), 32));
+    const float d = i2f(readlane(f2i(v), 48));
+    return fmaxf(fmaxf(a, b), fmaxf(c, d));
+}
+
+// Minimum over the wave of a signed int; every lane gets the result.
+__device__ __forceinline__ int wave_min(int v) {
+    v = min(v, dpp<kDppQuadXor1>(v));
+    v = min(v, dpp<kDppQuadXor2>(v));
+    v = min(v, dpp<kDppRowHalfMirror>(v));
+    v = min(v, dpp<kDppRowMirror>(v));
+    const int a = readlane(v, 0);
+    const int b = readlane(v, 16);
+    const int c = readlane(v, 32);
+    const int d = readlane(v, 48);
+    return min(min(a, b), min(c, d));
+}
+
+// (d, i) strictly before (e, j): smaller distance, then smaller index
+// (the reference's kNN ordering, kernels/knn.metal:27-30).  NaN is never
+// before anything.
+__device__ __forceinline__ bool before(float d, int i, float e, int j) {
+    return d < e || (d == e && static_cast<uint32_t>(i) < static_cast<uint32_t>(j));
+}
+
+// Map 32-bit block ids so that consecutive logical ids share an XCD: the
+// hardware deals workgroups round-robin over the 8 XCDs, and neighbouring
+// logical blocks touch the same cloud, so keeping them on one XCD keeps the
+// cloud in that XCD's L2.
+__device__ __forceinline__ uint32_t xcd_local_block(uint32_t hw, uint32_t nblocks) {
+    constexpr uint32_t kXcds = 8;
+    if (nblocks % kXcds != 0) return hw;
+    const uint32_t per = nblocks / kXcds;
+    return (hw % kXcds) * per + hw / kXcds;
+}
+
+}  // namespace pointops
+
+// Host-side launch helper: checks the launch and returns its status.
+#define POINTOPS_LAUNCH_STATUS() (hipGetLastError())

@@ -1,0 +1,150 @@
+"""Dense FPS, kNN and ball query on ROCm (signatures of
+/root/reference/mps_pointops/ops.py).
+
+Tensors must live on a ROCm device (``device='cuda'``); every call enqueues a
+hand-written gfx950 kernel through libpointops_hip.so on the current stream.
+Validation order, error types and messages follow the reference.
+"""
+
+from __future__ import annotations
+
+from typing import Literal
+
+import torch
+from torch import Tensor
+
+from . import _native
+from ._ball_query import _checked_radius_and_k, ball_query as _native_ball_query
+
+# Largest cloud the single-launch large-cloud FPS path addresses (21-bit index
+# in its per-step records).
+_FPS_LARGE_MAX_N = 1 << 21
+# One cloud with at least this many points uses the all-CU persistent kernel
+# under strategy="auto"; smaller clouds fit one workgroup's registers and LDS.
+_FPS_MULTIGROUP_MIN_N = 65_536
+# Same limit as the reference kernel (ops.py:30).
+_KNN_MAX_K = 256
+
+
+def furthest_point_sample(
+    xyz: Tensor,
+    npoint: int,
+    start_idx: int = 0,
+    skip_near_origin: bool = False,
+    *,
+    strategy: Literal["auto", "single", "multigroup"] = "auto",
+) -> Tensor:
+    """Farthest point sampling (ops.py:53-141).
+
+    Sampling starts at ``start_idx``; ties go to the smaller index; once every
+    point has been sampled, the remaining slots repeat index 0.  With
+    ``skip_near_origin`` points with x^2 + y^2 + z^2 <= 1e-3 are never picked
+    (only the start index can be one).
+
+    ``strategy``: ``single`` runs one workgroup per cloud; ``multigroup`` runs
+    one persistent launch over every CU for a single cloud (B must be 1);
+    ``auto`` picks ``multigroup`` for one cloud of at least 65,536 points.
+
+    Returns:
+        (B, npoint) int64 indices into ``xyz``.
+    """
+    if xyz.dim() != 3 or xyz.shape[-1] != 3:
+        raise ValueError(f"xyz must have shape (B, N, 3), got {tuple(xyz.shape)}")
+    if strategy not in ("auto", "single", "multigroup"):
+        raise ValueError(f"strategy must be auto, single, or multigroup, got {strategy!r}")
+    B, N, _ = xyz.shape
+    if npoint < 0:
+        raise ValueError(f"npoint must be >= 0, got {npoint}")
+    if npoint > 0 and N == 0:
+        raise ValueError("cannot sample from an empty point cloud")
+    if npoint > 0 and not 0 <= start_idx < N:
+        raise IndexError(f"start_idx {start_idx} is out of range for {N} points")
+    _native.require_device(xyz.device)
+    if xyz.dtype != torch.float32:
+        raise TypeError(f"xyz must be float32 on ROCm, got {xyz.dtype}")
+    if strategy == "multigroup" and B > 1 and npoint > 1:
+        raise ValueError("multigroup FPS requires batch size 1; use auto or single for batches")
+    use_large = B == 1 and npoint > 1 and (
+        strategy == "multigroup" or (strategy == "auto" and N >= _FPS_MULTIGROUP_MIN_N)
+    )
+    if use_large and N > _FPS_LARGE_MAX_N:
+        if strategy == "multigroup":
+            raise ValueError(f"multigroup FPS requires at most {_FPS_LARGE_MAX_N} points")
+        use_large = False
+    out = torch.empty((B, npoint), dtype=torch.long, device=xyz.device)
+    if B == 0 or npoint == 0:
+        return out
+    xyz = xyz.contiguous()
+    stream = _native.stream(xyz.device)
+    if use_large:
+        size = _native.size_query("pointops_fps_large_workspace_bytes", N, npoint)
+        workspace = torch.zeros(size, dtype=torch.uint8, device=xyz.device)
+        _native.call("pointops_fps_large", xyz.data_ptr(), out.data_ptr(), workspace.data_ptr(),
+                     N, npoint, start_idx, int(skip_near_origin), stream)
+        return out
+    size = _native.size_query("pointops_fps_dense_scratch_bytes", B, N)
+    scratch = torch.empty(size, dtype=torch.uint8, device=xyz.device) if size else None
+    _native.call("pointops_fps_dense", xyz.data_ptr(), out.data_ptr(), _native.ptr(scratch),
+                 B, N, npoint, start_idx, int(skip_near_origin), stream)
+    return out
+
+
+def knn(query: Tensor, ref: Tensor, k: int) -> tuple[Tensor, Tensor]:
+    """Exact brute-force k nearest neighbours (ops.py:144-205).
+
+    Neighbours are sorted by float32 squared distance, then by index.  D = 3
+    uses the coordinate kernel; other D accumulate dimensions in order.
+    ``k`` can be at most 256.  Selection has no coordinate gradients.
+
+    Returns:
+        dist: (B, M, k) Euclidean distances, ascending.
+        idx: (B, M, k) int64 indices into ``ref``.
+    """
+    if query.dim() != 3 or query.shape[-1] < 1:
+        raise ValueError(f"query must have shape (B, M, D) with D >= 1, got {tuple(query.shape)}")
+    if ref.dim() != 3 or ref.shape[-1] != query.shape[-1]:
+        raise ValueError(f"ref must have shape (B, N, {query.shape[-1]}), got {tuple(ref.shape)}")
+    if query.device != ref.device:
+        raise ValueError(f"query and ref are on different devices: {query.device} and {ref.device}")
+    if query.shape[0] != ref.shape[0]:
+        raise ValueError(f"batch sizes differ: {query.shape[0]} and {ref.shape[0]}")
+    B, M, D = query.shape
+    N = ref.shape[1]
+    if not 0 <= k <= N:
+        raise ValueError(f"k must be in [0, {N}], got {k}")
+    _native.require_device(query.device)
+    if query.dtype != torch.float32 or ref.dtype != torch.float32:
+        raise TypeError(f"query and ref must be float32 on ROCm, got {query.dtype} and {ref.dtype}")
+    if k > _KNN_MAX_K:
+        raise ValueError(f"k must be at most {_KNN_MAX_K} on ROCm, got {k}")
+    if M >= 2**31 or N >= 2**31 - 64 or D >= 2**31:
+        raise ValueError("M, N, and D must each be below 2**31 for the native kNN kernel")
+    dist = torch.empty(B, M, k, dtype=torch.float32, device=query.device)
+    idx = torch.empty(B, M, k, dtype=torch.long, device=query.device)
+    if B == 0 or M == 0 or k == 0:
+        return dist, idx
+    query, ref = query.contiguous(), ref.contiguous()
+    stream = _native.stream(query.device)
+    if D == 3:
+        _native.call("pointops_knn3", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
+                     idx.data_ptr(), B, M, N, k, stream)
+    else:
+        _native.call("pointops_knn_feat", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
+                     idx.data_ptr(), B, M, N, D, k, stream)
+    return dist, idx
+
+
+def ball_query(query: Tensor, ref: Tensor, radius: float, K: int) -> tuple[Tensor, Tensor]:
+    """First-K radius search with squared distances and -1 padded indices
+    (ops.py:208-227).  Shapes (B, M, 3), (B, N, 3) -> (B, M, K); float32 or
+    float16 inputs; coordinate gradients flow through the squared distances.
+    """
+    _checked_radius_and_k(radius, K)
+    if query.dim() != 3 or ref.dim() != 3 or query.shape[-1] != 3 or ref.shape[-1] != 3:
+        raise ValueError("query and ref must have shapes (B, M, 3) and (B, N, 3)")
+    if query.shape[0] != ref.shape[0]:
+        raise ValueError("query and ref must have the same batch size")
+    if query.device != ref.device:
+        raise ValueError(f"query and ref are on different devices: {query.device} and {ref.device}")
+    result = _native_ball_query(query, ref, radius=radius, k=K)
+    return result.distances, result.indices

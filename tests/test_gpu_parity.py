@@ -1,0 +1,555 @@
+"""GPU parity: the native kernels against the oracle and the golden vectors.
+
+Integer outputs (indices) must be bit-identical; float outputs computed by
+the same operation sequence (squared distances, sqrt, interpolation) are
+compared bit for bit as well; atomics-accumulated gradients are compared with
+a tolerance (rtol 1e-5 / atol 1e-6, stated per test).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import bench
+from conftest import GOLDEN, load_known_answers, load_pointnet2_parity
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def cuda(x, dtype=torch.float32):
+    return torch.as_tensor(np.asarray(x), dtype=dtype).cuda()
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().cpu().numpy()
+
+
+def same_bits(a, b):
+    a = np.ascontiguousarray(np.asarray(a, np.float32))
+    b = np.ascontiguousarray(np.asarray(b, np.float32))
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
+# ------------------------------------------------------------ known answers
+
+@pytest.mark.parametrize("case", load_known_answers("fps"), ids=lambda c: c["name"])
+def test_fps_known_answers(cuda_device, case):
+    import mps_pointops as mp
+    from mps_pointops import compat
+
+    xyz = cuda(case["xyz"])
+    if case["skip"]:
+        got = compat.furthest_point_sample(xyz, case["npoint"])
+        assert got.dtype == torch.int32
+    else:
+        got = mp.furthest_point_sample(xyz, case["npoint"], case["start_idx"])
+        assert got.dtype == torch.long
+    assert got.cpu().tolist() == case["expect"], case["source"]
+    if case["npoint"] > 1:
+        large = mp.furthest_point_sample(xyz, case["npoint"], case["start_idx"], case["skip"],
+                                         strategy="multigroup")
+        assert large.cpu().tolist() == case["expect"]
+
+
+@pytest.mark.parametrize("case", load_known_answers("fps_flat"), ids=lambda c: c["name"])
+def test_fps_flat_known_answers(cuda_device, case):
+    from mps_pointops import flat
+
+    x = cuda(case["x"])
+    # Both transcribed cases use ratio 0.5 (tests/test_flat.py:20-29).
+    got = flat.fps(x, ptr=case["ptr"], ratio=0.5, random_start=False)
+    assert got.cpu().tolist() == case["expect"], case["source"]
+
+
+@pytest.mark.parametrize("case", load_known_answers("knn"), ids=lambda c: c["name"])
+def test_knn_known_answers(cuda_device, case):
+    import mps_pointops as mp
+
+    d, i = mp.knn(cuda(case["query"]), cuda(case["ref"]), case["k"])
+    assert i.cpu().tolist() == case["expect_idx"], case["source"]
+    np.testing.assert_allclose(host(d), np.array(case["expect_dist"], np.float32), rtol=1e-6)
+
+
+def _batch(v):
+    return None if v is None else torch.tensor(v, dtype=torch.long).cuda()
+
+
+@pytest.mark.parametrize("case", load_known_answers("knn_flat"), ids=lambda c: c["name"])
+def test_knn_flat_known_answers(cuda_device, case):
+    from mps_pointops import flat
+
+    got = flat.knn(cuda(case["x"]), cuda(case["y"]), case["k"], _batch(case["batch_x"]),
+                   _batch(case["batch_y"]))
+    assert got.cpu().tolist() == case["expect"], case["source"]
+
+
+@pytest.mark.parametrize("case", load_known_answers("radius_flat"), ids=lambda c: c["name"])
+def test_radius_flat_known_answers(cuda_device, case):
+    from mps_pointops import flat
+
+    got = flat.radius(cuda(case["x"]), cuda(case["y"]), case["r"], _batch(case["batch_x"]),
+                      _batch(case["batch_y"]), max_num_neighbors=case["k"])
+    assert got.cpu().tolist() == case["expect"], case["source"]
+
+
+@pytest.mark.parametrize("case", load_known_answers("ball_query"), ids=lambda c: c["name"])
+def test_ball_query_known_answers(cuda_device, case):
+    import mps_pointops as mp
+    from mps_pointops import compat
+
+    q = cuda(case["query"]).requires_grad_(case.get("expect_grad_p") is not None)
+    p = cuda(case["ref"]).requires_grad_(case.get("expect_grad_p") is not None)
+    dist, idx = mp.ball_query(q, p, case["radius"], case["k"])
+    assert idx.cpu().tolist() == case["expect_idx"], case["source"]
+    if case.get("expect_dist") is not None:
+        np.testing.assert_allclose(host(dist), np.array(case["expect_dist"], np.float32),
+                                   rtol=1e-6, atol=0)
+    if case.get("expect_dist_bits") is not None:
+        assert host(dist).view(np.uint32).tolist() == case["expect_dist_bits"]
+    if case.get("compat") is not None:
+        got = compat.ball_query(case["radius"], case["k"], p.detach(), q.detach())
+        assert got.dtype == torch.int32 and got.cpu().tolist() == case["compat"]
+    if case.get("expect_grad_p") is not None:
+        g = case.get("grad_out")
+        grad = torch.ones_like(dist) if g is None else cuda(g)
+        dist.backward(grad)
+        want_p = np.array(case["expect_grad_p"], np.float32).reshape(host(p.grad).shape)
+        np.testing.assert_allclose(host(p.grad), want_p, rtol=1e-6, atol=1e-7)
+        if case.get("expect_grad_q") is not None:
+            np.testing.assert_allclose(host(q.grad), np.array(case["expect_grad_q"], np.float32),
+                                       rtol=1e-6, atol=1e-7)
+        if case.get("expect_grad_q_row0") is not None:
+            np.testing.assert_allclose(host(q.grad)[0, 0], case["expect_grad_q_row0"], rtol=1e-6)
+            assert np.all(host(q.grad)[0, 1:] == 0)
+
+
+@pytest.mark.parametrize("case", load_known_answers("three_nn"), ids=lambda c: c["name"])
+def test_three_nn_known_answers(cuda_device, case):
+    from mps_pointops import three_nn
+
+    d, i = three_nn(cuda(case["unknown"]), cuda(case["known"]))
+    assert i.dtype == torch.int32 and i.cpu().tolist() == case["expect_idx"]
+    np.testing.assert_allclose(host(d), np.array(case["expect_dist"], np.float32), rtol=1e-6)
+
+
+@pytest.mark.parametrize("case", load_known_answers("three_interpolate"), ids=lambda c: c["name"])
+def test_three_interpolate_known_answers(cuda_device, case):
+    from mps_pointops import three_interpolate
+
+    f = cuda(case["features"]).requires_grad_()
+    w = cuda(case["weights"]).requires_grad_()
+    out = three_interpolate(f, torch.tensor(case["indices"], dtype=torch.int32).cuda(), w)
+    assert out.cpu().tolist() == case["expect"]
+    out.backward(cuda(case["grad_out"]))
+    assert f.grad.cpu().tolist() == case["expect_grad"]
+    assert w.grad is not None and torch.count_nonzero(w.grad).item() == 0
+
+
+@pytest.mark.parametrize("case", load_known_answers("chamfer_nearest"), ids=lambda c: c["name"])
+def test_chamfer_nearest_known_answers(cuda_device, case):
+    from mps_pointops import chamfer
+
+    q, r = cuda(case["query"]), cuda(case["ref"])
+    B = q.shape[0]
+    ql = _batch(case.get("query_lengths") or [q.shape[1]] * B)
+    rl = _batch(case.get("ref_lengths") or [r.shape[1]] * B)
+    dist, idx = chamfer._nearest_mps(q, r, ql, rl, norm=case["norm"])
+    assert idx.cpu().tolist() == case["expect_idx"], case["source"]
+    np.testing.assert_array_equal(host(dist), np.array(case["expect_dist"], np.float32))
+
+
+# ----------------------------------------- reference-recorded selections
+
+def test_segmentation_selections_match_metal_recording(cuda_device):
+    """The compat path on the GPU reproduces all 12 index arrays recorded on
+    the reference's Metal kernels (docs/parity/pointnet2-segmentation-mps-safe.npz)."""
+    from mps_pointops import compat
+    from mps_pointops.pointnet2 import three_nn
+
+    z = np.load(GOLDEN / "segmentation_selections.npz")
+    xyz = [cuda(z["xyz"])]
+    got = []
+    for npoint, radius in ((1024, 0.1), (256, 0.2), (64, 0.4), (16, 0.8)):
+        x = xyz[-1]
+        idx = compat.furthest_point_sample(x, npoint)
+        new = compat.gather_operation(x.transpose(1, 2).contiguous(), idx).transpose(1, 2)
+        new = new.contiguous()
+        got += [idx, compat.ball_query(radius, 32, x, new)]
+        xyz.append(new)
+    for i in range(4):
+        got.append(three_nn(xyz[3 - i], xyz[4 - i])[1])
+    names = sorted(k for k in z.files if k.startswith("mps::"))
+    for name, arr in zip(names, got):
+        np.testing.assert_array_equal(host(arr), z[name], err_msg=name)
+
+
+def test_pointnet2_parity_fixtures(cuda_device):
+    from mps_pointops import three_interpolate, three_nn
+
+    for name, case in load_pointnet2_parity()["cases"].items():
+        inp = case["inputs"]
+        dist, idx = three_nn(cuda(inp["unknown"]), cuda(inp["known"]))
+        want = case["mps_safe"]
+        assert idx.cpu().tolist() == want["nearest_indices"], name
+        assert idx.cpu().tolist() == case["cuda"]["nearest_indices"], name
+        np.testing.assert_allclose(host(dist), np.array(want["distances"], np.float32), rtol=1e-6)
+        interp = idx.clone()
+        for b, row in inp["override"].items():
+            interp[int(b), 0] = torch.tensor(row, dtype=torch.int32)
+        f = cuda(inp["features"]).requires_grad_()
+        w = cuda(inp["weights"]).requires_grad_()
+        out = three_interpolate(f, interp, w)
+        np.testing.assert_array_equal(host(out), np.array(want["interpolated"], np.float32))
+        out.backward(cuda(inp["gradient"]))
+        np.testing.assert_allclose(host(f.grad), np.array(want["feature_gradient"], np.float32),
+                                   rtol=1e-6, atol=1e-6)
+        assert torch.count_nonzero(w.grad).item() == 0
+
+
+# ------------------------------------------------------- oracle parity
+
+def rand_cloud(b, n, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(b, n, 3, generator=g) * scale).float()
+
+
+@pytest.mark.parametrize("n", [1, 2, 31, 32, 33, 63, 64, 65, 255, 256, 257, 1023, 1024, 1025,
+                               4095, 4096, 4097, 8192, 8193, 20000])
+def test_fps_matches_oracle_edge_sizes(cuda_device, n):
+    import mps_pointops as mp
+
+    xyz = rand_cloud(2, n, n)
+    npoint = min(n + 3, 300)
+    start = n // 3
+    want = O.fps(xyz, npoint, start)
+    got = mp.furthest_point_sample(xyz.cuda(), npoint, start, strategy="single")
+    np.testing.assert_array_equal(host(got), want)
+
+
+@pytest.mark.parametrize("n", [1, 33, 1025, 4097, 65537, 100_000, 300_000])
+def test_fps_large_matches_oracle(cuda_device, n):
+    import mps_pointops as mp
+
+    xyz = rand_cloud(1, n, 27 + n)
+    xyz[0, : n // 7] = xyz[0, n // 7: 2 * (n // 7)]  # duplicates -> ties
+    npoint = min(n + 2, 200)
+    start = n // 2
+    for skip in (False, True):
+        want = O.fps(xyz, npoint, start, skip)
+        got = mp.furthest_point_sample(xyz.cuda(), npoint, start, skip, strategy="multigroup")
+        np.testing.assert_array_equal(host(got), want)
+
+
+def test_fps_skip_near_origin_boundary(cuda_device):
+    """tests/test_compat.py:96-111: points just inside the 1e-3 radius are
+    never picked, the one just outside is."""
+    from mps_pointops import compat
+
+    xyz = rand_cloud(1, 2000, 0)
+    inside = np.float32(np.sqrt(np.float32(1e-3))) * np.float32(0.999)
+    outside = np.float32(np.sqrt(np.float32(1e-3))) * np.float32(1.001)
+    g = torch.Generator().manual_seed(1)
+    xyz[0, 1:40] = torch.tensor([float(inside), 0.0, 0.0]) * torch.rand(39, 1, generator=g)
+    xyz[0, 40] = torch.tensor([float(inside), 0.0, 0.0])
+    xyz[0, 41] = torch.tensor([float(outside), 0.0, 0.0])
+    got = compat.furthest_point_sample(xyz.cuda(), 2000).cpu()
+    want = O.fps(xyz, 2000, 0, True).astype(np.int32)
+    np.testing.assert_array_equal(got.numpy(), want)
+    picked = set(got[0].tolist())
+    assert picked.isdisjoint(range(1, 41)) and 41 in picked
+
+
+def test_fps_c1_and_c2_full(cuda_device):
+    import mps_pointops as mp
+
+    c1 = bench.make_c1()
+    np.testing.assert_array_equal(host(mp.furthest_point_sample(c1.cuda(), 512)), O.fps(c1, 512))
+    c2 = bench.make_c2()
+    np.testing.assert_array_equal(host(mp.furthest_point_sample(c2.cuda(), 1024)), O.fps(c2, 1024))
+
+
+@pytest.mark.parametrize("n,k", [(1, 1), (31, 5), (64, 64), (65, 65), (300, 17), (1000, 128),
+                                 (700, 256), (5000, 32)])
+def test_knn3_matches_oracle(cuda_device, n, k):
+    import mps_pointops as mp
+
+    ref = rand_cloud(2, n, n + k)
+    ref[:, n // 3:] = torch.round(ref[:, n // 3:] * 2) / 2  # exact ties
+    query = torch.cat([ref[:, :5], rand_cloud(2, 9, 1)], 1)
+    want_d, want_i = O.knn3(query, ref, k)
+    d, i = mp.knn(query.cuda(), ref.cuda(), k)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+@pytest.mark.parametrize("descending", [False, True])
+def test_knn3_spatially_sorted_reference(cuda_device, descending):
+    import mps_pointops as mp
+
+    ref = rand_cloud(1, 20000, 0)
+    ref = ref[:, ref[0, :, 0].argsort(descending=descending)].contiguous()
+    query = rand_cloud(1, 64, 1)
+    want_d, want_i = O.knn3(query, ref, 128)
+    d, i = mp.knn(query.cuda(), ref.cuda(), 128)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+def test_knn3_nan_padding_matches_reference_kernel(cuda_device):
+    """kernels/knn.metal semantics: NaN distances never insert; unfilled slots
+    stay (inf, 2^32-1); inf distances are ordinary candidates."""
+    import mps_pointops as mp
+
+    ref = torch.tensor([[[np.nan, 0, 0], [np.inf, 0, 0], [1, 0, 0], [np.nan, 1, 1]]]).float()
+    query = torch.tensor([[[0, 0, 0], [np.nan, 0, 0]]]).float()
+    want_d, want_i = O.knn3(query, ref, 3)
+    d, i = mp.knn(query.cuda(), ref.cuda(), 3)
+    assert want_i.tolist() == [[[2, 1, 4294967295], [4294967295] * 3]]
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+@pytest.mark.parametrize("dim,k", [(1, 5), (2, 1), (4, 33), (64, 20), (128, 256), (7, 64)])
+def test_knn_feat_matches_oracle(cuda_device, dim, k):
+    import mps_pointops as mp
+
+    g = torch.Generator().manual_seed(107 + dim)
+    query = torch.randn(2, 9, dim, generator=g)
+    ref = torch.randn(2, 300, dim, generator=g)
+    ref[:, 20] = ref[:, 3]
+    query[:, 0] = ref[:, 3]
+    q_view = torch.cat((query, query), dim=1)[:, ::2]
+    want_d, want_i = O.knn_feat(q_view, ref, k)
+    d, i = mp.knn(q_view.cuda(), ref.cuda(), k)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+@pytest.mark.parametrize("radius,k", [(0.1, 16), (0.2, 32), (0.4, 128), (0.7, 1), (2.0, 65)])
+def test_ball_query_matches_oracle(cuda_device, radius, k):
+    import mps_pointops as mp
+
+    p = bench.make_c2(seed=11, B=3, N=1500)
+    q = p[:, ::5].contiguous()
+    want_d, want_i = O.ball_query(q, p, radius, k)
+    d, i = mp.ball_query(q.cuda(), p.cuda(), radius, k)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+def test_ball_query_lengths_poisoned_outputs(cuda_device):
+    """tests/test_ball_query_mps.py:127-213: every slot is written (outputs
+    poisoned first), lengths respected, NaN/inf points never match."""
+    from mps_pointops import _ball_query_mps as bq
+    from mps_pointops import _native
+
+    batch, nq, npts = 2, 9, 65
+    q = torch.zeros(batch, nq, 3)
+    p = torch.zeros(batch, npts, 3)
+    for j in range(npts):
+        p[:, j, 0] = 2.0 if j % 5 == 1 else (0.25 if j % 3 == 0 else 0.5)
+    p[:, 31, 0] = float("nan")
+    p[:, 32, 0] = float("inf")
+    q[:, 2, 0] = 0.5
+    q[:, 4, 0] = 20.0
+    ql, pl = [9, 7], [65, 49]
+    for dtype in (torch.float32, torch.float16):
+        for k in (1, 31, 32, 33, 65):
+            want_d, want_i = O.ball_query(q.to(dtype).float(), p.to(dtype).float(), 1.0, k, ql, pl)
+            idx = torch.full((batch, nq, k), -777, dtype=torch.int64).cuda()
+            dist = torch.full((batch, nq, k), float("nan")).cuda()
+            qc, pc = q.to(dtype).cuda(), p.to(dtype).cuda()
+            qlc, plc = torch.tensor(ql).cuda(), torch.tensor(pl).cuda()
+            _, r2 = bq._checked_radius_and_k(1.0, k)
+            name = "pointops_ball_query_f32" if dtype == torch.float32 else "pointops_ball_query_f16"
+            _native.call(name, qc.data_ptr(), pc.data_ptr(), qlc.data_ptr(), plc.data_ptr(),
+                         idx.data_ptr(), dist.data_ptr(), batch, nq, npts, k, r2,
+                         _native.stream(qc.device))
+            torch.cuda.synchronize()
+            np.testing.assert_array_equal(host(idx), want_i)
+            same_bits(host(dist), want_d)
+            res = bq.ball_query(qc, pc, radius=1.0, k=k, query_lengths=qlc, point_lengths=plc)
+            np.testing.assert_array_equal(host(res.indices), want_i)
+
+
+def test_ball_query_c1_c2_c3_full(cuda_device):
+    import mps_pointops as mp
+
+    c1 = bench.make_c1()
+    centres = c1.gather(1, torch.from_numpy(O.fps(c1, 512))[..., None].expand(-1, -1, 3))
+    want_d, want_i = O.ball_query(centres, c1, 0.2, 32)
+    d, i = mp.ball_query(centres.cuda(), c1.cuda(), 0.2, 32)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+    c2 = bench.make_c2()
+    centres = c2.gather(1, torch.from_numpy(O.fps(c2, 1024))[..., None].expand(-1, -1, 3))
+    for radius, k in bench.C2_RADII:
+        want_d, want_i = O.ball_query(centres, c2, radius, k)
+        d, i = mp.ball_query(centres.cuda(), c2.cuda(), radius, k)
+        np.testing.assert_array_equal(host(i), want_i)
+        same_bits(host(d), want_d)
+
+
+def test_knn_c1_c2_full(cuda_device):
+    import mps_pointops as mp
+
+    for make, npoint in ((bench.make_c1, 512), (bench.make_c2, 1024)):
+        x = make()
+        centres = x.gather(1, torch.from_numpy(O.fps(x, npoint))[..., None].expand(-1, -1, 3))
+        want_d, want_i = O.knn3(centres, x, 16)
+        d, i = mp.knn(centres.cuda(), x.cuda(), 16)
+        np.testing.assert_array_equal(host(i), want_i)
+        same_bits(host(d), want_d)
+
+
+def test_three_nn_and_interpolate_c2(cuda_device):
+    from mps_pointops import three_interpolate, three_nn
+
+    x = bench.make_c2()
+    centres = x.gather(1, torch.from_numpy(O.fps(x, 1024))[..., None].expand(-1, -1, 3))
+    want_d, want_i = O.three_nn(x, centres)
+    d, i = three_nn(x.cuda(), centres.cuda())
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+    inv = 1.0 / (d + 1e-8)
+    w = (inv / inv.sum(-1, keepdim=True)).contiguous()
+    g = torch.Generator().manual_seed(9)
+    feats = torch.randn(32, 128, 1024, generator=g)
+    out = three_interpolate(feats.cuda(), i, w)
+    same_bits(host(out), O.three_interpolate(feats, host(i), host(w)))
+    fc = feats.cuda().requires_grad_()
+    upstream = torch.randn(32, 128, 4096, generator=g)
+    three_interpolate(fc, i, w).backward(upstream.cuda())
+    want_g = O.three_interpolate_backward(upstream, host(i), host(w), 1024)
+    np.testing.assert_allclose(host(fc.grad), want_g, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("m", [3, 4, 50, 1025, 2100])
+def test_three_nn_matches_oracle(cuda_device, m):
+    from mps_pointops import three_nn
+
+    u = rand_cloud(2, 300, m)
+    k = rand_cloud(2, m, m + 1)
+    k[:, m // 2:] = k[:, : m - m // 2]
+    want_d, want_i = O.three_nn(u, k)
+    d, i = three_nn(u.cuda(), k.cuda())
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
+def test_three_nn_nonfinite(cuda_device):
+    from mps_pointops import three_nn
+
+    u = torch.zeros(1, 2, 3)
+    u[0, 1, 0] = float("nan")
+    k = torch.tensor([[[np.nan, 0, 0], [np.inf, 0, 0], [1, 0, 0], [np.nan, 0, 0], [2, 0, 0]]]).float()
+    want_d, want_i = O.three_nn(u, k)
+    d, i = three_nn(u.cuda(), k.cuda())
+    np.testing.assert_array_equal(host(i), want_i)
+
+
+@pytest.mark.parametrize("dim,norm,dtype", [(3, 2, torch.float32), (3, 1, torch.float32),
+                                            (5, 2, torch.float32), (64, 1, torch.float32),
+                                            (3, 2, torch.float64), (2, 1, torch.float64)])
+def test_chamfer_nearest_matches_oracle(cuda_device, dim, norm, dtype):
+    from mps_pointops import chamfer
+
+    g = torch.Generator().manual_seed(dim * 10 + norm)
+    q = torch.randn(3, 300, dim, generator=g, dtype=torch.float64).to(dtype)
+    r = (torch.round(torch.randn(3, 2100, dim, generator=g, dtype=torch.float64) * 2) / 2).to(dtype)
+    ql, rl = [300, 40, 299], [2100, 1025, 3]
+    want_d, want_i = O.chamfer_nearest(q, r, ql, rl, norm)
+    d, i = chamfer._nearest_mps(q.cuda(), r.cuda(), _batch(ql), _batch(rl), norm=norm)
+    np.testing.assert_array_equal(host(i), want_i)
+    np.testing.assert_array_equal(host(d), want_d)
+
+
+def test_chamfer_c5_forward_backward_reduced(cuda_device):
+    """Config 5 generator at B=4 (the oracle's cost is quadratic): loss and
+    both gradients against the closed form on the oracle's pairs."""
+    import mps_pointops as mp
+
+    y1, y2 = bench.make_c5(B=4, P=2048)
+    a = y1.cuda().requires_grad_()
+    b = y2.cuda().requires_grad_()
+    loss, _ = mp.chamfer_distance(a, b)
+    loss.backward()
+    d12, i12 = O.chamfer_nearest(y1, y2)
+    d21, i21 = O.chamfer_nearest(y2, y1)
+    want_loss = (d12.astype(np.float64).mean(1) + d21.astype(np.float64).mean(1)).mean()
+    np.testing.assert_allclose(loss.item(), want_loss, rtol=1e-5)
+    B, P = 4, 2048
+    g = 1.0 / (B * P)
+    ga = np.zeros((B, P, 3))
+    gb = np.zeros((B, P, 3))
+    y1n, y2n = y1.numpy().astype(np.float64), y2.numpy().astype(np.float64)
+    for bb in range(B):
+        diff = y1n[bb] - y2n[bb, i12[bb]]
+        ga[bb] += 2 * g * diff
+        np.add.at(gb[bb], i12[bb], -2 * g * diff)
+        diff = y2n[bb] - y1n[bb, i21[bb]]
+        gb[bb] += 2 * g * diff
+        np.add.at(ga[bb], i21[bb], -2 * g * diff)
+    np.testing.assert_allclose(host(a.grad), ga, rtol=1e-4, atol=1e-9)
+    np.testing.assert_allclose(host(b.grad), gb, rtol=1e-4, atol=1e-9)
+
+
+@pytest.mark.parametrize("k", [1, 4, 40, 256])
+def test_flat_knn_radius_match_oracle(cuda_device, k):
+    from mps_pointops import flat
+
+    rng = np.random.default_rng(k)
+    x = rng.random((3000, 3), dtype=np.float32)
+    y = rng.random((500, 3), dtype=np.float32)
+    bx = np.sort(rng.integers(0, 5, 3000))
+    by = np.sort(rng.integers(0, 5, 500))
+    size = int(max(bx.max(), by.max())) + 1
+    px = np.searchsorted(bx, np.arange(size + 1)).astype(np.int64)
+    py = np.searchsorted(by, np.arange(size + 1)).astype(np.int64)
+    xc, yc = torch.from_numpy(x).cuda(), torch.from_numpy(y).cuda()
+    bxc, byc = torch.from_numpy(bx).cuda(), torch.from_numpy(by).cuda()
+    got = flat.knn(xc, yc, k, bxc, byc)
+    want = O.knn_flat(x, y, px, py, min(k, len(x)))
+    q, s = np.nonzero(want >= 0)
+    assert got.cpu().tolist() == [q.tolist(), want[q, s].tolist()]
+    got = flat.radius(xc, yc, 0.07, bxc, byc, max_num_neighbors=k)
+    want = O.radius_flat(x, y, px, py, 0.07, min(k, len(x)))
+    q, s = np.nonzero(want >= 0)
+    assert got.cpu().tolist() == [q.tolist(), want[q, s].tolist()]
+    feats = rng.standard_normal((3000, 16)).astype(np.float32)
+    qf = rng.standard_normal((500, 16)).astype(np.float32)
+    got = flat.knn(torch.from_numpy(feats).cuda(), torch.from_numpy(qf).cuda(), min(k, 64), bxc, byc)
+    want = O.knn_flat(feats, qf, px, py, min(k, 64))
+    q, s = np.nonzero(want >= 0)
+    assert got.cpu().tolist() == [q.tolist(), want[q, s].tolist()]
+
+
+def test_flat_fps_ragged_matches_oracle(cuda_device):
+    from mps_pointops import flat
+
+    g = torch.Generator().manual_seed(7)
+    x = torch.rand(20000, 3, generator=g)
+    ptr = [0, 2, 82, 82, 87, 9087, 20000]
+    lengths = np.diff(ptr)
+    got = flat.fps(x.cuda(), ptr=ptr, ratio=0.25, random_start=False)
+    counts = np.ceil(lengths.astype(np.float32) * np.float32(0.25)).astype(np.int64)
+    out_ptr = np.concatenate([[0], np.cumsum(counts)])
+    want = O.fps_flat(x, ptr, out_ptr, np.zeros(len(lengths), np.int64))
+    np.testing.assert_array_equal(host(got), want)
+
+
+def test_repeated_dispatch_is_stable(cuda_device):
+    import mps_pointops as mp
+
+    x = bench.make_c2(B=4).cuda()
+    first = mp.furthest_point_sample(x, 256)
+    c = x.gather(1, first[..., None].expand(-1, -1, 3)).contiguous()
+    bq = mp.ball_query(c, x, 0.2, 32)[1]
+    kn = mp.knn(c, x, 16)[1]
+    for _ in range(20):
+        assert torch.equal(mp.furthest_point_sample(x, 256), first)
+        assert torch.equal(mp.ball_query(c, x, 0.2, 32)[1], bq)
+        assert torch.equal(mp.knn(c, x, 16)[1], kn)
