@@ -97,8 +97,9 @@ hipError_t pointops_knn_flat(const float *y, const float *x, const int64_t *ptr_
  * _ball_query_mps.py:139-162 (kernels/ball_query.metal:126-166).  The first K
  * points j in input order with fl32((dx^2+dy^2)+dz^2) < radius_sq; empty
  * slots are (idx -1, dist2 0).  Queries at or beyond query_lengths[b] are
- * padding; only points below point_lengths[b] are scanned.  The _f16 entry
- * takes IEEE half coordinates (uint16 bit patterns) widened exactly. */
+ * padding; only points below point_lengths[b] are scanned (either lengths
+ * pointer may be NULL: every query / point is valid).  The _f16 entry takes
+ * IEEE half coordinates (uint16 bit patterns) widened exactly. */
 hipError_t pointops_ball_query_f32(const float *queries, const float *points,
                                    const int64_t *query_lengths, const int64_t *point_lengths,
                                    int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,

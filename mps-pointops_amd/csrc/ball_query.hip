@@ -48,8 +48,9 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
     int64_t* oi = out_idx + row * K;
     float* od = out_dist + row * K;
     int found = 0;
-    if (qi < query_lengths[b]) {
-        const int64_t plen = point_lengths[b];
+    const int64_t qlen = query_lengths != nullptr ? query_lengths[b] : Q;
+    if (qi < qlen) {
+        const int64_t plen = point_lengths != nullptr ? point_lengths[b] : P;
         const int n = static_cast<int>(plen < P ? plen : P);
         const S* qp = queries + 3 * row;
         const float qx = widen(qp[0]), qy = widen(qp[1]), qz = widen(qp[2]);

@@ -228,9 +228,208 @@ __global__ __launch_bounds__(kKnnThreads) void knn_flat_kernel(
     }
 }
 
+// ------------------------------------------------------------------------
+// Small-K 3-D kNN (K <= KMAX <= 32): one lane per query.
+//
+// A block serves 64 queries of one cloud (lane = query); its 4 waves split
+// the references into 4 contiguous ranges and each wave keeps, per lane, the
+// best KMAX keys of its range; the 4 partial lists are merged at the end.
+// Every lane of a wave reads the same reference, so references come through
+// uniform (scalar) loads.  Keys are the squared distance's bit pattern:
+// non-negative floats and +inf order like unsigned integers and NaN patterns
+// are larger, so `bits(d) < tau`, with tau = key of the K-th entry
+// (0x7F800001 while the list has free slots), admits exactly the references
+// that beat the K-th entry under the (distance, index) order of the reference
+// kernel -- a range is visited in index order, so an equal distance never
+// beats an entry already kept, and NaN never enters.  Admitted references go
+// to a per-lane LDS buffer ([slot][lane], conflict free); when any lane's
+// buffer is full, and at the end, each lane merges it into its sorted register
+// list.
+constexpr int kLaneWaves = 4;
+constexpr int kLaneThreads = kLaneWaves * kWave;
+constexpr int kLaneCap = 32;  // buffered candidates per lane (merged at half)
+constexpr uint32_t kEmptyKey = 0x7F800001u;
+
+template <int KMAX>
+__device__ __forceinline__ uint32_t kth_key(const uint32_t (&lk)[KMAX], int K) {
+    if (K == KMAX) return lk[KMAX - 1];
+    uint32_t t = 0;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+        if (s == K - 1) t = lk[s];
+    return t;
+}
+
+// Insert this lane's `cnt` buffered candidates (in index order) into its
+// sorted list; the wave loops while any lane has entries left.
+template <int KMAX>
+__device__ __forceinline__ void lane_merge(uint32_t (&lk)[KMAX], int (&li)[KMAX], uint32_t& tau,
+                                           int K, const uint2* buf, int lane, int cnt) {
+    for (int e = 0;; ++e) {
+        const bool has = e < cnt;
+        if (ballot(has) == 0) break;
+        // A lane with nothing to insert inserts the no-op key 0xFFFFFFFF
+        // (never below a slot), so the network runs without branches.
+        uint32_t ck = 0xFFFFFFFFu;
+        int cj = 0;
+        if (has) {
+            const uint2 c = buf[e * kWave + lane];
+            if (c.x < tau) {  // the K-th key may have tightened since buffering
+                ck = c.x;
+                cj = static_cast<int>(c.y);
+            }
+        }
+        if (ballot(ck != 0xFFFFFFFFu) == 0) continue;
+        // Slots after the insertion point move down one place; `here` means
+        // the candidate goes before slot s, `prev` before slot s - 1.
+        bool here = ck < lk[KMAX - 1];
+#pragma unroll
+        for (int s = KMAX - 1; s > 0; --s) {
+            const bool prev = ck < lk[s - 1];
+            lk[s] = prev ? lk[s - 1] : min(ck, lk[s]);
+            li[s] = prev ? li[s - 1] : (here ? cj : li[s]);
+            here = prev;
+        }
+        lk[0] = min(ck, lk[0]);
+        li[0] = here ? cj : li[0];
+        tau = kth_key<KMAX>(lk, K);
+    }
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
+    int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
+    // Per wave: the candidate buffer during the scan, then the final list.
+    __shared__ uint2 lds[kLaneWaves][KMAX > kLaneCap ? KMAX : kLaneCap][kWave];
+    // Per wave and lane: the key of its K-th entry, read by the other waves.
+    __shared__ uint32_t taus[kLaneWaves][kWave];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t b = blockIdx.y;
+    const int64_t m = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+    const bool active = m < M;
+    const float* qp = query + 3 * (b * M + (active ? m : 0));
+    const float qx = qp[0], qy = qp[1], qz = qp[2];
+    const float* rp = ref + 3 * b * N;
+    uint2* buf = &lds[wave][0][0];
+    const int64_t span = (N + kLaneWaves - 1) / kLaneWaves;
+    const int64_t lo = wave * span;
+    const int64_t hi = min<int64_t>(N, lo + span);
+
+    uint32_t lk[KMAX];
+    int li[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        lk[s] = kEmptyKey;
+        li[s] = -1;
+    }
+    uint32_t tau = active ? kEmptyKey : 0u;  // inactive lanes admit nothing
+    taus[wave][lane] = tau;
+    __syncthreads();
+    // Admission limit: this wave's K-th key and the other waves' K-th keys
+    // (read without synchronisation: they only decrease, so a stale value is
+    // a looser but still valid limit).  A lower range holds smaller indices,
+    // so an equal key from a higher range cannot beat its K-th entry, while an
+    // equal key from a lower range can beat a higher range's K-th entry.
+    auto limit = [&]() {
+        uint32_t lim = tau;
+#pragma unroll
+        for (int w = 0; w < kLaneWaves; ++w) {
+            if (w == wave) continue;
+            const uint32_t t = taus[w][lane];
+            lim = min(lim, w < wave ? t : t + 1u);
+        }
+        return lim;
+    };
+    int cnt = 0;
+    uint32_t lim = tau;
+    auto visit = [&](float rx, float ry, float rz, int j) {
+        const uint32_t key = static_cast<uint32_t>(f2i(sqdist3(rx, ry, rz, qx, qy, qz)));
+        const bool pass = key < lim;
+        if (ballot(pass) == 0) return;
+        if (pass) {
+            buf[cnt * kWave + lane] = make_uint2(key, static_cast<uint32_t>(j));
+            ++cnt;
+        }
+    };
+    constexpr int kRefBatch = 8;
+    // After a batch: merge once a lane's buffer could not take another batch.
+    auto drain = [&]() {
+        if (ballot(cnt > kLaneCap - kRefBatch) != 0) {
+            lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
+            cnt = 0;
+            taus[wave][lane] = tau;
+        }
+    };
+    // Batches of kRefBatch references through uniform (scalar) loads.
+    int j0 = static_cast<int>(lo);
+    const int jhi = static_cast<int>(hi);
+    for (; j0 + kRefBatch <= jhi; j0 += kRefBatch) {
+        float cur[3 * kRefBatch];
+        const float* r = rp + 3 * static_cast<int64_t>(j0);
+#pragma unroll
+        for (int t = 0; t < 3 * kRefBatch; ++t) cur[t] = r[t];
+        lim = limit();
+#pragma unroll
+        for (int u = 0; u < kRefBatch; ++u) visit(cur[3 * u], cur[3 * u + 1], cur[3 * u + 2], j0 + u);
+        drain();
+    }
+    for (; j0 < jhi; ++j0) {
+        const float* r = rp + 3 * static_cast<int64_t>(j0);
+        lim = limit();
+        visit(r[0], r[1], r[2], j0);
+        drain();
+    }
+    lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
+
+    // Publish the partial list ([slot][lane]) and merge the 4 lists in wave 0.
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+        if (s < K) buf[s * kWave + lane] = make_uint2(lk[s], static_cast<uint32_t>(li[s]));
+    __syncthreads();
+    if (wave != 0 || !active) return;
+    int head[kLaneWaves] = {0, 0, 0, 0};
+    const int64_t row = (b * M + m) * K;
+    for (int s = 0; s < K; ++s) {
+        uint2 best = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+        int from = 0;
+#pragma unroll
+        for (int w = 0; w < kLaneWaves; ++w) {
+            if (head[w] < K) {
+                const uint2 c = lds[w][head[w]][lane];
+                if (c.x < best.x || (c.x == best.x && c.y < best.y)) {
+                    best = c;
+                    from = w;
+                }
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < kLaneWaves; ++w)
+            if (w == from) ++head[w];
+        const bool empty = static_cast<int>(best.y) < 0;
+        out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(best.x)));
+        out_idx[row + s] = static_cast<int64_t>(best.y);
+    }
+}
+
+template <int KMAX>
+hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
+                       int64_t M, int64_t N, int K, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave), static_cast<uint32_t>(B));
+    hipLaunchKernelGGL((knn3_lane_kernel<KMAX>), grid, dim3(kLaneThreads), 0, stream, query, ref,
+                       dist, idx, M, N, K);
+    return hipGetLastError();
+}
+
 template <bool DIM3>
 hipError_t launch_dense(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                         int64_t M, int64_t N, int D, int K, hipStream_t stream) {
+    if (DIM3 && K <= 32 && B <= 65535 && (M + kWave - 1) / kWave <= INT32_MAX) {
+        if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, K, stream);
+        if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, K, stream);
+        return launch_lane<32>(query, ref, dist, idx, B, M, N, K, stream);
+    }
     const int64_t rows = B * M;
     const dim3 grid(static_cast<uint32_t>((rows + kKnnWaves - 1) / kKnnWaves));
     const dim3 block(kKnnThreads);

@@ -29,10 +29,13 @@ class BallQueryResult(NamedTuple):
 
 def _lengths_or_full(
     lengths: torch.Tensor | None, *, batch: int, count: int, device: torch.device, name: str
-) -> torch.Tensor:
-    """_ball_query_mps.py:73-84 (one host sync when lengths are given)."""
+) -> torch.Tensor | None:
+    """_ball_query_mps.py:73-84 (one host sync when lengths are given).
+
+    ``None`` stays ``None``: the kernel then treats every row as valid, which
+    saves two fill launches per call."""
     if lengths is None:
-        return torch.full((batch,), count, device=device, dtype=torch.int64)
+        return None
     if not isinstance(lengths, torch.Tensor):
         raise TypeError(f"{name} must be a torch.Tensor or None")
     if lengths.shape != (batch,) or lengths.dtype != torch.int64 or lengths.device != device:
@@ -83,8 +86,8 @@ def _launch(queries, points, query_lengths, point_lengths, radius_sq, k):
         name = ("pointops_ball_query_f32" if queries.dtype == torch.float32
                 else "pointops_ball_query_f16")
         _native.call(
-            name, queries.data_ptr(), points.data_ptr(), query_lengths.data_ptr(),
-            point_lengths.data_ptr(), indices.data_ptr(), distances.data_ptr(),
+            name, queries.data_ptr(), points.data_ptr(), _native.ptr(query_lengths),
+            _native.ptr(point_lengths), indices.data_ptr(), distances.data_ptr(),
             batch, query_count, point_count, k, radius_sq, _native.stream(device),
         )
     return distances, indices
