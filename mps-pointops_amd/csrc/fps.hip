@@ -9,9 +9,11 @@
 //
 // Kernels:
 //   fps_regs_kernel<P,T>    one workgroup per cloud, the cloud's points and
-//                           running distances in VGPRs (P per thread), a
-//                           float4 copy in LDS for the centroid broadcast,
-//                           one barrier per step (double-buffered slots).
+//                           running distances in VGPRs (P consecutive points
+//                           per thread, so lane order is index order and the
+//                           argmax needs no index reduction), a float4 copy
+//                           in LDS for the centroid broadcast, one barrier per
+//                           step (double-buffered slots).
 //   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
 //                           LDS: points re-read from L2, running distances in
 //                           a caller-provided scratch array.
@@ -86,6 +88,10 @@ __device__ __forceinline__ int block_argmax(const int2* slots) {
     return bidx;
 }
 
+// Thread t holds points t*P .. t*P+P-1, so point order = (wave, lane, slot)
+// order: the first maximum found by lane, then by wave, is the one with the
+// smallest index.  Running distances are never NaN (fminf), so their bit
+// patterns order like the floats as signed ints (-inf below +0).
 template <int P, int T>
 __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ xyz,
                                                      const int64_t* __restrict__ ptr,
@@ -94,6 +100,7 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
                                                      int64_t* __restrict__ out, int64_t N,
                                                      int64_t npoint, int64_t start, int skip) {
     constexpr int NW = T / kWave;
+    constexpr int kNegInf = static_cast<int>(0xFF800000u);
     __shared__ float4 spts[P * T];
     __shared__ int2 slots[2][NW];
 
@@ -106,10 +113,11 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
     const int wave = tid / kWave;
     const int lane = tid % kWave;
 
-    float px[P], py[P], pz[P], md[P];
+    float px[P], py[P], pz[P];
+    float md[P];  // running distances
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-        const int j = tid + k * T;
+        const int j = tid * P + k;
         if (j < n) {
             const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
             px[k] = x;
@@ -129,26 +137,43 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
         if (tid == 0) o[step] = seg.base + far;
         if (step + 1 == seg.cnt) break;
         const float4 c = spts[far];
-        float bv = -INFINITY;
-        int bi = INT_MAX;
+        int v[P], s[P];
 #pragma unroll
         for (int k = 0; k < P; ++k) {
             const float d = sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z);
-            const float m = fminf(md[k], d);
-            md[k] = m;
-            // k grows with the index inside a thread: strict > keeps the smaller one.
-            if (m > bv) {
-                bv = m;
-                bi = tid + k * T;
+            md[k] = fminf(md[k], d);
+            v[k] = f2i(md[k]);
+            s[k] = k;
+        }
+        // Lane argmax as a tree; the right (larger-index) side wins only if
+        // larger.  Slots merge by value, not by array position, so that the
+        // compiler keeps every step a register select.
+#pragma unroll
+        for (int w = 1; w < P; w <<= 1) {
+#pragma unroll
+            for (int k = 0; k + w < P; k += 2 * w) {
+                const int right = -static_cast<int>(v[k + w] > v[k]);
+                v[k] = max(v[k], v[k + w]);
+                s[k] ^= (s[k] ^ s[k + w]) & right;
             }
         }
-        const float wv = wave_max(bv);
-        const int wi = wave_min(bv == wv ? bi : INT_MAX);
+        // First lane holding the wave's largest value: the smallest index.
+        const int wv = wave_max_i32(v[0]);
+        const int wl = static_cast<int>(__builtin_ctzll(ballot(v[0] == wv)));
+        const int wi = (wave * kWave + wl) * P + readlane(s[0], wl);
         int2* buf = slots[step & 1];
-        if (lane == 0) buf[wave] = make_int2(f2i(wv), wi);
+        if (lane == 0) buf[wave] = make_int2(wv, wi);
         __syncthreads();
-        const int win = block_argmax<NW>(buf);
-        far = (win == INT_MAX) ? 0 : win;
+        int bv = buf[0].x, bi = buf[0].y;  // first wave with the largest value
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const int2 e = buf[w];
+            if (e.x > bv) {
+                bv = e.x;
+                bi = e.y;
+            }
+        }
+        far = (bv == kNegInf) ? 0 : bi;  // nothing can be picked: index 0, like the reference
     }
 }
 
@@ -412,8 +437,8 @@ __global__ __launch_bounds__(T) void fps_large_kernel(const float* __restrict__ 
 
 // ------------------------------------------------------------ dispatch
 
-constexpr int kRegsThreads = 256;
-constexpr int kRegsMaxPoints = 32 * kRegsThreads;  // 8192 points, 128 KiB of LDS
+constexpr int kRegsThreads = 512;  // 8 waves: two per SIMD hide each other's reduction latency
+constexpr int kRegsMaxPoints = 16 * kRegsThreads;  // 8192 points, 128 KiB of LDS
 constexpr int kGlobalThreads = 1024;
 
 template <int P>
@@ -440,8 +465,6 @@ hipError_t launch_fps(const float* xyz, const int64_t* ptr, const int64_t* out_p
         return launch_regs<8>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
     if (max_len <= 16 * kRegsThreads)
         return launch_regs<16>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
-    if (max_len <= 32 * kRegsThreads)
-        return launch_regs<32>(xyz, ptr, out_ptr, starts, out, blocks, N, npoint, start, skip, stream);
     if (scratch == nullptr) return hipErrorInvalidValue;
     hipLaunchKernelGGL((fps_global_kernel<kGlobalThreads>), dim3(static_cast<uint32_t>(blocks)),
                        dim3(kGlobalThreads), 0, stream, xyz, ptr, out_ptr, starts, out, scratch,

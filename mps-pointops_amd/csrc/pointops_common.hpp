@@ -75,6 +75,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Maximum over the wave of a signed int; every lane gets the result.
+__device__ __forceinline__ int wave_max_i32(int v) {
+    v = max(v, dpp<kDppQuadXor1>(v));
+    v = max(v, dpp<kDppQuadXor2>(v));
+    v = max(v, dpp<kDppRowHalfMirror>(v));
+    v = max(v, dpp<kDppRowMirror>(v));
+    const int a = readlane(v, 0);
+    const int b = readlane(v, 16);
+    const int c = readlane(v, 32);
+    const int d = readlane(v, 48);
+    return max(max(a, b), max(c, d));
+}
+
 // Minimum over the wave of a signed int; every lane gets the result.
 __device__ __forceinline__ int wave_min(int v) {
     v = min(v, dpp<kDppQuadXor1>(v));
