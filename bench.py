@@ -114,10 +114,13 @@ C2_KNN_K = 16
 # ---------------------------------------------------------------- timing
 
 MI355X_HBM_BYTES_PER_S = 8.0e12
-# FP32 VALU without packed math or FMA: 256 CUs x 64 lanes x 2.4 GHz op/s is
-# the issue-rate ceiling of this build; the published vector-FP32 peak
-# (157.3 TFLOP/s) counts packed FMA (4 flops per lane-cycle).
+# Published MI355X vector/matrix FP32 peak.  This path runs on the FP32 VALU
+# without FMA (the reference's rounding) and without packed FP32, so its own
+# issue ceiling is 256 CUs x 64 lanes x 2.4 GHz = 39.3 T op/s; the JSON line
+# reports against the published figure.
 MI355X_FP32_PEAK = 157.3e12
+FPS_OPS_PER_POINT_STEP = 9  # 3 sub, 3 mul, 2 add (unfused), 1 min
+PAIR_OPS = 8                # 3-D squared distance: 3 sub, 3 mul, 2 add
 
 
 class KernelTimer:
@@ -135,6 +138,32 @@ class KernelTimer:
         end.record(self.stream)
         end.synchronize()
         return start.elapsed_time(end) / 1e3 / reps
+
+
+def fps_kernel_name(n: int) -> str:
+    """Template instance fps_regs_kernel<P,512> that a cloud of n points uses."""
+    p = 1
+    while p * 512 < n:
+        p *= 2
+    return f"fps_regs_kernel<{p},512>"
+
+
+def profiled_traffic(kernel: str, workload: str):
+    """HBM bytes per launch of `kernel` on `workload`, as recorded from the
+    FETCH_SIZE/WRITE_SIZE counter runs in profiles/*.md (a line
+    `traffic_bytes_per_launch[<kernel>@<workload>]: <bytes>`), else None."""
+    key = f"traffic_bytes_per_launch[{kernel}@{workload}]:"
+    for path in sorted((ROOT / "profiles").glob("*.md")):
+        for line in path.read_text().splitlines():
+            if line.strip().startswith(key):
+                return float(line.split(":", 1)[1].strip())
+    return None
+
+
+def ball_scanned_pairs(idx: torch.Tensor, n: int) -> int:
+    """Pairs a first-K ball query must test: up to the K-th hit, else all n."""
+    last = idx[..., -1]
+    return int(torch.where(last >= 0, last + 1, torch.full_like(last, n)).sum())
 
 
 def cpu_info() -> dict:
@@ -182,6 +211,19 @@ def cpu_baseline(xyz_cpu: torch.Tensor, clouds: int) -> dict:
     }
 
 
+def timed_steps(step, steps: int, warmup: int) -> float:
+    """Seconds per step over exactly `steps` steps after `warmup` untimed ones,
+    synchronised on both sides."""
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        step()
+    torch.cuda.synchronize()
+    return (time.perf_counter() - t0) / steps
+
+
 def run(args) -> dict:
     import mps_pointops as mp
 
@@ -189,9 +231,7 @@ def run(args) -> dict:
     xyz_cpu = make_c2()
     xyz = xyz_cpu.to(device)
     B, N, _ = xyz.shape
-    stream = torch.cuda.current_stream(device)
-    timer = KernelTimer(stream)
-
+    timer = KernelTimer(torch.cuda.current_stream(device))
     state = {}
 
     def fps():
@@ -213,33 +253,31 @@ def run(args) -> dict:
         balls()
         knn()
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # Whole-step wall time over exactly K steps.
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for _ in range(args.steps):
-        step()
-    torch.cuda.synchronize()
-    wall = (time.perf_counter() - t0) / args.steps
+    wall = timed_steps(step, args.steps, args.warmup)
 
     # Per-op kernel time on the launch stream (HIP events).
     reps = max(5, args.steps)
     t_fps = timer.time(fps, reps)
     t_ball = timer.time(balls, reps)
     t_knn = timer.time(knn, reps)
-    t_sum = t_fps + t_ball + t_knn
-    value = B * N / t_sum
 
-    # Roofline of the dominant kernel (FPS): 9 FP32 ops per point per step
-    # (3 sub, 3 mul, 2 add, 1 min) over B*npoint*N point-steps.
-    fps_ops = 9.0 * B * C2_NPOINT * N
+    # Algorithmic work (FP32 ops): FPS 9 per point-step; ball query 8 per
+    # scanned pair (up to the K-th hit); kNN 8 per pair (all pairs).
+    fps_ops = FPS_OPS_PER_POINT_STEP * B * C2_NPOINT * N
+    ball_ops = sum(PAIR_OPS * ball_scanned_pairs(mp.ball_query(centres, xyz, r, k)[1], N)
+                   for r, k in C2_RADII)
+    knn_ops = PAIR_OPS * B * C2_NPOINT * N
+
+    def op(t, ops):
+        return {"ms": t * 1e3, "points_per_s": B * N / t, "tops": ops / t / 1e12,
+                "frac_fp32_peak": ops / t / MI355X_FP32_PEAK}
+
+    kernel = fps_kernel_name(N)
     achieved = fps_ops / t_fps
+    traffic = profiled_traffic(kernel, "c2")
     result = {
         "metric": "points/sec for FPS+ball_query+kNN at B=32,N=4096; % of HBM/FP32 roofline",
-        "value": value,
+        "value": B * N / wall,
         "unit": "points/s",
         "n_gpus": 1,
         "steps": args.steps,
@@ -255,20 +293,112 @@ def run(args) -> dict:
                         "(0.4,128) + kNN16",
             "B": B, "N": N, "npoint": C2_NPOINT,
         },
-        "breakdown_ms": {"fps": t_fps * 1e3, "ball_query_x3": t_ball * 1e3, "knn": t_knn * 1e3},
+        "ops": {"fps": op(t_fps, fps_ops), "ball_query_x3": op(t_ball, ball_ops),
+                "knn": op(t_knn, knn_ops)},
         "roofline": {
-            "kernel": "fps_regs_kernel<16,256>",
-            "bound": "valu",
+            "kernel": kernel,
+            "bound": "mfma",
+            "compute": "fp32 VALU, unfused (no MFMA, no FMA, no packed fp32)",
             "achieved": achieved / 1e12,
             "peak": MI355X_FP32_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / MI355X_FP32_PEAK,
-            "traffic": None,
+            "traffic": traffic,
         },
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(xyz_cpu, args.cpu_clouds)
     return result
+
+
+def run_other(args) -> dict:
+    """The other BASELINE.json configurations (kernel time on the launch
+    stream, inputs resident in HBM).  Reported for the record; the headline
+    metric is config 2."""
+    import mps_pointops as mp
+
+    dev = torch.device("cuda", 0)
+    timer = KernelTimer(torch.cuda.current_stream(dev))
+    reps = max(3, args.steps)
+    out = {"n_gpus": 1, "dtype": "f32", "data": f"synthetic (BASELINE.json {args.config} generator)",
+           "higher_is_better": True, "vs_baseline": None}
+    if args.config == "c1":
+        x = make_c1().to(dev)
+        B, N, _ = x.shape
+        idx = mp.furthest_point_sample(x, 512)
+        c = x.gather(1, idx[..., None].expand(-1, -1, 3)).contiguous()
+        t_fps = timer.time(lambda: mp.furthest_point_sample(x, 512), reps)
+        t_ball = timer.time(lambda: mp.ball_query(c, x, 0.2, 32), reps)
+        t_knn = timer.time(lambda: mp.knn(c, x, 16), reps)
+        t = t_fps + t_ball + t_knn
+        out.update(metric="points/sec for FPS512+ball(0.2,32)+kNN16 at B=16,N=1024", value=B * N / t,
+                   unit="points/s", config={"workload": "c1 PointNet++ SSG grouping B=16 N=1024"},
+                   ops_ms={"fps": t_fps * 1e3, "ball_query": t_ball * 1e3, "knn": t_knn * 1e3})
+    elif args.config == "c3":
+        x = make_c3().to(dev)
+        N = x.shape[1]
+        idx = mp.furthest_point_sample(x, 16384)
+        c = x.gather(1, idx[..., None].expand(-1, -1, 3)).contiguous()
+        r = max(1, reps // 5)
+        t_fps = timer.time(lambda: mp.furthest_point_sample(x, 16384), r)
+        t_ball = timer.time(lambda: mp.ball_query(c, x, 0.5, 32), r)
+        fps_ops = FPS_OPS_PER_POINT_STEP * 16384 * N
+        ball_ops = PAIR_OPS * ball_scanned_pairs(mp.ball_query(c, x, 0.5, 32)[1], N)
+        out.update(metric="points/sec for FPS16384+ball(0.5,32) at B=1,N=1048576",
+                   value=N / (t_fps + t_ball), unit="points/s",
+                   config={"workload": "c3 large single-cloud FPS (LiDAR-like slab) + ball query"},
+                   ops_ms={"fps": t_fps * 1e3, "ball_query": t_ball * 1e3},
+                   tops={"fps": fps_ops / t_fps / 1e12, "ball_query": ball_ops / t_ball / 1e12})
+    elif args.config == "c4":
+        ref, query, feat = (t.to(dev) for t in make_c4())
+        r = max(1, reps // 5)
+        t_knn = timer.time(lambda: mp.knn(query, ref, 16), r)
+        t_feat = timer.time(lambda: mp.knn(feat, feat, 20), reps)
+        M, N = query.shape[1], ref.shape[1]
+        Bf, Nf, D = feat.shape
+        out.update(metric="queries/sec for exact kNN16, 131072 queries x 1048576 refs",
+                   value=M / t_knn, unit="queries/s",
+                   config={"workload": "c4 kNN at scale + DGCNN feature kNN (8,2048,64) K=20"},
+                   ops_ms={"knn": t_knn * 1e3, "dgcnn_feature_knn": t_feat * 1e3},
+                   tops={"knn": PAIR_OPS * M * N / t_knn / 1e12,
+                         "dgcnn_feature_knn": (3 * D - 1) * Bf * Nf * Nf / t_feat / 1e12})
+    elif args.config == "c5":
+        y1, y2 = (t.to(dev) for t in make_c5())
+        B, P, _ = y1.shape
+        a = y1.clone().requires_grad_()
+        b = y2.clone().requires_grad_()
+
+        def fwd_bwd():
+            loss, _ = mp.chamfer_distance(a, b)
+            loss.backward()
+
+        t = timer.time(fwd_bwd, reps)
+        out.update(metric="points/sec for squared-L2 Chamfer forward+backward at B=32,P=8192",
+                   value=2 * B * P / t, unit="points/s",
+                   config={"workload": "c5 Chamfer mean/mean fwd+bwd, both directions"},
+                   ops_ms={"chamfer_fwd_bwd": t * 1e3},
+                   tops={"forward_pairs": 2 * PAIR_OPS * B * P * P / t / 1e12})
+    return out
+
+
+def probe() -> None:
+    """One pass of each config-2 kernel plus a 256 MiB device copy, for
+    hardware-counter runs (the copy's FETCH_SIZE/WRITE_SIZE give the scale of
+    the counters against known bytes)."""
+    import mps_pointops as mp
+
+    xyz = make_c2().cuda()
+    src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        idx = mp.furthest_point_sample(xyz, C2_NPOINT)
+        centres = xyz.gather(1, idx[..., None].expand(-1, -1, 3)).contiguous()
+        for radius, k in C2_RADII:
+            mp.ball_query(centres, xyz, radius, k)
+        mp.knn(centres, xyz, C2_KNN_K)
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("probe: 3 x (fps, 3 ball queries, knn, 256 MiB copy) done", flush=True)
 
 
 def main() -> None:
@@ -278,13 +408,20 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-clouds", type=int, default=32)
+    parser.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                        help="workload; the headline metric (and the default) is c2")
+    parser.add_argument("--probe", action="store_true",
+                        help="run each config-2 kernel 3 times (for rocprofv3 counter passes)")
     args = parser.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; every workload here runs on one "
                           "GPU (batch sharding across GPUs is described in DESIGN.md)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
-    result = run(args)
+    if args.probe:
+        probe()
+        return
+    result = run(args) if args.config == "c2" else run_other(args)
     print(json.dumps(result))
 
 
