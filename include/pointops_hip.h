@@ -35,7 +35,7 @@ int pointops_device_supported(int device);
 
 /* ------------------------------------------------------------------ FPS */
 
-/* Dense batched farthest point sampling.  Replaces ops.py:271-274
+/* Dense batched farthest point sampling.  Replaces ops.py:137-140
  * (`_library("fps").furthest_point_sample`, kernels/fps.metal:19-107).
  * xyz (B,N,3) f32 -> out (B,npoint) int64; ties go to the smaller index; once
  * every point is taken the rest repeat the first maximum (index 0).
@@ -48,7 +48,7 @@ hipError_t pointops_fps_dense(const float *xyz, int64_t *out, void *scratch, int
 
 /* Large single-cloud FPS (B = 1): one persistent cooperative launch over all
  * CUs with a per-step device-wide argmax.  Replaces the 2*(npoint-1)
- * dispatch loop of ops.py:253-270 (kernels/fps_multigroup.metal:10-133).
+ * dispatch loop of ops.py:119-136 (kernels/fps_multigroup.metal:10-133).
  * `workspace` must hold pointops_fps_large_workspace_bytes(N, npoint) bytes
  * and be zero-filled by the caller before every call. */
 size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint);
@@ -69,7 +69,7 @@ hipError_t pointops_fps_flat(const float *x, const int64_t *ptr, const int64_t *
 
 /* ------------------------------------------------------------------ kNN */
 
-/* Dense exact kNN, D = 3.  Replaces ops.py:329-333 (kernels/knn.metal:32-140).
+/* Dense exact kNN, D = 3.  Replaces ops.py:195-199 (kernels/knn.metal:32-140).
  * query (B,M,3), ref (B,N,3) -> dist (B,M,K) Euclidean, idx (B,M,K) int64,
  * sorted by (fl32 squared distance, index).  NaN distances never match;
  * unfilled slots are (inf, 4294967295).  1 <= K <= 256. */
@@ -77,14 +77,14 @@ hipError_t pointops_knn3(const float *query, const float *ref, float *dist, int6
                          int64_t B, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 /* Dense exact kNN in D dimensions (sequential per-dimension accumulation).
- * Replaces ops.py:334-338 (kernels/feature_knn.metal:133-164).  Non-finite
+ * Replaces ops.py:200-204 (kernels/feature_knn.metal:133-164).  Non-finite
  * queries and non-finite distances never match; unfilled slots are (inf, -1). */
 hipError_t pointops_knn_feat(const float *query, const float *ref, float *dist, int64_t *idx,
                              int64_t B, int64_t M, int64_t N, int64_t D, int64_t K,
                              hipStream_t stream);
 
 /* Flat (ragged) kNN, global x indices padded with -1, (Q,K).  Replaces
- * _flat_search_mps.py:192-203 (kernels/flat_search.metal:140-250 for D = 3,
+ * _flat_search_mps.py:96-107 (kernels/flat_search.metal:44-154 for D = 3,
  * kernels/feature_knn.metal:166-199 otherwise).  y (Q,D) queries, x (Nx,D)
  * references, ptr_y/ptr_x (batch+1,) segment offsets. */
 hipError_t pointops_knn_flat(const float *y, const float *x, const int64_t *ptr_y,
@@ -112,7 +112,7 @@ hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *poin
 /* Flat radius search (torch_cluster convention): first K global x indices
  * with squared distance < radius_sq, padded with -1, (Q,K); optional
  * exclusion of x index == y index before the cap.  Replaces
- * _flat_search_mps.py:230-242 (kernels/flat_search.metal:229-275). */
+ * _flat_search_mps.py:134-146 (kernels/flat_search.metal:229-275). */
 hipError_t pointops_radius_flat_f32(const float *y, const float *x, const int64_t *ptr_y,
                                     const int64_t *ptr_x, int64_t *out, int64_t Q,
                                     int64_t batch, int64_t K, float radius_sq,

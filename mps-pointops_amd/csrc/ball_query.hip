@@ -2,7 +2,7 @@
 //
 // One wave per query scans the candidate points in input order, 64 per block
 // (lane l <-> point base + l).  A hit is fl32((dx^2 + dy^2) + dz^2) < r2 with
-// the reference's separately rounded arithmetic (reference.py:96-134); NaN and
+// the reference's separately rounded arithmetic (reference.py:83-121); NaN and
 // overflowed distances never satisfy `<`.  The hits of a block take output
 // slots found + rank, where rank is the number of hit lanes below (ballot +
 // mbcnt), which keeps the first K hits in index order without atomics; the
@@ -10,7 +10,7 @@
 //
 //   dense: _ball_query_mps.py:122-166 / kernels/ball_query.metal:30-166
 //          (query/point lengths, (idx -1, dist2 0) padding, f32 or f16 input)
-//   flat:  _flat_search_mps.py:207-243 / kernels/flat_search.metal:171-275
+//   flat:  _flat_search_mps.py:111-147 / kernels/flat_search.metal:171-275
 //          (segments by ptr, global indices, -1 padding, optional exclusion of
 //          index == query index before the cap)
 #include <hip/hip_fp16.h>

@@ -1,6 +1,6 @@
 // Farthest point sampling for gfx950.
 //
-// Semantics (reference.py:40-71, kernels/fps.metal:19-107): sampling starts at
+// Semantics (reference.py:27-58, kernels/fps.metal:19-107): sampling starts at
 // `start`; each step takes the point whose running minimum squared distance
 // to the sampled set is largest, ties to the smaller index; points with
 // ((x*x + y*y) + z*z) < fl32(1e-3) are never picked when skip_near_origin is

@@ -1,5 +1,9 @@
 // Exact k-nearest-neighbour search for gfx950.
 //
+// Two designs.  Dense 3-D queries with K <= 32 use knn3_lane_kernel (one lane
+// per query, described with the kernel below).  Everything else (K up to 256,
+// D != 3, flat/ragged batches) uses the wave-per-query kernels:
+//
 // One wave per query.  Lane l scans reference j = 64*c + l of chunk c; the
 // current best K keys (squared distance, index) form a sorted list spread
 // over the wave: slot s lives in lane s % 64 of register s / 64 (K <= 256).
@@ -15,7 +19,7 @@
 //               unfilled slots are (inf, 2^32-1);
 //   dense D-dim kernels/feature_knn.metal:51-164: non-finite queries and
 //               distances never match, unfilled slots (inf, -1);
-//   flat        kernels/flat_search.metal:140-250 and feature_knn.metal:166-199:
+//   flat        kernels/flat_search.metal:44-154 and feature_knn.metal:166-199:
 //               segment by binary search on ptr_y, global indices, -1 padding.
 #include "pointops_common.hpp"
 #include "pointops_hip.h"

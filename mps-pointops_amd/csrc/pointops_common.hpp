@@ -4,7 +4,7 @@
 // each float expression below is one IEEE binary32 operation rounded to
 // nearest-even in the written order; denormals are preserved (no FTZ).  The
 // squared distance is therefore bit-identical to the reference's separately
-// rounded tensor ops ((dx*dx + dy*dy) + dz*dz), reference.py:34-37.
+// rounded tensor ops ((dx*dx + dy*dy) + dz*dz), reference.py:21-24.
 #pragma once
 
 #include <hip/hip_runtime.h>

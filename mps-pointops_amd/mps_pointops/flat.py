@@ -221,7 +221,7 @@ def _edges(indices: Tensor) -> Tensor:
 
 
 def _torch_cluster_radius_sq(r: float) -> float:
-    """fl32(r * r) with r * r in double (_flat_search_mps.py:162-172)."""
+    """fl32(r * r) with r * r in double (_flat_search_mps.py:66-76)."""
     try:
         return struct.unpack("f", struct.pack("f", r * r))[0]
     except OverflowError:
@@ -242,7 +242,7 @@ def knn_indices(x: Tensor, y: Tensor, ptr_x: Tensor, ptr_y: Tensor, k: int) -> T
 def radius_indices(x: Tensor, y: Tensor, ptr_x: Tensor, ptr_y: Tensor, r: float,
                    max_num_neighbors: int, ignore_same_index: bool = False) -> Tensor:
     """First valid global x indices per query, -1 padded
-    (_flat_search_mps.py:207-243)."""
+    (_flat_search_mps.py:111-147)."""
     if x.dtype not in (torch.float32, torch.float16) or y.dtype != x.dtype:
         raise TypeError("flat radius requires matching float32 or float16 x and y")
     radius_f32, _ = _checked_radius_and_k(r, max_num_neighbors)

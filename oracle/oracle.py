@@ -107,7 +107,7 @@ def ball_radius_sq(radius: float) -> float:
 
 
 def torch_cluster_radius_sq(radius: float) -> float:
-    """fl32(r * r in double), _flat_search_mps.py:162-172 (inf on overflow)."""
+    """fl32(r * r in double), _flat_search_mps.py:66-76 (inf on overflow)."""
     with np.errstate(over="ignore"):
         return float(np.float32(float(radius) * float(radius)))
 

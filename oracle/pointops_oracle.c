@@ -25,7 +25,7 @@
 
 #define PAD_UINT32_AS_I64 4294967295LL
 
-/* ((dx*dx + dy*dy) + dz*dz) with d = a - b: reference.py:34-37 (_sqdist). */
+/* ((dx*dx + dy*dy) + dz*dz) with d = a - b: reference.py:21-24 (_sqdist). */
 static inline float sqdist3(const float *a, const float *b) {
     float dx = a[0] - b[0];
     float dy = a[1] - b[1];
@@ -51,8 +51,8 @@ static inline int before(float d, int64_t i, float e, int64_t j) {
 /* ------------------------------------------------------------------ FPS */
 
 /*
- * reference.py:40-71 (furthest_point_sample).  For each cloud:
- *   min_d2 = +inf; skipped points (mag < fl32(1e-3), reference.py:59-63) = -inf
+ * reference.py:27-58 (furthest_point_sample).  For each cloud:
+ *   min_d2 = +inf; skipped points (mag < fl32(1e-3), reference.py:46-50) = -inf
  *   farthest = start
  *   for i: idx[i] = farthest
  *          min_d2 = minimum(min_d2, sqdist(xyz, xyz[farthest]))
@@ -194,7 +194,7 @@ static inline void topk_insert(float *ld, int64_t *li, int64_t k, float d, int64
 
 /*
  * Dense 3-D exact kNN with the reference kernel's semantics
- * (kernels/knn.metal:32-140, ops.py:278-339; exact oracle tests/test_knn.py:15-23):
+ * (kernels/knn.metal:32-140, ops.py:144-205; exact oracle tests/test_knn.py:15-23):
  * key (fl32 ((dx^2+dy^2)+dz^2) with d = ref - query, index); the k smallest
  * keys ascending; a NaN distance is never a candidate; unfilled slots keep
  * (inf, 2^32-1).  dist = sqrt(d2).
@@ -246,7 +246,7 @@ static int all_finite(const float *v, int64_t n) {
 }
 
 /*
- * Dense D-dim exact kNN (ops.py:335-338 -> kernels/feature_knn.metal:133-164;
+ * Dense D-dim exact kNN (ops.py:200-204 -> kernels/feature_knn.metal:133-164;
  * oracle tests/test_feature_knn.py:16-35): non-finite queries and non-finite
  * distances never match; unfilled slots are (inf, -1).
  */
@@ -327,11 +327,11 @@ void oracle_knn_flat(const float *y, const float *x, const int64_t *ptr_y,
 /* ------------------------------------------------------------ ball query */
 
 /*
- * Dense first-K ball query, reference.py:96-134: hits are the first K points
+ * Dense first-K ball query, reference.py:83-121: hits are the first K points
  * j (input order) with fl32((dx^2+dy^2)+dz^2) < r2 (strict), d = query - ref,
  * r2 = fl32(fl32(r) * fl32(r)) (_ball_query_mps.py:87-119).  Empty slots are
  * (d2 0, idx -1).  Lengths follow _ball_query_mps.py:73-84 / the native
- * kernel (kernels/ball_query.metal:262-275): queries at or beyond
+ * kernel (kernels/ball_query.metal:64-75): queries at or beyond
  * query_lengths[b] are all padding, only points below point_lengths[b] are
  * scanned.  NaN never satisfies `<`, so non-finite coordinates never match.
  */
@@ -364,9 +364,9 @@ void oracle_ball_query(const float *q, const float *p, const int64_t *qlen,
 /*
  * Flat radius search (torch_cluster convention), (Q, K) global indices padded
  * with -1: flat.py:264-288 (_reference_search with radius; d = refs - query),
- * threshold r2 = fl32(r*r computed in double) (_flat_search_mps.py:162-172),
- * optional exclusion of j == q before the cap (_flat_search_mps.py:207-216),
- * r == 0 returns no neighbours (_flat_search_mps.py:226-228).
+ * threshold r2 = fl32(r*r computed in double) (_flat_search_mps.py:66-76),
+ * optional exclusion of j == q before the cap (kernels/flat_search.metal:196-199),
+ * r == 0 returns no neighbours (_flat_search_mps.py:130-132).
  */
 void oracle_radius_flat(const float *y, const float *x, const int64_t *ptr_y,
                         const int64_t *ptr_x, int64_t Q, int64_t batch,

@@ -3,8 +3,8 @@ baseline that bench.py times beside the GPU (cpu_baseline.kind = "port").
 
 TEST INFRASTRUCTURE ONLY: the shipped package never imports this module.
 Each function restates /root/reference/mps_pointops/reference.py:
-furthest_point_sample (:40-71), knn (:74-93, cdist + topk, the reference's
-own CPU kNN) and ball_query (:96-134, chunks of at most 2**24 pairs).
+furthest_point_sample (:27-58), knn (:61-80, cdist + topk, the reference's
+own CPU kNN) and ball_query (:83-121, chunks of at most 2**24 pairs).
 """
 
 from __future__ import annotations

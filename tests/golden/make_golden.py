@@ -71,7 +71,7 @@ def known_answers() -> list[dict]:
         xyz=[[[0, 0, 0]] * 50], npoint=5, start_idx=0, skip=True, expect=[[0, 0, 0, 0, 0]])
     # Hand derivation: 3 points on a line; from start 1 the farthest is 2
     # (d2 4 vs 1), then 0; exhausted -> 0.
-    add(op="fps", name="start_idx_line", source="derived (reference.py:64-70)",
+    add(op="fps", name="start_idx_line", source="derived (reference.py:51-57)",
         xyz=[[[0, 0, 0], [1, 0, 0], [3, 0, 0]]], npoint=4, start_idx=1, skip=False,
         expect=[[1, 2, 0, 0]])
     add(op="fps_flat", name="flat_global_indices", source="tests/test_flat.py:20-23",
@@ -209,11 +209,11 @@ def known_answers() -> list[dict]:
         query=[[[0, 0, 0], [50, 50, 50]]], ref=[[[5.0, 0, 0], [0.1, 0, 0], [9, 9, 9], [0.2, 0, 0]]],
         radius=0.5, k=4, expect_idx=[[[1, 3, -1, -1], [-1, -1, -1, -1]]], expect_dist=None,
         compat=[[[1, 3, 1, 1], [0, 0, 0, 0]]])
-    # reference.py:115-121 with r = 1e20: r2 = fl32(1e40) = inf, so every
+    # reference.py:102-121 with r = 1e20: r2 = fl32(1e40) = inf, so every
     # finite d2 is a hit and an overflowed d2 (5e19^2) is not: [[0, -1, -1]].
     # (The reference's Metal kernel takes a normalised path here and also
     # accepts index 1; this build follows reference.py.)
-    add(op="ball_query", name="huge_radius_overflow", source="reference.py:96-134 (r2 = inf)",
+    add(op="ball_query", name="huge_radius_overflow", source="reference.py:83-121 (r2 = inf)",
         query=[[[0, 0, 0]]], ref=[[[1e19, 0, 0], [5e19, 0, 0], [2e20, 0, 0]]], radius=1e20, k=3,
         expect_idx=[[[0, -1, -1]]], expect_dist=None)
     add(op="ball_query", name="zero_radius", source="tests/test_ball_query_api.py:53-57",

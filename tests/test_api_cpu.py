@@ -304,7 +304,7 @@ def test_bench_rejects_multi_gpu():
 def test_torch_port_matches_oracle():
     """The CPU baseline port restates reference.py: FPS and ball query agree
     with the oracle bit for bit; cdist+topk kNN agrees on distances to
-    tolerance (reference.py:74-93 is not exact by design)."""
+    tolerance (reference.py:61-80 is not exact by design)."""
     from oracle import torch_port
 
     g = torch.Generator().manual_seed(0)
