@@ -23,6 +23,7 @@ namespace {
 
 constexpr int kBqThreads = 256;
 constexpr int kBqWaves = kBqThreads / kWave;
+constexpr int kBqDepth = 8;  // 64-point blocks in flight per wave (even)
 
 template <typename S>
 __device__ __forceinline__ float widen(S v);
@@ -55,28 +56,46 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
         const S* qp = queries + 3 * row;
         const float qx = widen(qp[0]), qy = widen(qp[1]), qz = widen(qp[2]);
         const S* pp = points + 3 * b * P;
-        for (int base = 0; base < n; base += kWave) {
-            const int j = base + lane;
-            bool hit = false;
-            float d = 0.f;
-            if (j < n) {
-                const S* pt = pp + 3 * static_cast<int64_t>(j);
-                d = sqdist3(qx, qy, qz, widen(pt[0]), widen(pt[1]), widen(pt[2]));
-                hit = d < r2;
+        // kBqDepth blocks of 64 points are loaded before the first is tested,
+        // so one L2 round trip covers kBqDepth * 64 points.
+        for (int base = 0; base < n && found < K; base += kBqDepth * kWave) {
+            float vx[kBqDepth], vy[kBqDepth], vz[kBqDepth];
+#pragma unroll
+            for (int c = 0; c < kBqDepth; ++c) {
+                const int j = base + c * kWave + lane;
+                vx[c] = vy[c] = vz[c] = 0.f;
+                if (j < n) {
+                    const S* pt = pp + 3 * static_cast<int64_t>(j);
+                    vx[c] = widen(pt[0]);
+                    vy[c] = widen(pt[1]);
+                    vz[c] = widen(pt[2]);
+                }
             }
-            const uint64_t mask = ballot(hit);
-            if (mask == 0) continue;
-            const int slot = found + lanes_below(mask);
-            if (hit && slot < K) {
-                oi[slot] = j;
-                od[slot] = d;
-            }
-            found += __popcll(mask);
-            if (found >= K) {
-                found = K;
-                break;
+#pragma unroll
+            for (int c = 0; c < kBqDepth; c += 2) {
+                // Two blocks per round: straight-line tests, one branch.
+                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
+                const float d0 = sqdist3(qx, qy, qz, vx[c], vy[c], vz[c]);
+                const float d1 = sqdist3(qx, qy, qz, vx[c + 1], vy[c + 1], vz[c + 1]);
+                const bool h0 = j0 < n && d0 < r2;
+                const bool h1 = j1 < n && d1 < r2;
+                const uint64_t m0 = ballot(h0), m1 = ballot(h1);
+                if ((m0 | m1) == 0) continue;
+                const int s0 = found + lanes_below(m0);
+                const int s1 = found + __popcll(m0) + lanes_below(m1);
+                if (h0 && s0 < K) {
+                    oi[s0] = j0;
+                    od[s0] = d0;
+                }
+                if (h1 && s1 < K) {
+                    oi[s1] = j1;
+                    od[s1] = d1;
+                }
+                found += __popcll(m0) + __popcll(m1);
+                if (found >= K) break;
             }
         }
+        found = min(found, K);
     }
     for (int s = found + lane; s < K; s += kWave) {
         oi[s] = -1;
@@ -109,24 +128,34 @@ __global__ __launch_bounds__(kBqThreads) void radius_flat_kernel(
     int found = 0;
     if (r2 > 0.f) {
         const float qx = widen(y[3 * q]), qy = widen(y[3 * q + 1]), qz = widen(y[3 * q + 2]);
-        for (int64_t base = lo; base < hi; base += kWave) {
-            const int64_t j = base + lane;
-            bool hit = false;
-            if (j < hi && !(ignore_same_index && j == q)) {
-                const S* pt = x + 3 * j;
-                const float d = sqdist3(widen(pt[0]), widen(pt[1]), widen(pt[2]), qx, qy, qz);
-                hit = d < r2;
+        for (int64_t base = lo; base < hi && found < K; base += kBqDepth * kWave) {
+            float vx[kBqDepth], vy[kBqDepth], vz[kBqDepth];
+#pragma unroll
+            for (int c = 0; c < kBqDepth; ++c) {
+                const int64_t j = base + c * kWave + lane;
+                vx[c] = vy[c] = vz[c] = 0.f;
+                if (j < hi) {
+                    const S* pt = x + 3 * j;
+                    vx[c] = widen(pt[0]);
+                    vy[c] = widen(pt[1]);
+                    vz[c] = widen(pt[2]);
+                }
             }
-            const uint64_t mask = ballot(hit);
-            if (mask == 0) continue;
-            const int slot = found + lanes_below(mask);
-            if (hit && slot < K) o[slot] = j;
-            found += __popcll(mask);
-            if (found >= K) {
-                found = K;
-                break;
+#pragma unroll
+            for (int c = 0; c < kBqDepth; ++c) {
+                const int64_t j = base + c * kWave + lane;
+                bool hit = false;
+                if (j < hi && !(ignore_same_index && j == q))
+                    hit = sqdist3(vx[c], vy[c], vz[c], qx, qy, qz) < r2;
+                const uint64_t mask = ballot(hit);
+                if (mask == 0) continue;
+                const int slot = found + lanes_below(mask);
+                if (hit && slot < K) o[slot] = j;
+                found += __popcll(mask);
+                if (found >= K) break;
             }
         }
+        found = min(found, K);
     }
     for (int s = found + lane; s < K; s += kWave) o[s] = -1;
 }
@@ -135,7 +164,7 @@ template <typename S>
 hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t* pl, int64_t* idx,
                        float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K, float r2,
                        hipStream_t stream) {
-    if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kWave)
+    if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kBqDepth * kWave)
         return hipErrorInvalidValue;
     if (B == 0 || Q == 0 || K == 0) return hipSuccess;
     const int64_t blocks = (B * Q + kBqWaves - 1) / kBqWaves;
