@@ -227,36 +227,47 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
 }
 
 // ------------------------------------------------------------ large cloud
-
-// Per-step record published by each workgroup: four 64-bit words written with
-// agent-scope atomic stores, each carrying the step tag so that a reader can
-// tell a complete record of this step from a stale one two steps back
-// (records are double-buffered by step parity).
+//
+// fps_large_kernel<P>: one cloud over G <= 256 co-resident workgroups (one per
+// CU), cooperative launch.  Workgroup g owns points [g*chunk, g*chunk+chunk);
+// thread t holds P consecutive ones in VGPRs (and the chunk is copied to LDS
+// for coordinate lookups), so the local argmax is the register tree + DPP max
+// of fps_regs_kernel.  Per step the local winner is published as a record of
+// four 64-bit words written with agent-scope atomic stores, each carrying the
+// step tag so that a reader can tell a complete record of this step from a
+// stale one two steps back (records are double-buffered by step parity):
 //   w0 = vkey << 32 | tag << 21 | (~idx & 0x1FFFFF)
 //   w1 = x_bits << 32 | tag,  w2 = y_bits << 32 | tag,  w3 = z_bits << 32 | tag
 // vkey = 0 when the workgroup has no candidate, else float bits + 1 (running
-// distances are >= +0 for candidates, so the bits order like the values).
+// distances are >= +0 for candidates, so the bits order like the values and
+// the largest (vkey, ~idx) is the largest value with the smallest index).
+// Thread t of every workgroup polls record t (one poll round trip), the wave
+// reduces the keys with two 32-bit DPP maxima, and a barrier combines the four
+// waves.  Polls are bounded: after kSpinLimit attempts (or when another
+// workgroup has given up) the kernel raises a status word and every workgroup
+// returns, so no launch can hang.
 constexpr int kLargeIdxBits = 21;
 constexpr uint32_t kLargeIdxMask = (1u << kLargeIdxBits) - 1u;
 constexpr int64_t kLargeMaxN = int64_t(1) << kLargeIdxBits;
 constexpr uint32_t kSpinLimit = 1u << 22;
+constexpr int kLargeThreads = 256;
+constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread
 
 __device__ __forceinline__ uint32_t step_tag(int64_t step) {
     return (static_cast<uint32_t>(step >> 1) & 0x3FFu) | 0x400u;  // never 0
 }
 
-template <int P, int T>
-__global__ __launch_bounds__(T) void fps_large_kernel(const float* __restrict__ xyz,
-                                                      int64_t* __restrict__ out,
-                                                      uint64_t* __restrict__ records,
-                                                      uint32_t* __restrict__ status, int N,
-                                                      int64_t npoint, int start, int skip,
-                                                      int chunk) {
+template <int P>
+__global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
+    const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
+    uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk) {
+    constexpr int T = kLargeThreads;
     constexpr int NW = T / kWave;
+    constexpr int kNegInf = static_cast<int>(0xFF800000u);
+    __shared__ float4 spts[P * T];
     __shared__ int2 slots[2][NW];
-    __shared__ uint64_t red_key[NW];
-    __shared__ int red_src[NW];
-    __shared__ float4 centroid;
+    __shared__ uint64_t red_key[2][NW];
+    __shared__ float4 red_xyz[2][NW];
     __shared__ int abort_flag;
 
     const int G = gridDim.x;
@@ -271,19 +282,21 @@ __global__ __launch_bounds__(T) void fps_large_kernel(const float* __restrict__ 
     float px[P], py[P], pz[P], md[P];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-        const int j = tid + k * T;
+        const int j = tid * P + k;
         if (j < n) {
             const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
             px[k] = x;
             py[k] = y;
             pz[k] = z;
             md[k] = (skip && near_origin(x, y, z)) ? -INFINITY : INFINITY;
+            spts[j] = make_float4(x, y, z, 0.f);
         } else {
             px[k] = py[k] = pz[k] = 0.f;
             md[k] = -INFINITY;
         }
     }
     if (tid == 0) abort_flag = 0;
+    __syncthreads();
 
     int far = start;
     float cx = xyz[3 * static_cast<int64_t>(far)];
@@ -292,146 +305,128 @@ __global__ __launch_bounds__(T) void fps_large_kernel(const float* __restrict__ 
     for (int64_t step = 0; step < npoint; ++step) {
         if (g == 0 && tid == 0) out[step] = far;
         if (step + 1 == npoint) break;
+        const int par = static_cast<int>(step & 1);
 
-        // Local (value, index) argmax of this workgroup's chunk.
-        float bv = -INFINITY;
-        int bk = -1;
+        // Local argmax of this workgroup's chunk: first maximum in index order.
+        int v[P], s[P];
 #pragma unroll
         for (int k = 0; k < P; ++k) {
-            const float d = sqdist3(px[k], py[k], pz[k], cx, cy, cz);
-            const float m = fminf(md[k], d);
-            md[k] = m;
-            if (m > bv) {
-                bv = m;
-                bk = k;
+            md[k] = fminf(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
+            v[k] = f2i(md[k]);
+            s[k] = k;
+        }
+#pragma unroll
+        for (int w = 1; w < P; w <<= 1) {
+#pragma unroll
+            for (int k = 0; k + w < P; k += 2 * w) {
+                const int right = -static_cast<int>(v[k + w] > v[k]);
+                v[k] = max(v[k], v[k + w]);
+                s[k] ^= (s[k] ^ s[k + w]) & right;
             }
         }
-        const int bi = bk < 0 ? INT_MAX : lo + tid + bk * T;
-        const float wv = wave_max(bv);
-        const int wi = wave_min(bv == wv ? bi : INT_MAX);
-        int2* buf = slots[step & 1];
-        if (lane == 0) buf[wave] = make_int2(f2i(wv), wi);
+        const int wv = wave_max_i32(v[0]);
+        const int wl = static_cast<int>(__builtin_ctzll(ballot(v[0] == wv)));
+        const int wi = (wave * kWave + wl) * P + readlane(s[0], wl);
+        if (lane == 0) slots[par][wave] = make_int2(wv, wi);
         __syncthreads();
-        const int win = block_argmax<NW>(buf);
-        float winv = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NW; ++w)
-            if (buf[w].y == win) winv = i2f(buf[w].x);
 
-        // The owner of the local winner publishes the record.
+        // Thread 0 publishes this workgroup's record.
         const uint32_t tag = step_tag(step);
-        uint64_t* rec = records + ((step & 1) * static_cast<int64_t>(G) + g) * 4;
-        const int owner = (win == INT_MAX) ? 0 : ((win - lo) % T);
-        if (tid == owner) {
-            uint32_t vkey = 0;
-            float wx = 0.f, wy = 0.f, wz = 0.f;
-            if (win != INT_MAX) {
-                vkey = static_cast<uint32_t>(f2i(winv)) + 1u;
-                const int kk = (win - lo) / T;
+        uint64_t* base = records + static_cast<int64_t>(par) * G * 4;
+        if (tid == 0) {
+            int bv = slots[par][0].x, bi = slots[par][0].y;
 #pragma unroll
-                for (int k = 0; k < P; ++k) {
-                    if (k == kk) {
-                        wx = px[k];
-                        wy = py[k];
-                        wz = pz[k];
-                    }
+            for (int w = 1; w < NW; ++w) {
+                if (slots[par][w].x > bv) {
+                    bv = slots[par][w].x;
+                    bi = slots[par][w].y;
                 }
             }
-            const uint64_t w0 = (static_cast<uint64_t>(vkey) << 32) |
-                                (static_cast<uint64_t>(tag) << kLargeIdxBits) |
-                                (~static_cast<uint32_t>(win) & kLargeIdxMask);
-            __hip_atomic_store(rec + 1, (static_cast<uint64_t>(f2i(wx)) << 32) | tag,
+            uint32_t vkey = 0;
+            float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (bv != kNegInf) {
+                vkey = static_cast<uint32_t>(bv) + 1u;
+                c = spts[bi];
+            }
+            const uint32_t gidx = static_cast<uint32_t>(lo + bi);
+            uint64_t* rec = base + 4 * g;
+            __hip_atomic_store(rec + 1, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.x))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 2, (static_cast<uint64_t>(f2i(wy)) << 32) | tag,
+            __hip_atomic_store(rec + 2, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.y))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 3, (static_cast<uint64_t>(f2i(wz)) << 32) | tag,
+            __hip_atomic_store(rec + 3, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.z))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 0, w0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(rec + 0,
+                               (static_cast<uint64_t>(vkey) << 32) |
+                                   (static_cast<uint64_t>(tag) << kLargeIdxBits) |
+                                   (~gidx & kLargeIdxMask),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 
-        // Poll every workgroup's record of this step (thread t reads records
-        // t, t+T, ...), keep the best complete one.
-        uint64_t best = 0;
-        int best_src = -1;
-        const uint64_t* base = records + (step & 1) * static_cast<int64_t>(G) * 4;
-        for (int r = tid; r < G; r += T) {
-            const uint64_t* q = base + 4 * r;
-            uint32_t spins = 0;
-            uint64_t w0, w1, w2, w3;
-            while (true) {
-                w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const bool ready = ((w0 >> kLargeIdxBits) & 0x7FFu) == tag &&
-                                   static_cast<uint32_t>(w1) == tag &&
-                                   static_cast<uint32_t>(w2) == tag &&
-                                   static_cast<uint32_t>(w3) == tag;
-                if (ready) break;
-                if (++spins > kSpinLimit || __hip_atomic_load(status, __ATOMIC_RELAXED,
-                                                              __HIP_MEMORY_SCOPE_AGENT)) {
+        // Thread t polls record t until all four words carry this step's tag.
+        uint32_t khi = 0, klo = 0;
+        int rx = 0, ry = 0, rz = 0;
+        if (tid < G) {
+            const uint64_t* q = base + 4 * tid;
+            for (uint32_t spins = 0;; ++spins) {
+                const uint64_t w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const uint64_t w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (((w0 >> kLargeIdxBits) & 0x7FFu) == tag && static_cast<uint32_t>(w1) == tag &&
+                    static_cast<uint32_t>(w2) == tag && static_cast<uint32_t>(w3) == tag) {
+                    khi = static_cast<uint32_t>(w0 >> 32);
+                    klo = static_cast<uint32_t>(w0) & kLargeIdxMask;
+                    rx = static_cast<int>(w1 >> 32);
+                    ry = static_cast<int>(w2 >> 32);
+                    rz = static_cast<int>(w3 >> 32);
+                    break;
+                }
+                if (spins >= kSpinLimit ||
+                    ((spins & 63u) == 63u &&
+                     __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
                     __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     abort_flag = 1;
                     break;
                 }
                 __builtin_amdgcn_s_sleep(1);
             }
-            // Order: vkey, then ~idx (tag bits are equal for every record).
-            const uint64_t key = (w0 & 0xFFFFFFFF00000000ull) | (w0 & kLargeIdxMask);
-            if (best_src < 0 || key > best) {
-                best = key;
-                best_src = r;
-            }
-            (void)w1;
-            (void)w2;
-            (void)w3;
         }
-        // Wave reduction of (key, src) with shuffles (one per step), then a
-        // block reduction through LDS.
-        uint64_t k64 = best_src < 0 ? 0 : best;
-        int s64 = best_src;
-        for (int off = 32; off >= 1; off >>= 1) {
-            const uint64_t ok = __shfl_xor(k64, off);
-            const int os = __shfl_xor(s64, off);
-            if (os >= 0 && (s64 < 0 || ok > k64)) {
-                k64 = ok;
-                s64 = os;
-            }
-        }
+        // Wave maximum of (khi, klo): khi <= 0x7F800001 and klo < 2^21, so both
+        // compare correctly as signed ints.
+        const int hmax = wave_max_i32(static_cast<int>(khi));
+        const int lmax = wave_max_i32(static_cast<int>(khi) == hmax ? static_cast<int>(klo) : -1);
+        const int rl = static_cast<int>(__builtin_ctzll(
+            ballot(static_cast<int>(khi) == hmax && static_cast<int>(klo) == lmax)));
         if (lane == 0) {
-            red_key[wave] = k64;
-            red_src[wave] = s64;
+            red_key[par][wave] = (static_cast<uint64_t>(static_cast<uint32_t>(hmax)) << 32) |
+                                 static_cast<uint32_t>(lmax);
+            red_xyz[par][wave] = make_float4(i2f(readlane(rx, rl)), i2f(readlane(ry, rl)),
+                                             i2f(readlane(rz, rl)), 0.f);
         }
         __syncthreads();
-        if (abort_flag) return;  // uniform: read after the barrier
-        uint64_t gk = red_key[0];
-        int gs = red_src[0];
+        if (abort_flag) return;  // uniform: written before the barrier
+        int bw = 0;
+        uint64_t best = red_key[par][0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
-            if (red_src[w] >= 0 && (gs < 0 || red_key[w] > gk)) {
-                gk = red_key[w];
-                gs = red_src[w];
+            if (red_key[par][w] > best) {
+                best = red_key[par][w];
+                bw = w;
             }
         }
-        const uint32_t vk = static_cast<uint32_t>(gk >> 32);
-        const int idx = static_cast<int>(~static_cast<uint32_t>(gk) & kLargeIdxMask);
-        far = (vk == 0) ? 0 : idx;
-        if (tid == 0) {
-            if (vk == 0) {
-                centroid = make_float4(xyz[0], xyz[1], xyz[2], 0.f);
-            } else {
-                const uint64_t* q = base + 4 * gs;
-                const uint64_t w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                centroid = make_float4(i2f(static_cast<int>(w1 >> 32)), i2f(static_cast<int>(w2 >> 32)),
-                                       i2f(static_cast<int>(w3 >> 32)), 0.f);
-            }
+        if ((best >> 32) == 0) {  // nothing can be picked: index 0, like the reference
+            far = 0;
+            cx = xyz[0];
+            cy = xyz[1];
+            cz = xyz[2];
+        } else {
+            far = static_cast<int>(~static_cast<uint32_t>(best) & kLargeIdxMask);
+            const float4 c = red_xyz[par][bw];
+            cx = c.x;
+            cy = c.y;
+            cz = c.z;
         }
-        __syncthreads();
-        cx = centroid.x;
-        cy = centroid.y;
-        cz = centroid.z;
     }
 }
 
@@ -472,30 +467,27 @@ hipError_t launch_fps(const float* xyz, const int64_t* ptr, const int64_t* out_p
     return hipGetLastError();
 }
 
-constexpr int kLargeThreads = 256;
-
 template <int P>
 hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint32_t* status,
                         int N, int64_t npoint, int start, int skip, int chunk, int grid,
                         hipStream_t stream) {
     void* args[] = {(void*)&xyz, (void*)&out, (void*)&records, (void*)&status, (void*)&N,
                     (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk};
-    return hipLaunchCooperativeKernel(
-        reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>), dim3(grid),
-        dim3(kLargeThreads), args, 0, stream);
+    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&fps_large_kernel<P>),
+                                      dim3(grid), dim3(kLargeThreads), args, 0, stream);
 }
 
 template <int P>
 int large_capacity(int device) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>),
-            kLargeThreads, 0) != hipSuccess)
+            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P>), kLargeThreads, 0) !=
+        hipSuccess)
         return 0;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
         return 0;
-    return per_cu * cus;
+    return min(per_cu, 1) * cus;  // at most one workgroup per CU
 }
 
 }  // namespace
@@ -542,8 +534,7 @@ size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
     // status word (padded to 256 B) + 2 parities x grid x 4 words
-    const int64_t max_grid = 4096;
-    return 256 + static_cast<size_t>(2 * max_grid * 4) * sizeof(uint64_t);
+    return 256 + static_cast<size_t>(2 * kLargeMaxGrid * 4) * sizeof(uint64_t);
 }
 
 hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,
@@ -556,28 +547,33 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
     int device = 0;
     hipError_t err = hipGetDevice(&device);
     if (err != hipSuccess) return err;
-    // Choose points per thread so that the cloud fits the co-resident grid.
-    const int choices[] = {4, 8, 16, 32};
+    // Smallest P (points per thread) whose grid fits one workgroup per CU
+    // and one polled record per thread.
+    auto* status = static_cast<uint32_t*>(workspace);
+    auto* records = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + 256);
+    const int n32 = static_cast<int>(N);
+    const int s32 = static_cast<int>(start_idx);
+    const int skip = skip_near_origin ? 1 : 0;
+    const int choices[] = {1, 2, 4, 8, 16, 32};
     for (int P : choices) {
         int cap = 0;
         switch (P) {
+            case 1: cap = large_capacity<1>(device); break;
+            case 2: cap = large_capacity<2>(device); break;
             case 4: cap = large_capacity<4>(device); break;
             case 8: cap = large_capacity<8>(device); break;
             case 16: cap = large_capacity<16>(device); break;
             default: cap = large_capacity<32>(device); break;
         }
-        cap = cap < 4096 ? cap : 4096;
+        cap = min(cap, kLargeMaxGrid);
         const int64_t per_block = static_cast<int64_t>(P) * kLargeThreads;
         const int64_t need = (N + per_block - 1) / per_block;
         if (cap <= 0 || need > cap) continue;
         const int grid = static_cast<int>(need);
         const int chunk = static_cast<int>(per_block);
-        auto* status = static_cast<uint32_t*>(workspace);
-        auto* records = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + 256);
-        const int n32 = static_cast<int>(N);
-        const int s32 = static_cast<int>(start_idx);
-        const int skip = skip_near_origin ? 1 : 0;
         switch (P) {
+            case 1: return launch_large<1>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
+            case 2: return launch_large<2>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
             case 4: return launch_large<4>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
             case 8: return launch_large<8>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
             case 16: return launch_large<16>(xyz, out, records, status, n32, npoint, s32, skip, chunk, grid, stream);
