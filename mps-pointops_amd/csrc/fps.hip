@@ -117,18 +117,29 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
     float md[P];  // running distances
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-        const int j = tid * P + k;
-        if (j < n) {
-            const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
-            px[k] = x;
-            py[k] = y;
-            pz[k] = z;
-            md[k] = (skip && near_origin(x, y, z)) ? -INFINITY : INFINITY;
-            spts[j] = make_float4(x, y, z, 0.f);
-        } else {
-            px[k] = py[k] = pz[k] = 0.f;
-            md[k] = -INFINITY;  // never a candidate
+        px[k] = py[k] = pz[k] = 0.f;
+    }
+    if (n > 0) {
+        // Loads are clamped into the cloud (not skipped) so that all P of
+        // them are in flight at once; padding slots are masked below.
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int jj = min(tid * P + k, n - 1);
+            px[k] = p[3 * jj];
+            py[k] = p[3 * jj + 1];
+            pz[k] = p[3 * jj + 2];
         }
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid * P + k;
+        const bool valid = j < n;
+        px[k] = valid ? px[k] : 0.f;
+        py[k] = valid ? py[k] : 0.f;
+        pz[k] = valid ? pz[k] : 0.f;
+        md[k] = !valid ? -INFINITY
+                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+        if (valid) spts[j] = make_float4(px[k], py[k], pz[k], 0.f);
     }
     __syncthreads();
 
@@ -257,6 +268,46 @@ __device__ __forceinline__ uint32_t step_tag(int64_t step) {
     return (static_cast<uint32_t>(step >> 1) & 0x3FFu) | 0x400u;  // never 0
 }
 
+struct RecordPoll {
+    uint64_t w0, w1, w2, w3;
+};
+
+// One agent-scope read of the four words of a record (structure of arrays).
+__device__ __forceinline__ RecordPoll poll_record(const uint64_t* q) {
+    RecordPoll r;
+    r.w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r.w1 = __hip_atomic_load(q + 1 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r.w2 = __hip_atomic_load(q + 2 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    r.w3 = __hip_atomic_load(q + 3 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return r;
+}
+
+__device__ __forceinline__ bool record_ready(const RecordPoll& r, uint32_t tag) {
+    return ((r.w0 >> kLargeIdxBits) & 0x7FFu) == tag && static_cast<uint32_t>(r.w1) == tag &&
+           static_cast<uint32_t>(r.w2) == tag && static_cast<uint32_t>(r.w3) == tag;
+}
+
+__device__ __forceinline__ void take_record(const RecordPoll& r, uint32_t& khi, uint32_t& klo,
+                                            int& rx, int& ry, int& rz) {
+    khi = static_cast<uint32_t>(r.w0 >> 32);
+    klo = static_cast<uint32_t>(r.w0) & kLargeIdxMask;
+    rx = static_cast<int>(r.w1 >> 32);
+    ry = static_cast<int>(r.w2 >> 32);
+    rz = static_cast<int>(r.w3 >> 32);
+}
+
+// True when this poller must stop: too many polls, or another workgroup has
+// already given up (checked every 64 polls).  Raises the shared status word.
+__device__ __forceinline__ bool poll_give_up(uint32_t* status, uint32_t spins) {
+    if (spins >= kSpinLimit ||
+        ((spins & 63u) == 63u &&
+         __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
+        __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        return true;
+    }
+    return false;
+}
+
 template <int P>
 __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
     const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
@@ -282,18 +333,29 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
     float px[P], py[P], pz[P], md[P];
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-        const int j = tid * P + k;
-        if (j < n) {
-            const float x = p[3 * j], y = p[3 * j + 1], z = p[3 * j + 2];
-            px[k] = x;
-            py[k] = y;
-            pz[k] = z;
-            md[k] = (skip && near_origin(x, y, z)) ? -INFINITY : INFINITY;
-            spts[j] = make_float4(x, y, z, 0.f);
-        } else {
-            px[k] = py[k] = pz[k] = 0.f;
-            md[k] = -INFINITY;
+        px[k] = py[k] = pz[k] = 0.f;
+    }
+    if (n > 0) {
+        // Loads are clamped into the cloud (not skipped) so that all P of
+        // them are in flight at once; padding slots are masked below.
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int jj = min(tid * P + k, n - 1);
+            px[k] = p[3 * jj];
+            py[k] = p[3 * jj + 1];
+            pz[k] = p[3 * jj + 2];
         }
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid * P + k;
+        const bool valid = j < n;
+        px[k] = valid ? px[k] : 0.f;
+        py[k] = valid ? py[k] : 0.f;
+        pz[k] = valid ? pz[k] : 0.f;
+        md[k] = !valid ? -INFINITY
+                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+        if (valid) spts[j] = make_float4(px[k], py[k], pz[k], 0.f);
     }
     if (tid == 0) abort_flag = 0;
     __syncthreads();
@@ -330,9 +392,11 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
         if (lane == 0) slots[par][wave] = make_int2(wv, wi);
         __syncthreads();
 
-        // Thread 0 publishes this workgroup's record.
+        // Thread 0 publishes this workgroup's record.  Word w of record g is
+        // base[w * kLargeMaxGrid + g], so a wave's poll of 64 records reads
+        // four contiguous 512-byte runs.
         const uint32_t tag = step_tag(step);
-        uint64_t* base = records + static_cast<int64_t>(par) * G * 4;
+        uint64_t* base = records + static_cast<int64_t>(par) * 4 * kLargeMaxGrid;
         if (tid == 0) {
             int bv = slots[par][0].x, bi = slots[par][0].y;
 #pragma unroll
@@ -349,12 +413,12 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
                 c = spts[bi];
             }
             const uint32_t gidx = static_cast<uint32_t>(lo + bi);
-            uint64_t* rec = base + 4 * g;
-            __hip_atomic_store(rec + 1, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.x))) << 32) | tag,
+            uint64_t* rec = base + g;
+            __hip_atomic_store(rec + 1 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.x))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 2, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.y))) << 32) | tag,
+            __hip_atomic_store(rec + 2 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.y))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 3, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.z))) << 32) | tag,
+            __hip_atomic_store(rec + 3 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.z))) << 32) | tag,
                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(rec + 0,
                                (static_cast<uint64_t>(vkey) << 32) |
@@ -367,25 +431,14 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
         uint32_t khi = 0, klo = 0;
         int rx = 0, ry = 0, rz = 0;
         if (tid < G) {
-            const uint64_t* q = base + 4 * tid;
+            const uint64_t* q = base + tid;
             for (uint32_t spins = 0;; ++spins) {
-                const uint64_t w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w1 = __hip_atomic_load(q + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w2 = __hip_atomic_load(q + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                const uint64_t w3 = __hip_atomic_load(q + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (((w0 >> kLargeIdxBits) & 0x7FFu) == tag && static_cast<uint32_t>(w1) == tag &&
-                    static_cast<uint32_t>(w2) == tag && static_cast<uint32_t>(w3) == tag) {
-                    khi = static_cast<uint32_t>(w0 >> 32);
-                    klo = static_cast<uint32_t>(w0) & kLargeIdxMask;
-                    rx = static_cast<int>(w1 >> 32);
-                    ry = static_cast<int>(w2 >> 32);
-                    rz = static_cast<int>(w3 >> 32);
+                const RecordPoll r = poll_record(q);
+                if (record_ready(r, tag)) {
+                    take_record(r, khi, klo, rx, ry, rz);
                     break;
                 }
-                if (spins >= kSpinLimit ||
-                    ((spins & 63u) == 63u &&
-                     __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
-                    __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (poll_give_up(status, spins)) {
                     abort_flag = 1;
                     break;
                 }
