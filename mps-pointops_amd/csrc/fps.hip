@@ -17,10 +17,11 @@
 //   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
 //                           LDS: points re-read from L2, running distances in
 //                           a caller-provided scratch array.
-//   fps_large_kernel<P,T>   one cloud over every CU (cooperative launch): each
-//                           workgroup keeps its chunk on chip and publishes a
-//                           tagged (distance, index, xyz) record per step;
-//                           every workgroup polls all records and reduces them.
+//   fps_large_kernel<P,T>   one cloud over up to 128 CUs (cooperative launch):
+//                           each workgroup keeps its chunk in VGPRs and
+//                           publishes a tagged (distance, index, xyz) record
+//                           per step; every workgroup polls all records and
+//                           reduces them.
 #include <hip/hip_cooperative_groups.h>
 
 #include "pointops_common.hpp"
@@ -239,30 +240,41 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
 
 // ------------------------------------------------------------ large cloud
 //
-// fps_large_kernel<P>: one cloud over G <= 256 co-resident workgroups (one per
-// CU), cooperative launch.  Workgroup g owns points [g*chunk, g*chunk+chunk);
-// thread t holds P consecutive ones in VGPRs (and the chunk is copied to LDS
-// for coordinate lookups), so the local argmax is the register tree + DPP max
-// of fps_regs_kernel.  Per step the local winner is published as a record of
+// fps_large_kernel<P,T>: one cloud over G <= kLargeMaxGrid co-resident
+// workgroups (at most one per CU), cooperative launch.  Workgroup g owns points
+// [g*chunk, g*chunk+chunk); thread t holds P consecutive ones in VGPRs, so the
+// local argmax is the register tree + DPP max of fps_regs_kernel, and the wave
+// holding the winner reads its coordinates from its own registers (uniform
+// register index).  Per step the local winner is published as a record of
 // four 64-bit words written with agent-scope atomic stores, each carrying the
 // step tag so that a reader can tell a complete record of this step from a
-// stale one two steps back (records are double-buffered by step parity):
+// stale one two steps back (records are double-buffered by step parity and
+// stored as structure of arrays):
 //   w0 = vkey << 32 | tag << 21 | (~idx & 0x1FFFFF)
 //   w1 = x_bits << 32 | tag,  w2 = y_bits << 32 | tag,  w3 = z_bits << 32 | tag
 // vkey = 0 when the workgroup has no candidate, else float bits + 1 (running
 // distances are >= +0 for candidates, so the bits order like the values and
 // the largest (vkey, ~idx) is the largest value with the smallest index).
-// Thread t of every workgroup polls record t (one poll round trip), the wave
-// reduces the keys with two 32-bit DPP maxima, and a barrier combines the four
-// waves.  Polls are bounded: after kSpinLimit attempts (or when another
+// Thread t of every workgroup polls record t, the wave reduces the keys with
+// two 32-bit DPP maxima, and a barrier combines the waves.  Fewer, larger
+// chunks (128 workgroups for a 1M-point cloud) poll less and measured faster
+// than one workgroup per CU.  Polls are bounded: after kSpinLimit attempts (or when another
 // workgroup has given up) the kernel raises a status word and every workgroup
 // returns, so no launch can hang.
 constexpr int kLargeIdxBits = 21;
 constexpr uint32_t kLargeIdxMask = (1u << kLargeIdxBits) - 1u;
 constexpr int64_t kLargeMaxN = int64_t(1) << kLargeIdxBits;
 constexpr uint32_t kSpinLimit = 1u << 22;
-constexpr int kLargeThreads = 256;
-constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread
+#ifndef POINTOPS_FPS_LARGE_THREADS
+#define POINTOPS_FPS_LARGE_THREADS 256
+#endif
+#ifndef POINTOPS_FPS_LARGE_GRID
+#define POINTOPS_FPS_LARGE_GRID 128  // fewer, larger chunks: less poll traffic per step
+#endif
+constexpr int kLargeThreads = POINTOPS_FPS_LARGE_THREADS;
+constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread (SoA stride)
+constexpr int kLargePreferredGrid = POINTOPS_FPS_LARGE_GRID;
+static_assert(kLargePreferredGrid <= kLargeMaxGrid, "one polled record per thread");
 
 __device__ __forceinline__ uint32_t step_tag(int64_t step) {
     return (static_cast<uint32_t>(step >> 1) & 0x3FFu) | 0x400u;  // never 0
@@ -308,14 +320,12 @@ __device__ __forceinline__ bool poll_give_up(uint32_t* status, uint32_t spins) {
     return false;
 }
 
-template <int P>
-__global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
+template <int P, int T>
+__global__ __launch_bounds__(T) void fps_large_kernel(
     const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
     uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk) {
-    constexpr int T = kLargeThreads;
     constexpr int NW = T / kWave;
     constexpr int kNegInf = static_cast<int>(0xFF800000u);
-    __shared__ float4 spts[P * T];
     __shared__ int2 slots[2][NW];
     __shared__ uint64_t red_key[2][NW];
     __shared__ float4 red_xyz[2][NW];
@@ -355,7 +365,6 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
         pz[k] = valid ? pz[k] : 0.f;
         md[k] = !valid ? -INFINITY
                        : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
-        if (valid) spts[j] = make_float4(px[k], py[k], pz[k], 0.f);
     }
     if (tid == 0) abort_flag = 0;
     __syncthreads();
@@ -392,39 +401,47 @@ __global__ __launch_bounds__(kLargeThreads) void fps_large_kernel(
         if (lane == 0) slots[par][wave] = make_int2(wv, wi);
         __syncthreads();
 
-        // Thread 0 publishes this workgroup's record.  Word w of record g is
-        // base[w * kLargeMaxGrid + g], so a wave's poll of 64 records reads
-        // four contiguous 512-byte runs.
+        // The wave holding the workgroup's winner publishes its record: the
+        // winner's coordinates are read from that lane's registers.
         const uint32_t tag = step_tag(step);
         uint64_t* base = records + static_cast<int64_t>(par) * 4 * kLargeMaxGrid;
-        if (tid == 0) {
-            int bv = slots[par][0].x, bi = slots[par][0].y;
+        int bv = slots[par][0].x, bi = slots[par][0].y;
 #pragma unroll
-            for (int w = 1; w < NW; ++w) {
-                if (slots[par][w].x > bv) {
-                    bv = slots[par][w].x;
-                    bi = slots[par][w].y;
-                }
+        for (int w = 1; w < NW; ++w) {
+            if (slots[par][w].x > bv) {
+                bv = slots[par][w].x;
+                bi = slots[par][w].y;
             }
-            uint32_t vkey = 0;
-            float4 c = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (bv != kNegInf) {
-                vkey = static_cast<uint32_t>(bv) + 1u;
-                c = spts[bi];
+        }
+        bv = uniform(bv);
+        bi = uniform(bi);
+        if (wave == bi / (kWave * P)) {
+            // Uniform register index (GPR indexing mode), then the lane.
+            const int ol = uniform((bi / P) % kWave), os = uniform(bi % P);
+            float ox = i2f(readlane(f2i(px[os]), ol));
+            float oy = i2f(readlane(f2i(py[os]), ol));
+            float oz = i2f(readlane(f2i(pz[os]), ol));
+            if (lane == 0) {
+                uint32_t vkey = 0;
+                if (bv != kNegInf) vkey = static_cast<uint32_t>(bv) + 1u;
+                else ox = oy = oz = 0.f;
+                const uint32_t gidx = static_cast<uint32_t>(lo + bi);
+                uint64_t* rec = base + g;
+                __hip_atomic_store(rec + 1 * kLargeMaxGrid,
+                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(ox))) << 32) | tag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(rec + 2 * kLargeMaxGrid,
+                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(oy))) << 32) | tag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(rec + 3 * kLargeMaxGrid,
+                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(oz))) << 32) | tag,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(rec + 0,
+                                   (static_cast<uint64_t>(vkey) << 32) |
+                                       (static_cast<uint64_t>(tag) << kLargeIdxBits) |
+                                       (~gidx & kLargeIdxMask),
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             }
-            const uint32_t gidx = static_cast<uint32_t>(lo + bi);
-            uint64_t* rec = base + g;
-            __hip_atomic_store(rec + 1 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.x))) << 32) | tag,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 2 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.y))) << 32) | tag,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 3 * kLargeMaxGrid, (static_cast<uint64_t>(static_cast<uint32_t>(f2i(c.z))) << 32) | tag,
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(rec + 0,
-                               (static_cast<uint64_t>(vkey) << 32) |
-                                   (static_cast<uint64_t>(tag) << kLargeIdxBits) |
-                                   (~gidx & kLargeIdxMask),
-                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
 
         // Thread t polls record t until all four words carry this step's tag.
@@ -526,15 +543,17 @@ hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint3
                         hipStream_t stream) {
     void* args[] = {(void*)&xyz, (void*)&out, (void*)&records, (void*)&status, (void*)&N,
                     (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk};
-    return hipLaunchCooperativeKernel(reinterpret_cast<const void*>(&fps_large_kernel<P>),
-                                      dim3(grid), dim3(kLargeThreads), args, 0, stream);
+    return hipLaunchCooperativeKernel(
+        reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>), dim3(grid),
+        dim3(kLargeThreads), args, 0, stream);
 }
 
 template <int P>
 int large_capacity(int device) {
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P>), kLargeThreads, 0) !=
+            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>),
+            kLargeThreads, 0) !=
         hipSuccess)
         return 0;
     int cus = 0;
@@ -608,6 +627,9 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
     const int s32 = static_cast<int>(start_idx);
     const int skip = skip_near_origin ? 1 : 0;
     const int choices[] = {1, 2, 4, 8, 16, 32};
+    // Prefer at most kLargePreferredGrid workgroups; clouds too large for that
+    // use up to one workgroup per CU (and per polling thread).
+    for (int limit : {kLargePreferredGrid, kLargeMaxGrid})
     for (int P : choices) {
         int cap = 0;
         switch (P) {
@@ -618,7 +640,7 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
             case 16: cap = large_capacity<16>(device); break;
             default: cap = large_capacity<32>(device); break;
         }
-        cap = min(cap, kLargeMaxGrid);
+        cap = min(cap, limit);
         const int64_t per_block = static_cast<int64_t>(P) * kLargeThreads;
         const int64_t need = (N + per_block - 1) / per_block;
         if (cap <= 0 || need > cap) continue;

@@ -229,7 +229,7 @@ def test_fps_matches_oracle_edge_sizes(cuda_device, n):
     np.testing.assert_array_equal(host(got), want)
 
 
-@pytest.mark.parametrize("n", [1, 33, 1025, 4097, 65537, 100_000, 300_000])
+@pytest.mark.parametrize("n", [1, 33, 1025, 4097, 65537, 100_000, 300_000, 1_500_000, 1 << 21])
 def test_fps_large_matches_oracle(cuda_device, n):
     import mps_pointops as mp
 
