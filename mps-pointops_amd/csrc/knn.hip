@@ -300,6 +300,42 @@ __device__ __forceinline__ void lane_merge(uint32_t (&lk)[KMAX], int (&li)[KMAX]
     }
 }
 
+// Publish each wave's sorted list ([slot][lane] in lds[wave]) and merge the
+// kLaneWaves lists of every lane in wave 0, writing K (sqrt distance, index)
+// pairs at row `row`.  Unfilled slots get (inf, empty_index).
+template <int KMAX>
+__device__ __forceinline__ void lane_publish_and_merge(
+    uint2 (&lds)[kLaneWaves][KMAX > kLaneCap ? KMAX : kLaneCap][kWave], const uint32_t (&lk)[KMAX],
+    const int (&li)[KMAX], int K, int wave, int lane, bool active, int64_t row,
+    float* __restrict__ out_dist, int64_t* __restrict__ out_idx, int64_t empty_index) {
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+        if (s < K) lds[wave][s][lane] = make_uint2(lk[s], static_cast<uint32_t>(li[s]));
+    __syncthreads();
+    if (wave != 0 || !active) return;
+    int head[kLaneWaves] = {0, 0, 0, 0};
+    for (int s = 0; s < K; ++s) {
+        uint2 best = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+        int from = 0;
+#pragma unroll
+        for (int w = 0; w < kLaneWaves; ++w) {
+            if (head[w] < K) {
+                const uint2 c = lds[w][head[w]][lane];
+                if (c.x < best.x || (c.x == best.x && c.y < best.y)) {
+                    best = c;
+                    from = w;
+                }
+            }
+        }
+#pragma unroll
+        for (int w = 0; w < kLaneWaves; ++w)
+            if (w == from) ++head[w];
+        const bool empty = static_cast<int>(best.y) < 0;
+        out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(best.x)));
+        out_idx[row + s] = empty ? empty_index : static_cast<int64_t>(best.y);
+    }
+}
+
 template <int KMAX>
 __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
@@ -387,34 +423,144 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     }
     lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
 
-    // Publish the partial list ([slot][lane]) and merge the 4 lists in wave 0.
+    lane_publish_and_merge<KMAX>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
+                                 out_idx, static_cast<int64_t>(0xFFFFFFFFu));
+}
+
+// Feature-space kNN, K <= KMAX <= 32, D a multiple of 4 up to 128: one lane
+// per query, the scheme of knn3_lane_kernel (4 waves split the references into
+// 4 contiguous ranges, per-lane sorted lists, shared admission limits).  The
+// query stays in VGPRs; each wave streams its range through a wave-private
+// 4 KiB LDS tile (the next tile is loaded into registers while the current
+// one is scanned) and reads each reference with broadcast LDS loads.
+// Semantics of kernels/feature_knn.metal:51-164: a non-finite query matches
+// nothing, non-finite distances never match (keys below the bits of +inf
+// only), unfilled slots are (inf, -1).  The distance is the sequential
+// s = d0^2; s = s + dt^2 with dt = r - q.
+constexpr int kFeatTileFloats = 1024;
+constexpr uint32_t kInfKey = 0x7F800000u;
+
+template <int KMAX, int D>
+__global__ __launch_bounds__(kLaneThreads) void knn_feat_lane_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
+    int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
+    static_assert(D % 4 == 0 && D <= 128, "feature width");
+    constexpr int TR = kFeatTileFloats / D;                // references per tile
+    constexpr int PER_LANE = kFeatTileFloats / kWave / 4;  // float4 loads per lane per tile
+    constexpr int kGroup = 8;                              // references between drains
+    static_assert(TR % kGroup == 0, "tile holds whole groups");
+    __shared__ uint2 lds[kLaneWaves][KMAX > kLaneCap ? KMAX : kLaneCap][kWave];
+    __shared__ uint32_t taus[kLaneWaves][kWave];
+    __shared__ float4 tiles[kLaneWaves][kFeatTileFloats / 4];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t b = blockIdx.y;
+    const int64_t m = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+    const bool active = m < M;
+    const float4* qp = reinterpret_cast<const float4*>(query + D * (b * M + (active ? m : 0)));
+    float q[D];
+    bool ok = active;
 #pragma unroll
-    for (int s = 0; s < KMAX; ++s)
-        if (s < K) buf[s * kWave + lane] = make_uint2(lk[s], static_cast<uint32_t>(li[s]));
+    for (int t = 0; t < D / 4; ++t) {
+        const float4 v = qp[t];
+        q[4 * t] = v.x;
+        q[4 * t + 1] = v.y;
+        q[4 * t + 2] = v.z;
+        q[4 * t + 3] = v.w;
+    }
+#pragma unroll
+    for (int t = 0; t < D; ++t) ok = ok && isfinite(q[t]);
+    const float* rp = ref + D * b * N;
+    uint2* buf = &lds[wave][0][0];
+    float4* tile = tiles[wave];
+    const int64_t span = (N + kLaneWaves - 1) / kLaneWaves;
+    const int64_t lo = wave * span;
+    const int64_t hi = min<int64_t>(N, lo + span);
+
+    uint32_t lk[KMAX];
+    int li[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        lk[s] = kInfKey;
+        li[s] = -1;
+    }
+    uint32_t tau = ok ? kInfKey : 0u;  // admits finite keys only; nothing for bad queries
+    taus[wave][lane] = tau;
     __syncthreads();
-    if (wave != 0 || !active) return;
-    int head[kLaneWaves] = {0, 0, 0, 0};
-    const int64_t row = (b * M + m) * K;
-    for (int s = 0; s < K; ++s) {
-        uint2 best = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
-        int from = 0;
+    auto limit = [&]() {
+        uint32_t lim = tau;
 #pragma unroll
         for (int w = 0; w < kLaneWaves; ++w) {
-            if (head[w] < K) {
-                const uint2 c = lds[w][head[w]][lane];
-                if (c.x < best.x || (c.x == best.x && c.y < best.y)) {
-                    best = c;
-                    from = w;
+            if (w == wave) continue;
+            const uint32_t t = taus[w][lane];
+            lim = min(lim, w < wave ? t : t + 1u);
+        }
+        return lim;
+    };
+    // Load the tile of references starting at t0 into registers (zeros past hi).
+    auto fetch = [&](int64_t t0, float4 (&pf)[PER_LANE]) {
+        const int64_t valid = max<int64_t>(0, min<int64_t>(TR, hi - t0)) * D / 4;
+        const float4* src = reinterpret_cast<const float4*>(rp + D * t0);
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) {
+            const int e = i * kWave + lane;
+            pf[i] = e < valid ? src[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    int cnt = 0;
+    float4 pf[PER_LANE];
+    if (lo < hi) fetch(lo, pf);
+    for (int64_t t0 = lo; t0 < hi; t0 += TR) {
+        // Publish the prefetched tile to this wave's LDS and fetch the next.
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int i = 0; i < PER_LANE; ++i) tile[i * kWave + lane] = pf[i];
+        __builtin_amdgcn_wave_barrier();
+        if (t0 + TR < hi) fetch(t0 + TR, pf);
+        const int nref = static_cast<int>(min<int64_t>(TR, hi - t0));
+        for (int g0 = 0; g0 < nref; g0 += kGroup) {
+            const uint32_t lim = limit();
+#pragma unroll
+            for (int u = 0; u < kGroup; ++u) {
+                if (g0 + u >= nref) break;  // uniform
+                const float4* r = tile + (g0 + u) * (D / 4);
+                float sd = 0.f;
+#pragma unroll
+                for (int t = 0; t < D / 4; ++t) {
+                    const float4 v = r[t];  // same address in every lane: broadcast
+                    const float d0 = v.x - q[4 * t], d1 = v.y - q[4 * t + 1];
+                    const float d2 = v.z - q[4 * t + 2], d3 = v.w - q[4 * t + 3];
+                    sd = t == 0 ? d0 * d0 : sd + d0 * d0;
+                    sd = sd + d1 * d1;
+                    sd = sd + d2 * d2;
+                    sd = sd + d3 * d3;
+                }
+                const uint32_t key = static_cast<uint32_t>(f2i(sd));
+                const bool pass = key < lim;
+                if (ballot(pass) != 0 && pass) {
+                    buf[cnt * kWave + lane] = make_uint2(key, static_cast<uint32_t>(t0 + g0 + u));
+                    ++cnt;
                 }
             }
+            if (ballot(cnt > kLaneCap - kGroup) != 0) {
+                lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
+                cnt = 0;
+                taus[wave][lane] = tau;
+            }
         }
-#pragma unroll
-        for (int w = 0; w < kLaneWaves; ++w)
-            if (w == from) ++head[w];
-        const bool empty = static_cast<int>(best.y) < 0;
-        out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(best.x)));
-        out_idx[row + s] = static_cast<int64_t>(best.y);
     }
+    lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
+    lane_publish_and_merge<KMAX>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
+                                 out_idx, -1);
+}
+
+template <int KMAX, int D>
+hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, int64_t* idx,
+                            int64_t B, int64_t M, int64_t N, int K, hipStream_t stream) {
+    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave), static_cast<uint32_t>(B));
+    hipLaunchKernelGGL((knn_feat_lane_kernel<KMAX, D>), grid, dim3(kLaneThreads), 0, stream, query,
+                       ref, dist, idx, M, N, K);
+    return hipGetLastError();
 }
 
 template <int KMAX>
@@ -433,6 +579,12 @@ hipError_t launch_dense(const float* query, const float* ref, float* dist, int64
         if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, K, stream);
         if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, K, stream);
         return launch_lane<32>(query, ref, dist, idx, B, M, N, K, stream);
+    }
+    const bool aligned = (reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(ref)) % 16 == 0;
+    if (!DIM3 && D == 64 && K <= 32 && aligned && B <= 65535 && (M + kWave - 1) / kWave <= INT32_MAX) {
+        if (K <= 8) return launch_feat_lane<8, 64>(query, ref, dist, idx, B, M, N, K, stream);
+        if (K <= 16) return launch_feat_lane<16, 64>(query, ref, dist, idx, B, M, N, K, stream);
+        return launch_feat_lane<32, 64>(query, ref, dist, idx, B, M, N, K, stream);
     }
     const int64_t rows = B * M;
     const dim3 grid(static_cast<uint32_t>((rows + kKnnWaves - 1) / kKnnWaves));

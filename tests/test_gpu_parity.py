@@ -328,6 +328,34 @@ def test_knn_feat_matches_oracle(cuda_device, dim, k):
     same_bits(host(d), want_d)
 
 
+@pytest.mark.parametrize("m,n,k", [(1, 1, 1), (63, 15, 8), (65, 17, 9), (130, 100, 16),
+                                   (70, 1000, 17), (64, 2049, 32), (3, 40, 33)])
+def test_knn_feat_dim64_lane_path(cuda_device, m, n, k):
+    """D=64, K<=32 runs one lane per query with LDS reference tiles: ragged
+    tiles and wave ranges, duplicate references (ties), non-finite queries
+    and references, and K=33 (wave-per-query path) against the oracle."""
+    import mps_pointops as mp
+
+    if k > n:
+        k = n
+    g = torch.Generator().manual_seed(1000 * m + n + k)
+    ref = torch.randn(2, n, 64, generator=g)
+    query = torch.randn(2, m, 64, generator=g)
+    if n > 4:
+        ref[:, n - 1] = ref[:, 1]
+        ref[:, n // 2] = ref[:, 1]
+        ref[0, 2, 7] = float("nan")
+        ref[1, 3, 0] = float("inf")
+    query[:, 0] = ref[:, min(1, n - 1)]
+    if m > 2:
+        query[0, 2, 5] = float("inf")
+        query[1, 1, 63] = float("nan")
+    want_d, want_i = O.knn_feat(query, ref, k)
+    d, i = mp.knn(query.cuda(), ref.cuda(), k)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
 @pytest.mark.parametrize("radius,k", [(0.1, 16), (0.2, 32), (0.4, 128), (0.7, 1), (2.0, 65)])
 def test_ball_query_matches_oracle(cuda_device, radius, k):
     import mps_pointops as mp
