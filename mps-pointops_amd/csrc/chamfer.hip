@@ -14,6 +14,8 @@
 // Backward (chamfer.py:227-294): gq = (q - ref[idx]) * (2 g) for squared L2,
 // gq = (q > ref[idx] ? 1 : -1) * g for L1; grad_ref[idx] -= gq with hardware
 // float atomics.
+#include <type_traits>
+
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -114,6 +116,65 @@ __global__ __launch_bounds__(kChThreads) void chamfer3_kernel(
 }
 
 // Generic D: sequential accumulation in increasing dimension order.
+// Float 3-D variant: lane = query, the references come through uniform
+// (scalar) loads in batches of 8 (no LDS tile, no barriers); same visiting
+// order and first-minimum rule as chamfer3_kernel.
+template <int NORM>
+__global__ __launch_bounds__(kChThreads) void chamfer3_lane_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref,
+    const int64_t* __restrict__ qlen, const int64_t* __restrict__ rlen,
+    float* __restrict__ out_dist, int64_t* __restrict__ out_idx, int64_t Q, int64_t R) {
+    constexpr int kBatch = 8;
+    const int64_t b = blockIdx.y;
+    const int64_t qi = static_cast<int64_t>(blockIdx.x) * kChThreads + threadIdx.x;
+    const int64_t nq = qlen[b];
+    const int64_t nr = rlen[b];
+    const bool active = qi < Q && qi < nq && nr > 0;
+    float qx = 0.f, qy = 0.f, qz = 0.f;
+    if (active) {
+        const float* qp = query + 3 * (b * Q + qi);
+        qx = qp[0];
+        qy = qp[1];
+        qz = qp[2];
+    }
+    float best = 0.f;
+    int bi = -1;
+    if (ballot(active) != 0) {  // uniform: a wave of padding rows skips the scan
+        const float* rp = ref + 3 * b * R;
+        const int n = static_cast<int>(nr);
+        best = dist3<float, NORM>(qx, qy, qz, rp[0], rp[1], rp[2]);  // first is always taken
+        bi = 0;
+        int j = 1;
+        for (; j + kBatch <= n; j += kBatch) {
+            float c[3 * kBatch];
+            const float* r = rp + 3 * static_cast<int64_t>(j);
+#pragma unroll
+            for (int t = 0; t < 3 * kBatch; ++t) c[t] = r[t];
+#pragma unroll
+            for (int u = 0; u < kBatch; ++u) {
+                const float d = dist3<float, NORM>(qx, qy, qz, c[3 * u], c[3 * u + 1], c[3 * u + 2]);
+                if (d < best) {
+                    best = d;
+                    bi = j + u;
+                }
+            }
+        }
+        for (; j < n; ++j) {
+            const float* r = rp + 3 * static_cast<int64_t>(j);
+            const float d = dist3<float, NORM>(qx, qy, qz, r[0], r[1], r[2]);
+            if (d < best) {
+                best = d;
+                bi = j;
+            }
+        }
+    }
+    if (qi < Q) {
+        const int64_t o = b * Q + qi;
+        out_dist[o] = active ? best : 0.f;
+        out_idx[o] = active ? int64_t(bi) : int64_t(-1);
+    }
+}
+
 template <typename T, int NORM>
 __global__ __launch_bounds__(kChThreads) void chamfer_nd_kernel(
     const T* __restrict__ query, const T* __restrict__ ref, const int64_t* __restrict__ qlen,
@@ -191,7 +252,17 @@ hipError_t launch_nearest(const T* q, const T* r, const int64_t* ql, const int64
     const dim3 grid(static_cast<uint32_t>((Q + kChThreads - 1) / kChThreads),
                     static_cast<uint32_t>(B));
     const dim3 block(kChThreads);
-    if (D == 3) {
+    if (D == 3 && std::is_same<T, float>::value) {
+        const float* qf = reinterpret_cast<const float*>(q);
+        const float* rf = reinterpret_cast<const float*>(r);
+        float* df = reinterpret_cast<float*>(dist);
+        if (norm == 2)
+            hipLaunchKernelGGL((chamfer3_lane_kernel<2>), grid, block, 0, stream, qf, rf, ql, rl, df,
+                               idx, Q, R);
+        else
+            hipLaunchKernelGGL((chamfer3_lane_kernel<1>), grid, block, 0, stream, qf, rf, ql, rl, df,
+                               idx, Q, R);
+    } else if (D == 3) {
         if (norm == 2)
             hipLaunchKernelGGL((chamfer3_kernel<T, 2>), grid, block, 0, stream, q, r, ql, rl, dist, idx,
                                Q, R);
