@@ -386,9 +386,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     uint32_t lim = tau;
     auto visit = [&](float rx, float ry, float rz, int j) {
         const uint32_t key = static_cast<uint32_t>(f2i(sqdist3(rx, ry, rz, qx, qy, qz)));
-        const bool pass = key < lim;
-        if (ballot(pass) == 0) return;
-        if (pass) {
+        if (key < lim) {  // rare once the lists fill: the masked store is skipped
             buf[cnt * kWave + lane] = make_uint2(key, static_cast<uint32_t>(j));
             ++cnt;
         }
@@ -536,8 +534,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn_feat_lane_kernel(
                     sd = sd + d3 * d3;
                 }
                 const uint32_t key = static_cast<uint32_t>(f2i(sd));
-                const bool pass = key < lim;
-                if (ballot(pass) != 0 && pass) {
+                if (key < lim) {
                     buf[cnt * kWave + lane] = make_uint2(key, static_cast<uint32_t>(t0 + g0 + u));
                     ++cnt;
                 }
