@@ -272,6 +272,38 @@ def run(args) -> dict:
         return {"ms": t * 1e3, "points_per_s": B * N / t, "tops": ops / t / 1e12,
                 "frac_fp32_peak": ops / t / MI355X_FP32_PEAK}
 
+    # Config 2's feature propagation (not part of the metric): three_nn from
+    # the 1024 centres to the 4096 points, three_interpolate of C=128 features
+    # (forward and backward), HBM bytes = inputs read once + outputs written.
+    from mps_pointops import three_interpolate, three_nn
+
+    g = torch.Generator().manual_seed(9)
+    feats = torch.randn(B, 128, C2_NPOINT, generator=g).to(device)
+    tn_d, tn_i = three_nn(xyz, centres)
+    inv = 1.0 / (tn_d + 1e-8)
+    w = (inv / inv.sum(-1, keepdim=True)).contiguous()
+    upstream = torch.randn(B, 128, N, generator=g).to(device)
+    fleaf = feats.clone().requires_grad_()
+
+    def interp_fwd_bwd():
+        fleaf.grad = None
+        three_interpolate(fleaf, tn_i, w).backward(upstream)
+
+    for _ in range(max(1, args.warmup)):  # first-use library loading
+        three_nn(xyz, centres)
+        three_interpolate(feats, tn_i, w)
+        interp_fwd_bwd()
+    torch.cuda.synchronize()
+    t_tn = timer.time(lambda: three_nn(xyz, centres), reps)
+    t_ti = timer.time(lambda: three_interpolate(feats, tn_i, w), reps)
+    t_tib = timer.time(interp_fwd_bwd, reps)
+    interp_bytes = 4 * (B * 128 * C2_NPOINT + 2 * B * N * 3 + B * 128 * N)
+    propagation = {
+        "three_nn": {"ms": t_tn * 1e3, "tops": PAIR_OPS * B * N * C2_NPOINT / t_tn / 1e12},
+        "three_interpolate": {"ms": t_ti * 1e3, "gbps": interp_bytes / t_ti / 1e9},
+        "three_interpolate_fwd_bwd": {"ms": t_tib * 1e3, "gbps": 2 * interp_bytes / t_tib / 1e9},
+    }
+
     kernel = fps_kernel_name(N)
     achieved = fps_ops / t_fps
     traffic = profiled_traffic(kernel, "c2")
@@ -295,6 +327,7 @@ def run(args) -> dict:
         },
         "ops": {"fps": op(t_fps, fps_ops), "ball_query_x3": op(t_ball, ball_ops),
                 "knn": op(t_knn, knn_ops)},
+        "propagation_not_in_value": propagation,
         "roofline": {
             "kernel": kernel,
             "bound": "mfma",

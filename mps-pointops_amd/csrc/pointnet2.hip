@@ -9,9 +9,11 @@
 // index) and the strict cascade of kernels/pointnet2.metal:24-43.
 //
 // three_interpolate: out[b,c,n] = (f[i0]*w0 + f[i1]*w1) + f[i2]*w2
-// (kernels/pointnet2.metal:52-71); one lane per (b, n) over a few channels so
-// that the index/weight triplet is read once per channel group.  The backward
-// adds g*w_t into grad_features with hardware float atomics.
+// (kernels/pointnet2.metal:52-71).  When a group of feature rows fits LDS
+// (M <= 16384) a block stages CG rows of one batch and gathers from LDS; the
+// backward accumulates g*w_t into LDS rows with LDS float atomics and writes
+// each row once.  Larger M falls back to one lane per (b, n) over 4 channels,
+// gathering from memory, with hardware float atomics in the backward.
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -126,6 +128,137 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_kernel(
     }
 }
 
+// LDS-staged variants (M <= kTiLdsFloats / CG): one block per (batch,
+// group of CG channels, slice of the unknowns).  The CG feature rows are
+// staged in LDS with coalesced loads, so the three gathers per output hit LDS
+// instead of the vector-memory path, and the index/weight triplets are read
+// once per channel group.  Backward accumulates into LDS rows with LDS float
+// atomics and writes each row once (no global atomics): the block covers all
+// unknowns of its (batch, channel group).
+constexpr int kTiLdsFloats = 16384;  // 64 KiB of dynamic LDS
+constexpr int kTiSlices = 4;         // unknown-slices per (batch, channel group) in the forward
+
+// Copy `count` floats from global memory to LDS with float4 loads, eight in
+// flight per thread (the source is 16-byte aligned when count % 4 == 0).
+__device__ __forceinline__ void stage_rows(float* __restrict__ dst, const float* __restrict__ src,
+                                           int64_t count) {
+    constexpr int kInFlight = 8;
+    if (count % 4 == 0 && reinterpret_cast<uintptr_t>(src) % 16 == 0) {
+        const int64_t n4 = count / 4;
+        const float4* s4 = reinterpret_cast<const float4*>(src);
+        float4* d4 = reinterpret_cast<float4*>(dst);
+        for (int64_t e0 = threadIdx.x; e0 < n4; e0 += kInFlight * kTiThreads) {
+            float4 v[kInFlight];
+#pragma unroll
+            for (int u = 0; u < kInFlight; ++u) {
+                const int64_t e = e0 + u * kTiThreads;
+                v[u] = e < n4 ? s4[e] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kInFlight; ++u) {
+                const int64_t e = e0 + u * kTiThreads;
+                if (e < n4) d4[e] = v[u];
+            }
+        }
+    } else {
+        for (int64_t e = threadIdx.x; e < count; e += kTiThreads) dst[e] = src[e];
+    }
+}
+
+template <int CG>
+__global__ __launch_bounds__(kTiThreads) void three_interpolate_lds_kernel(
+    const float* __restrict__ features, const int32_t* __restrict__ idx,
+    const float* __restrict__ weights, float* __restrict__ out, int64_t C, int64_t M, int64_t N) {
+    extern __shared__ float rows[];  // CG x M
+    const int64_t b = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CG;
+    const int cg = static_cast<int>(min<int64_t>(CG, C - c0));
+    stage_rows(rows, features + (b * C + c0) * M, cg * M);  // cg consecutive rows
+    __syncthreads();
+    const int64_t per = (N + kTiSlices - 1) / kTiSlices;
+    const int64_t n_lo = blockIdx.z * per, n_hi = min<int64_t>(N, n_lo + per);
+    for (int64_t n = n_lo + threadIdx.x; n < n_hi; n += kTiThreads) {
+        const int64_t tri = 3 * (b * N + n);
+        const int32_t a0 = idx[tri], a1 = idx[tri + 1], a2 = idx[tri + 2];
+        const float w0 = weights[tri], w1 = weights[tri + 1], w2 = weights[tri + 2];
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc) {
+            if (cc >= cg) break;
+            const float* f = rows + cc * M;
+            const float x = f[a0] * w0;
+            const float y = f[a1] * w1;
+            const float z = f[a2] * w2;
+            out[(b * C + c0 + cc) * N + n] = (x + y) + z;
+        }
+    }
+}
+
+template <int CG>
+__global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_lds_kernel(
+    const float* __restrict__ grad_out, const int32_t* __restrict__ idx,
+    const float* __restrict__ weights, float* __restrict__ grad_features, int64_t C, int64_t M,
+    int64_t N) {
+    extern __shared__ float acc[];  // CG x M
+    const int64_t b = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CG;
+    const int cg = static_cast<int>(min<int64_t>(CG, C - c0));
+    for (int64_t e = threadIdx.x; e < cg * M; e += kTiThreads) acc[e] = 0.f;
+    __syncthreads();
+    for (int64_t n = threadIdx.x; n < N; n += kTiThreads) {
+        const int64_t tri = 3 * (b * N + n);
+        const int32_t a0 = idx[tri], a1 = idx[tri + 1], a2 = idx[tri + 2];
+        const float w0 = weights[tri], w1 = weights[tri + 1], w2 = weights[tri + 2];
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc) {
+            if (cc >= cg) break;
+            const float g = grad_out[(b * C + c0 + cc) * N + n];
+            float* a = acc + cc * M;
+            atomicAdd(a + a0, g * w0);
+            atomicAdd(a + a1, g * w1);
+            atomicAdd(a + a2, g * w2);
+        }
+    }
+    __syncthreads();
+    float* dst = grad_features + (b * C + c0) * M;
+    for (int64_t e = threadIdx.x; e < cg * M; e += kTiThreads) dst[e] = acc[e];
+}
+
+// Channels per block so that CG rows of M floats fit the LDS budget (0: too big).
+int lds_channel_group(int64_t M) {
+    for (int cg : {16, 8, 4, 2, 1})
+        if (static_cast<int64_t>(cg) * M <= kTiLdsFloats) return cg;
+    return 0;
+}
+
+template <int CG>
+hipError_t launch_interp_lds(bool backward, const float* a, const int32_t* idx, const float* w,
+                             float* o, int64_t B, int64_t C, int64_t M, int64_t N,
+                             hipStream_t stream) {
+    const size_t shmem = static_cast<size_t>(CG) * static_cast<size_t>(M) * sizeof(float);
+    const uint32_t groups = static_cast<uint32_t>((C + CG - 1) / CG);
+    if (backward)
+        hipLaunchKernelGGL((three_interpolate_backward_lds_kernel<CG>),
+                           dim3(groups, static_cast<uint32_t>(B), 1), dim3(kTiThreads), shmem,
+                           stream, a, idx, w, o, C, M, N);
+    else
+        hipLaunchKernelGGL((three_interpolate_lds_kernel<CG>),
+                           dim3(groups, static_cast<uint32_t>(B), kTiSlices), dim3(kTiThreads), shmem,
+                           stream, a, idx, w, o, C, M, N);
+    return hipGetLastError();
+}
+
+hipError_t dispatch_interp_lds(bool backward, const float* a, const int32_t* idx, const float* w,
+                               float* o, int64_t B, int64_t C, int64_t M, int64_t N,
+                               hipStream_t stream) {
+    switch (lds_channel_group(M)) {
+        case 16: return launch_interp_lds<16>(backward, a, idx, w, o, B, C, M, N, stream);
+        case 8: return launch_interp_lds<8>(backward, a, idx, w, o, B, C, M, N, stream);
+        case 4: return launch_interp_lds<4>(backward, a, idx, w, o, B, C, M, N, stream);
+        case 2: return launch_interp_lds<2>(backward, a, idx, w, o, B, C, M, N, stream);
+        default: return launch_interp_lds<1>(backward, a, idx, w, o, B, C, M, N, stream);
+    }
+}
+
 bool grid_fits(int64_t B, int64_t C, int64_t N) {
     return B <= 65535 && (C + kTiChannels - 1) / kTiChannels <= 65535 &&
            (N + kTiThreads - 1) / kTiThreads <= INT32_MAX;
@@ -157,6 +290,8 @@ hipError_t pointops_three_interpolate(const float* features, const int32_t* idx,
     if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
     if (B == 0 || C == 0 || N == 0) return hipSuccess;
     if (M == 0 || !grid_fits(B, C, N)) return hipErrorInvalidValue;
+    if (lds_channel_group(M) > 0)
+        return dispatch_interp_lds(false, features, idx, weights, out, B, C, M, N, stream);
     const dim3 grid(static_cast<uint32_t>((N + kTiThreads - 1) / kTiThreads),
                     static_cast<uint32_t>((C + kTiChannels - 1) / kTiChannels),
                     static_cast<uint32_t>(B));
@@ -172,6 +307,8 @@ hipError_t pointops_three_interpolate_backward(const float* grad_out, const int3
     if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
     if (B == 0 || C == 0 || N == 0) return hipSuccess;
     if (M == 0 || !grid_fits(B, C, N)) return hipErrorInvalidValue;
+    if (lds_channel_group(M) > 0)
+        return dispatch_interp_lds(true, grad_out, idx, weights, grad_features, B, C, M, N, stream);
     const dim3 grid(static_cast<uint32_t>((N + kTiThreads - 1) / kTiThreads),
                     static_cast<uint32_t>((C + kTiChannels - 1) / kTiChannels),
                     static_cast<uint32_t>(B));
