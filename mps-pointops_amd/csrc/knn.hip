@@ -301,11 +301,11 @@ __device__ __forceinline__ void lane_merge(uint32_t (&lk)[KMAX], int (&li)[KMAX]
 }
 
 // Publish each wave's sorted list ([slot][lane] in lds[wave]) and merge the
-// kLaneWaves lists of every lane in wave 0, writing K (sqrt distance, index)
+// NW lists of every lane in wave 0, writing K (sqrt distance, index)
 // pairs at row `row`.  Unfilled slots get (inf, empty_index).
-template <int KMAX>
+template <int KMAX, int NW, int CAP>
 __device__ __forceinline__ void lane_publish_and_merge(
-    uint2 (&lds)[kLaneWaves][KMAX > kLaneCap ? KMAX : kLaneCap][kWave], const uint32_t (&lk)[KMAX],
+    uint2 (&lds)[NW][KMAX > CAP ? KMAX : CAP][kWave], const uint32_t (&lk)[KMAX],
     const int (&li)[KMAX], int K, int wave, int lane, bool active, int64_t row,
     float* __restrict__ out_dist, int64_t* __restrict__ out_idx, int64_t empty_index) {
 #pragma unroll
@@ -313,12 +313,14 @@ __device__ __forceinline__ void lane_publish_and_merge(
         if (s < K) lds[wave][s][lane] = make_uint2(lk[s], static_cast<uint32_t>(li[s]));
     __syncthreads();
     if (wave != 0 || !active) return;
-    int head[kLaneWaves] = {0, 0, 0, 0};
+    int head[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) head[w] = 0;
     for (int s = 0; s < K; ++s) {
         uint2 best = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
         int from = 0;
 #pragma unroll
-        for (int w = 0; w < kLaneWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             if (head[w] < K) {
                 const uint2 c = lds[w][head[w]][lane];
                 if (c.x < best.x || (c.x == best.x && c.y < best.y)) {
@@ -328,7 +330,7 @@ __device__ __forceinline__ void lane_publish_and_merge(
             }
         }
 #pragma unroll
-        for (int w = 0; w < kLaneWaves; ++w)
+        for (int w = 0; w < NW; ++w)
             if (w == from) ++head[w];
         const bool empty = static_cast<int>(best.y) < 0;
         out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(best.x)));
@@ -336,14 +338,14 @@ __device__ __forceinline__ void lane_publish_and_merge(
     }
 }
 
-template <int KMAX>
-__global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
+template <int KMAX, int NW, int CAP>
+__global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
     int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
     // Per wave: the candidate buffer during the scan, then the final list.
-    __shared__ uint2 lds[kLaneWaves][KMAX > kLaneCap ? KMAX : kLaneCap][kWave];
+    __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
     // Per wave and lane: the key of its K-th entry, read by the other waves.
-    __shared__ uint32_t taus[kLaneWaves][kWave];
+    __shared__ uint32_t taus[NW][kWave];
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
     const int64_t b = blockIdx.y;
@@ -353,7 +355,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     const float qx = qp[0], qy = qp[1], qz = qp[2];
     const float* rp = ref + 3 * b * N;
     uint2* buf = &lds[wave][0][0];
-    const int64_t span = (N + kLaneWaves - 1) / kLaneWaves;
+    const int64_t span = (N + NW - 1) / NW;
     const int64_t lo = wave * span;
     const int64_t hi = min<int64_t>(N, lo + span);
 
@@ -375,7 +377,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     auto limit = [&]() {
         uint32_t lim = tau;
 #pragma unroll
-        for (int w = 0; w < kLaneWaves; ++w) {
+        for (int w = 0; w < NW; ++w) {
             if (w == wave) continue;
             const uint32_t t = taus[w][lane];
             lim = min(lim, w < wave ? t : t + 1u);
@@ -394,7 +396,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     constexpr int kRefBatch = 8;
     // After a batch: merge once a lane's buffer could not take another batch.
     auto drain = [&]() {
-        if (ballot(cnt > kLaneCap - kRefBatch) != 0) {
+        if (ballot(cnt > CAP - kRefBatch) != 0) {
             lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
             cnt = 0;
             taus[wave][lane] = tau;
@@ -421,7 +423,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn3_lane_kernel(
     }
     lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
 
-    lane_publish_and_merge<KMAX>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
+    lane_publish_and_merge<KMAX, NW, CAP>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
                                  out_idx, static_cast<int64_t>(0xFFFFFFFFu));
 }
 
@@ -547,8 +549,8 @@ __global__ __launch_bounds__(kLaneThreads) void knn_feat_lane_kernel(
         }
     }
     lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
-    lane_publish_and_merge<KMAX>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
-                                 out_idx, -1);
+    lane_publish_and_merge<KMAX, kLaneWaves, kLaneCap>(lds, lk, li, K, wave, lane, active,
+                                                      (b * M + m) * K, out_dist, out_idx, -1);
 }
 
 template <int KMAX, int D>
@@ -564,8 +566,12 @@ template <int KMAX>
 hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                        int64_t M, int64_t N, int K, hipStream_t stream) {
     const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave), static_cast<uint32_t>(B));
-    hipLaunchKernelGGL((knn3_lane_kernel<KMAX>), grid, dim3(kLaneThreads), 0, stream, query, ref,
-                       dist, idx, M, N, K);
+    // Small lists: 8 waves per 64 queries (more waves in flight, 16-entry
+    // buffers); K up to 32: 4 waves with 32-entry buffers.
+    constexpr int NW = KMAX <= 16 ? 8 : 4;
+    constexpr int CAP = KMAX <= 16 ? 16 : 32;
+    hipLaunchKernelGGL((knn3_lane_kernel<KMAX, NW, CAP>), grid, dim3(NW * kWave), 0, stream, query,
+                       ref, dist, idx, M, N, K);
     return hipGetLastError();
 }
 
