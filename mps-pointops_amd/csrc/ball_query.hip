@@ -60,16 +60,15 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
         // so one L2 round trip covers kBqDepth * 64 points.
         for (int base = 0; base < n && found < K; base += kBqDepth * kWave) {
             float vx[kBqDepth], vy[kBqDepth], vz[kBqDepth];
+            // Loads are clamped into the cloud (not skipped) so that all of
+            // them are in flight at once; lanes past n are masked below.
 #pragma unroll
             for (int c = 0; c < kBqDepth; ++c) {
-                const int j = base + c * kWave + lane;
-                vx[c] = vy[c] = vz[c] = 0.f;
-                if (j < n) {
-                    const S* pt = pp + 3 * static_cast<int64_t>(j);
-                    vx[c] = widen(pt[0]);
-                    vy[c] = widen(pt[1]);
-                    vz[c] = widen(pt[2]);
-                }
+                const int jj = min(base + c * kWave + lane, n - 1);
+                const S* pt = pp + 3 * static_cast<int64_t>(jj);
+                vx[c] = widen(pt[0]);
+                vy[c] = widen(pt[1]);
+                vz[c] = widen(pt[2]);
             }
 #pragma unroll
             for (int c = 0; c < kBqDepth; c += 2) {
@@ -132,14 +131,11 @@ __global__ __launch_bounds__(kBqThreads) void radius_flat_kernel(
             float vx[kBqDepth], vy[kBqDepth], vz[kBqDepth];
 #pragma unroll
             for (int c = 0; c < kBqDepth; ++c) {
-                const int64_t j = base + c * kWave + lane;
-                vx[c] = vy[c] = vz[c] = 0.f;
-                if (j < hi) {
-                    const S* pt = x + 3 * j;
-                    vx[c] = widen(pt[0]);
-                    vy[c] = widen(pt[1]);
-                    vz[c] = widen(pt[2]);
-                }
+                const int64_t jj = min<int64_t>(base + c * kWave + lane, hi - 1);
+                const S* pt = x + 3 * jj;
+                vx[c] = widen(pt[0]);
+                vy[c] = widen(pt[1]);
+                vz[c] = widen(pt[2]);
             }
 #pragma unroll
             for (int c = 0; c < kBqDepth; ++c) {
