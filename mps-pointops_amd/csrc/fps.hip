@@ -89,10 +89,21 @@ __device__ __forceinline__ int block_argmax(const int2* slots) {
     return bidx;
 }
 
+// One wave's candidate for a step: its largest running distance, the
+// smallest point index holding it, and that point's coordinates.
+struct alignas(16) WaveBest {
+    int key;    // running distance bits
+    int index;  // local point index
+    float x, y, z;
+    int pad[3];
+};
+
 // Thread t holds points t*P .. t*P+P-1, so point order = (wave, lane, slot)
-// order: the first maximum found by lane, then by wave, is the one with the
-// smallest index.  Running distances are never NaN (fminf), so their bit
-// patterns order like the floats as signed ints (-inf below +0).
+// order: the first maximum found by slot, then lane, then wave, is the one
+// with the smallest index.  Running distances are never NaN, so their bit
+// patterns order like the floats as signed ints (-inf below +0).  Each wave
+// publishes its candidate with the coordinates, so one barrier and one LDS
+// round trip per step give every wave the next centroid.
 template <int P, int T>
 __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ xyz,
                                                      const int64_t* __restrict__ ptr,
@@ -101,9 +112,8 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
                                                      int64_t* __restrict__ out, int64_t N,
                                                      int64_t npoint, int64_t start, int skip) {
     constexpr int NW = T / kWave;
-    constexpr int kNegInf = static_cast<int>(0xFF800000u);
-    __shared__ float4 spts[P * T];
-    __shared__ int2 slots[2][NW];
+    static_assert(NW <= 8, "the block argmax reduces 8 lanes");
+    __shared__ WaveBest slots[2][8];
 
     const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
     if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
@@ -114,12 +124,16 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
     const int wave = tid / kWave;
     const int lane = tid % kWave;
 
-    float px[P], py[P], pz[P];
+    // One spare element each: with 9+ elements a uniform dynamic index
+    // (px[os] below) compiles to one indexed move instead of a select chain.
+    float px[P + 1], py[P + 1], pz[P + 1];
     float md[P];  // running distances
 #pragma unroll
-    for (int k = 0; k < P; ++k) {
+    for (int k = 0; k <= P; ++k) {
         px[k] = py[k] = pz[k] = 0.f;
     }
+    int far = static_cast<int>(seg.start);
+    float cx = 0.f, cy = 0.f, cz = 0.f;  // coordinates of point `far`
     if (n > 0) {
         // Loads are clamped into the cloud (not skipped) so that all P of
         // them are in flight at once; padding slots are masked below.
@@ -130,6 +144,10 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
             py[k] = p[3 * jj + 1];
             pz[k] = p[3 * jj + 2];
         }
+        const int f = min(max(far, 0), n - 1);
+        cx = p[3 * f];
+        cy = p[3 * f + 1];
+        cz = p[3 * f + 2];
     }
 #pragma unroll
     for (int k = 0; k < P; ++k) {
@@ -140,52 +158,52 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
         pz[k] = valid ? pz[k] : 0.f;
         md[k] = !valid ? -INFINITY
                        : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
-        if (valid) spts[j] = make_float4(px[k], py[k], pz[k], 0.f);
     }
-    __syncthreads();
 
-    int far = static_cast<int>(seg.start);
+    // Lanes of the block argmax: lane l reads wave (l % 8)'s candidate;
+    // waves past NW read a copy of wave 0's, which never wins a tie.
+    const int peer = (lane % 8) < NW ? lane % 8 : 0;
     for (int64_t step = 0; step < seg.cnt; ++step) {
         if (tid == 0) o[step] = seg.base + far;
         if (step + 1 == seg.cnt) break;
-        const float4 c = spts[far];
-        int v[P], s[P];
+        int v[P];
 #pragma unroll
         for (int k = 0; k < P; ++k) {
-            const float d = sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z);
-            md[k] = fminf(md[k], d);
+            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
             v[k] = f2i(md[k]);
-            s[k] = k;
         }
-        // Lane argmax as a tree; the right (larger-index) side wins only if
-        // larger.  Slots merge by value, not by array position, so that the
-        // compiler keeps every step a register select.
+        int lm = v[0];
 #pragma unroll
-        for (int w = 1; w < P; w <<= 1) {
+        for (int k = 1; k < P; ++k) lm = max(lm, v[k]);
+        int ls = P - 1;  // first slot of this lane holding lm
 #pragma unroll
-            for (int k = 0; k + w < P; k += 2 * w) {
-                const int right = -static_cast<int>(v[k + w] > v[k]);
-                v[k] = max(v[k], v[k + w]);
-                s[k] ^= (s[k] ^ s[k + w]) & right;
-            }
-        }
+        for (int k = P - 2; k >= 0; --k) ls = v[k] == lm ? k : ls;
         // First lane holding the wave's largest value: the smallest index.
-        const int wv = wave_max_i32(v[0]);
-        const int wl = static_cast<int>(__builtin_ctzll(ballot(v[0] == wv)));
-        const int wi = (wave * kWave + wl) * P + readlane(s[0], wl);
-        int2* buf = slots[step & 1];
-        if (lane == 0) buf[wave] = make_int2(wv, wi);
-        __syncthreads();
-        int bv = buf[0].x, bi = buf[0].y;  // first wave with the largest value
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            const int2 e = buf[w];
-            if (e.x > bv) {
-                bv = e.x;
-                bi = e.y;
-            }
+        const int wv = wave_max_i32_l63(lm);
+        const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
+        const int os = readlane(ls, wl);
+        WaveBest* buf = slots[step & 1];
+        const float wx = i2f(readlane(f2i(px[os]), wl));
+        const float wy = i2f(readlane(f2i(py[os]), wl));
+        const float wz = i2f(readlane(f2i(pz[os]), wl));
+        if (lane == 0) {
+            WaveBest c;
+            c.key = wv;
+            c.index = (wave * kWave + wl) * P + os;
+            c.x = wx;
+            c.y = wy;
+            c.z = wz;
+            c.pad[0] = c.pad[1] = c.pad[2] = 0;
+            buf[wave] = c;
         }
-        far = (bv == kNegInf) ? 0 : bi;  // nothing can be picked: index 0, like the reference
+        __syncthreads();
+        const WaveBest e = buf[peer];
+        const int bv = group8_max_i32(e.key);
+        const int bw = static_cast<int>(__builtin_ctzll(ballot(e.key == bv)));
+        far = readlane(e.index, bw);
+        cx = i2f(readlane(f2i(e.x), bw));
+        cy = i2f(readlane(f2i(e.y), bw));
+        cz = i2f(readlane(f2i(e.z), bw));
     }
 }
 

@@ -88,6 +88,45 @@ __device__ __forceinline__ int wave_max_i32(int v) {
     return max(max(a, b), max(c, d));
 }
 
+// DPP move whose unwritten lanes read INT_MIN, the identity of max, so that
+// max(v, dpp_or_lowest(v)) folds into one v_max_i32_dpp.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ int dpp_or_lowest(int v) {
+    return __builtin_amdgcn_update_dpp(static_cast<int>(0x80000000u), v, CTRL, ROW_MASK, 0xF,
+                                       false);
+}
+
+// Maximum over the wave of a signed int, as a wave-uniform value: butterflies
+// inside each row of 16, then row_bcast:15 / row_bcast:31 carry the row
+// maxima up to lane 63.
+__device__ __forceinline__ int wave_max_i32_l63(int v) {
+    v = max(v, dpp_or_lowest<kDppQuadXor1>(v));
+    v = max(v, dpp_or_lowest<kDppQuadXor2>(v));
+    v = max(v, dpp_or_lowest<kDppRowHalfMirror>(v));
+    v = max(v, dpp_or_lowest<kDppRowMirror>(v));
+    v = max(v, dpp_or_lowest<0x142, 0xA>(v));  // row_bcast:15 into rows 1 and 3
+    v = max(v, dpp_or_lowest<0x143, 0xC>(v));  // row_bcast:31 into rows 2 and 3
+    return readlane(v, 63);
+}
+
+// Maximum over each aligned group of 8 lanes, read from lane 0.
+__device__ __forceinline__ int group8_max_i32(int v) {
+    v = max(v, dpp_or_lowest<kDppQuadXor1>(v));
+    v = max(v, dpp_or_lowest<kDppQuadXor2>(v));
+    v = max(v, dpp_or_lowest<kDppRowHalfMirror>(v));
+    return readlane(v, 0);
+}
+
+// fminf(m, d) for a running minimum m that is never NaN and a computed d
+// (never a signalling NaN): in IEEE mode v_min_f32 returns the non-NaN
+// operand, as fminf does.  Written as one instruction because the compiler
+// otherwise canonicalises the loop-carried operand on every use.
+__device__ __forceinline__ float running_min(float m, float d) {
+    float r;
+    asm("v_min_f32 %0, %1, %2" : "=v"(r) : "v"(m), "v"(d));
+    return r;
+}
+
 // Minimum over the wave of a signed int; every lane gets the result.
 __device__ __forceinline__ int wave_min(int v) {
     v = min(v, dpp<kDppQuadXor1>(v));
