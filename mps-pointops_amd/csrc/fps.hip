@@ -11,9 +11,10 @@
 //   fps_regs_kernel<P,T>    one workgroup per cloud, the cloud's points and
 //                           running distances in VGPRs (P consecutive points
 //                           per thread, so lane order is index order and the
-//                           argmax needs no index reduction), a float4 copy
-//                           in LDS for the centroid broadcast, one barrier per
-//                           step (double-buffered slots).
+//                           argmax needs no index reduction); each wave
+//                           publishes (distance, index, xyz) of its best
+//                           point, so one barrier and one LDS read per step
+//                           (double-buffered slots) broadcast the centroid.
 //   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
 //                           LDS: points re-read from L2, running distances in
 //                           a caller-provided scratch array.
@@ -521,7 +522,7 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
 // ------------------------------------------------------------ dispatch
 
 constexpr int kRegsThreads = 512;  // 8 waves: two per SIMD hide each other's reduction latency
-constexpr int kRegsMaxPoints = 16 * kRegsThreads;  // 8192 points, 128 KiB of LDS
+constexpr int kRegsMaxPoints = 16 * kRegsThreads;  // 8192 points in VGPRs (P = 16)
 constexpr int kGlobalThreads = 1024;
 
 template <int P>
