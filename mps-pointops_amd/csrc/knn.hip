@@ -254,6 +254,13 @@ constexpr int kLaneThreads = kLaneWaves * kWave;
 constexpr int kLaneCap = 32;  // buffered candidates per lane (merged at half)
 constexpr uint32_t kEmptyKey = 0x7F800001u;
 
+// Median of three unsigned ints (one v_med3_u32).
+__device__ __forceinline__ uint32_t med3_u32(uint32_t a, uint32_t b, uint32_t c) {
+    uint32_t r;
+    asm("v_med3_u32 %0, %1, %2, %3" : "=v"(r) : "v"(a), "v"(b), "v"(c));
+    return r;
+}
+
 template <int KMAX>
 __device__ __forceinline__ uint32_t kth_key(const uint32_t (&lk)[KMAX], int K) {
     if (K == KMAX) return lk[KMAX - 1];
@@ -274,23 +281,21 @@ __device__ __forceinline__ void lane_merge(uint32_t (&lk)[KMAX], int (&li)[KMAX]
         if (ballot(has) == 0) break;
         // A lane with nothing to insert inserts the no-op key 0xFFFFFFFF
         // (never below a slot), so the network runs without branches.
-        uint32_t ck = 0xFFFFFFFFu;
-        int cj = 0;
-        if (has) {
-            const uint2 c = buf[e * kWave + lane];
-            if (c.x < tau) {  // the K-th key may have tightened since buffering
-                ck = c.x;
-                cj = static_cast<int>(c.y);
-            }
-        }
-        if (ballot(ck != 0xFFFFFFFFu) == 0) continue;
+        // Row e < max(cnt) <= CAP is inside the buffer for every lane; the
+        // K-th key may have tightened since buffering.
+        const uint2 c = buf[e * kWave + lane];
+        const bool take = has && c.x < tau;
+        const uint32_t ck = take ? c.x : 0xFFFFFFFFu;
+        const int cj = static_cast<int>(c.y);
+        if (ballot(take) == 0) continue;
         // Slots after the insertion point move down one place; `here` means
-        // the candidate goes before slot s, `prev` before slot s - 1.
+        // the candidate goes before slot s, `prev` before slot s - 1.  On a
+        // sorted list the new key of slot s is med3(ck, lk[s-1], lk[s]).
         bool here = ck < lk[KMAX - 1];
 #pragma unroll
         for (int s = KMAX - 1; s > 0; --s) {
             const bool prev = ck < lk[s - 1];
-            lk[s] = prev ? lk[s - 1] : min(ck, lk[s]);
+            lk[s] = med3_u32(ck, lk[s - 1], lk[s]);
             li[s] = prev ? li[s - 1] : (here ? cj : li[s]);
             here = prev;
         }
