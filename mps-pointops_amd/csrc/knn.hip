@@ -349,8 +349,10 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
     // Per wave: the candidate buffer during the scan, then the final list.
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
-    // Per wave and lane: the key of its K-th entry, read by the other waves.
-    __shared__ uint32_t taus[NW][kWave];
+    // Per lane and wave: the key of the wave's K-th entry, read by the other
+    // waves (one lane's NW keys are contiguous: two 16-byte reads).
+    static_assert(NW == 4 || NW == 8, "admission limit reads NW keys as uint4");
+    __shared__ uint4 taus[kWave][NW / 4];
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
     const int64_t b = blockIdx.y;
@@ -372,21 +374,28 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
         li[s] = -1;
     }
     uint32_t tau = active ? kEmptyKey : 0u;  // inactive lanes admit nothing
-    taus[wave][lane] = tau;
+    uint32_t* my_tau = reinterpret_cast<uint32_t*>(&taus[lane][0]) + wave;
+    *my_tau = tau;
     __syncthreads();
     // Admission limit: this wave's K-th key and the other waves' K-th keys
     // (read without synchronisation: they only decrease, so a stale value is
-    // a looser but still valid limit).  A lower range holds smaller indices,
-    // so an equal key from a higher range cannot beat its K-th entry, while an
-    // equal key from a lower range can beat a higher range's K-th entry.
+    // a looser but still valid limit; this wave's own published key is never
+    // below its current one).  A lower range holds smaller indices, so an
+    // equal key from a higher range cannot beat its K-th entry, while an equal
+    // key from a lower range can beat a higher range's K-th entry.
     auto limit = [&]() {
+        uint32_t t[NW];
+#pragma unroll
+        for (int v = 0; v < NW / 4; ++v) {
+            const uint4 q4 = taus[lane][v];
+            t[4 * v] = q4.x;
+            t[4 * v + 1] = q4.y;
+            t[4 * v + 2] = q4.z;
+            t[4 * v + 3] = q4.w;
+        }
         uint32_t lim = tau;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            if (w == wave) continue;
-            const uint32_t t = taus[w][lane];
-            lim = min(lim, w < wave ? t : t + 1u);
-        }
+        for (int w = 0; w < NW; ++w) lim = min(lim, t[w] + static_cast<uint32_t>(w > wave));
         return lim;
     };
     int cnt = 0;
@@ -404,18 +413,19 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
         if (ballot(cnt > CAP - kRefBatch) != 0) {
             lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
             cnt = 0;
-            taus[wave][lane] = tau;
+            *my_tau = tau;
         }
     };
-    // Batches of kRefBatch references through uniform (scalar) loads.
+    // Batches of kRefBatch references through uniform (scalar) loads; the
+    // shared limit is refreshed every second batch.
     int j0 = static_cast<int>(lo);
     const int jhi = static_cast<int>(hi);
-    for (; j0 + kRefBatch <= jhi; j0 += kRefBatch) {
+    for (int batch = 0; j0 + kRefBatch <= jhi; j0 += kRefBatch, ++batch) {
         float cur[3 * kRefBatch];
         const float* r = rp + 3 * static_cast<int64_t>(j0);
 #pragma unroll
         for (int t = 0; t < 3 * kRefBatch; ++t) cur[t] = r[t];
-        lim = limit();
+        lim = (batch & 1) ? min(lim, tau) : limit();
 #pragma unroll
         for (int u = 0; u < kRefBatch; ++u) visit(cur[3 * u], cur[3 * u + 1], cur[3 * u + 2], j0 + u);
         drain();
