@@ -418,17 +418,28 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     };
     // Batches of kRefBatch references through uniform (scalar) loads; the
     // shared limit is refreshed every second batch.
+    // The next batch is requested after the limit is read, so its scalar
+    // loads are in flight while this batch is scanned.
     int j0 = static_cast<int>(lo);
     const int jhi = static_cast<int>(hi);
-    for (int batch = 0; j0 + kRefBatch <= jhi; j0 += kRefBatch, ++batch) {
-        float cur[3 * kRefBatch];
+    float cur[3 * kRefBatch];
+    if (j0 + kRefBatch <= jhi) {
         const float* r = rp + 3 * static_cast<int64_t>(j0);
 #pragma unroll
         for (int t = 0; t < 3 * kRefBatch; ++t) cur[t] = r[t];
+    }
+    for (int batch = 0; j0 + kRefBatch <= jhi; j0 += kRefBatch, ++batch) {
         lim = (batch & 1) ? min(lim, tau) : limit();
+        float nxt[3 * kRefBatch];
+        const int jn = min(j0 + kRefBatch, jhi - kRefBatch);  // stays inside the range
+        const float* r = rp + 3 * static_cast<int64_t>(jn);
+#pragma unroll
+        for (int t = 0; t < 3 * kRefBatch; ++t) nxt[t] = r[t];
 #pragma unroll
         for (int u = 0; u < kRefBatch; ++u) visit(cur[3 * u], cur[3 * u + 1], cur[3 * u + 2], j0 + u);
         drain();
+#pragma unroll
+        for (int t = 0; t < 3 * kRefBatch; ++t) cur[t] = nxt[t];
     }
     for (; j0 < jhi; ++j0) {
         const float* r = rp + 3 * static_cast<int64_t>(j0);
