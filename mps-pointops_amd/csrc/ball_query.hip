@@ -7,6 +7,9 @@
 // slots found + rank, where rank is the number of hit lanes below (ballot +
 // mbcnt), which keeps the first K hits in index order without atomics; the
 // scan stops as soon as K hits are found and the remaining slots are padded.
+// Dense batches (B <= 65535) stage the points through LDS: a workgroup of
+// 8 waves (8 consecutive queries of one cloud) loads each 2048-point tile
+// once for all of them (ball_query_lds_kernel).
 //
 //   dense: _ball_query_mps.py:122-166 / kernels/ball_query.metal:30-166
 //          (query/point lengths, (idx -1, dist2 0) padding, f32 or f16 input)
@@ -24,6 +27,15 @@ namespace {
 constexpr int kBqThreads = 256;
 constexpr int kBqWaves = kBqThreads / kWave;
 constexpr int kBqDepth = 8;  // 64-point blocks in flight per wave (even)
+// Queries (waves) per workgroup of the LDS-staged dense kernel.
+#ifndef POINTOPS_BQ_LDS_QUERIES
+#define POINTOPS_BQ_LDS_QUERIES 8
+#endif
+constexpr int kBqLdsQueries = POINTOPS_BQ_LDS_QUERIES;
+#ifndef POINTOPS_BQ_LDS_DEPTH
+#define POINTOPS_BQ_LDS_DEPTH 32
+#endif
+constexpr int kBqLdsDepth = POINTOPS_BQ_LDS_DEPTH;  // 64-point blocks per LDS tile
 
 template <typename S>
 __device__ __forceinline__ float widen(S v);
@@ -102,6 +114,103 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
     }
 }
 
+// The same search with the candidate points staged through LDS: a workgroup
+// serves NWQ consecutive queries of one cloud (one wave each), its threads
+// load each tile of kBqDepth * 64 points once, and every wave tests its query
+// against the tile.  The workgroup stops after the tile in which its last
+// query reached K hits, so a tile is read from L2 once per NWQ queries.
+template <typename S, int NWQ>
+__global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
+    const S* __restrict__ queries, const S* __restrict__ points,
+    const int64_t* __restrict__ query_lengths, const int64_t* __restrict__ point_lengths,
+    int64_t* __restrict__ out_idx, float* __restrict__ out_dist, int64_t Q, int64_t P, int K,
+    float r2) {
+    constexpr int kTile = kBqLdsDepth * kWave;
+    constexpr int kPer = kTile / (NWQ * kWave);  // points each thread stages per tile
+    static_assert(kPer * NWQ * kWave == kTile && kBqLdsDepth % 2 == 0, "tile shape");
+    __shared__ float4 tile[kTile];
+    __shared__ int done_flags[NWQ];
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = uniform(tid / kWave);
+    const int64_t b = blockIdx.y;
+    const int64_t qi = static_cast<int64_t>(blockIdx.x) * NWQ + wave;
+    const int64_t qlen = query_lengths != nullptr ? query_lengths[b] : Q;
+    const int64_t plen = point_lengths != nullptr ? point_lengths[b] : P;
+    const int n = static_cast<int>(plen < P ? plen : P);
+    const bool live = qi < Q && qi < qlen;
+    const int64_t row = b * Q + (qi < Q ? qi : 0);
+    float qx = 0.f, qy = 0.f, qz = 0.f;
+    if (live) {
+        const S* qp = queries + 3 * row;
+        qx = widen(qp[0]);
+        qy = widen(qp[1]);
+        qz = widen(qp[2]);
+    }
+    int64_t* oi = out_idx + row * K;
+    float* od = out_dist + row * K;
+    const S* pp = points + 3 * b * P;
+    // Points of the tile at `base` for this thread (clamped into the cloud;
+    // points past n are masked in the test).
+    float4 pf[kPer];
+    auto fetch = [&](int base) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const S* pt = pp + 3 * static_cast<int64_t>(min(base + k * NWQ * kWave + tid, n - 1));
+            pf[k] = make_float4(widen(pt[0]), widen(pt[1]), widen(pt[2]), 0.f);
+        }
+    };
+    int found = 0;
+    // d < r2 is impossible for r2 <= 0 (d is never negative) or NaN r2.
+    bool done = !live || !(r2 > 0.f);
+    if (n > 0) fetch(0);
+    for (int base = 0; base < n; base += kTile) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) tile[k * NWQ * kWave + tid] = pf[k];
+        __syncthreads();
+        if (base + kTile < n) fetch(base + kTile);  // in flight during the scan
+        if (!done) {
+#pragma unroll
+            for (int c = 0; c < kBqLdsDepth; c += 2) {
+                const float4 p0 = tile[c * kWave + lane];
+                const float4 p1 = tile[(c + 1) * kWave + lane];
+                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
+                const float d0 = sqdist3(qx, qy, qz, p0.x, p0.y, p0.z);
+                const float d1 = sqdist3(qx, qy, qz, p1.x, p1.y, p1.z);
+                const bool h0 = j0 < n && d0 < r2;
+                const bool h1 = j1 < n && d1 < r2;
+                const uint64_t m0 = ballot(h0), m1 = ballot(h1);
+                if ((m0 | m1) == 0) continue;
+                const int s0 = found + lanes_below(m0);
+                const int s1 = found + __popcll(m0) + lanes_below(m1);
+                if (h0 && s0 < K) {
+                    oi[s0] = j0;
+                    od[s0] = d0;
+                }
+                if (h1 && s1 < K) {
+                    oi[s1] = j1;
+                    od[s1] = d1;
+                }
+                found += __popcll(m0) + __popcll(m1);
+                if (found >= K) break;
+            }
+            done = found >= K;
+        }
+        if (lane == 0) done_flags[wave] = done ? 1 : 0;
+        __syncthreads();  // flags written; every wave is past its reads of this tile
+        bool all_done = true;
+#pragma unroll
+        for (int w = 0; w < NWQ; ++w) all_done = all_done && done_flags[w] != 0;
+        if (all_done) break;
+    }
+    if (qi >= Q) return;
+    found = min(found, K);
+    for (int s = found + lane; s < K; s += kWave) {
+        oi[s] = -1;
+        od[s] = 0.f;
+    }
+}
+
 __device__ __forceinline__ int64_t segment_of(const int64_t* __restrict__ ptr, int64_t batch,
                                               int64_t q) {
     int64_t lo = 0, hi = batch;
@@ -163,6 +272,17 @@ hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t*
     if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kBqDepth * kWave)
         return hipErrorInvalidValue;
     if (B == 0 || Q == 0 || K == 0) return hipSuccess;
+    if constexpr (kBqLdsQueries > 0) {
+        constexpr int NWQ = kBqLdsQueries;
+        const int64_t qblocks = (Q + NWQ - 1) / NWQ;
+        if (B <= 65535 && qblocks <= INT32_MAX) {
+            hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ>),
+                               dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
+                               dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,
+                               static_cast<int>(K), r2);
+            return hipGetLastError();
+        }
+    }
     const int64_t blocks = (B * Q + kBqWaves - 1) / kBqWaves;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL((ball_query_kernel<S>), dim3(static_cast<uint32_t>(blocks)), dim3(kBqThreads),
