@@ -276,6 +276,8 @@ hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t*
         constexpr int NWQ = kBqLdsQueries;
         const int64_t qblocks = (Q + NWQ - 1) / NWQ;
         if (B <= 65535 && qblocks <= INT32_MAX) {
+            // Clouds are spread over all XCDs (blockIdx.x fastest), which
+            // balances clouds of different scan lengths across them.
             hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ>),
                                dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
                                dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,

@@ -355,8 +355,9 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     __shared__ uint4 taus[kWave][NW / 4];
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
-    const int64_t b = blockIdx.y;
-    const int64_t m = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+    const CloudBlock cb = cloud_block(static_cast<uint32_t>((M + kWave - 1) / kWave));
+    const int64_t b = cb.b;
+    const int64_t m = static_cast<int64_t>(cb.x) * kWave + lane;
     const bool active = m < M;
     const float* qp = query + 3 * (b * M + (active ? m : 0));
     const float qx = qp[0], qy = qp[1], qz = qp[2];
@@ -480,8 +481,9 @@ __global__ __launch_bounds__(kLaneThreads) void knn_feat_lane_kernel(
     __shared__ float4 tiles[kLaneWaves][kFeatTileFloats / 4];
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
-    const int64_t b = blockIdx.y;
-    const int64_t m = static_cast<int64_t>(blockIdx.x) * kWave + lane;
+    const CloudBlock cb = cloud_block(static_cast<uint32_t>((M + kWave - 1) / kWave));
+    const int64_t b = cb.b;
+    const int64_t m = static_cast<int64_t>(cb.x) * kWave + lane;
     const bool active = m < M;
     const float4* qp = reinterpret_cast<const float4*>(query + D * (b * M + (active ? m : 0)));
     float q[D];
@@ -582,7 +584,7 @@ __global__ __launch_bounds__(kLaneThreads) void knn_feat_lane_kernel(
 template <int KMAX, int D>
 hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, int64_t* idx,
                             int64_t B, int64_t M, int64_t N, int K, hipStream_t stream) {
-    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave), static_cast<uint32_t>(B));
+    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave * B));  // cloud_block order
     hipLaunchKernelGGL((knn_feat_lane_kernel<KMAX, D>), grid, dim3(kLaneThreads), 0, stream, query,
                        ref, dist, idx, M, N, K);
     return hipGetLastError();
@@ -591,7 +593,7 @@ hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, i
 template <int KMAX>
 hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                        int64_t M, int64_t N, int K, hipStream_t stream) {
-    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave), static_cast<uint32_t>(B));
+    const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave * B));  // cloud_block order
     // Small lists: 8 waves per 64 queries (more waves in flight, 16-entry
     // buffers); K up to 32: 4 waves with 32-entry buffers.
     constexpr int NW = KMAX <= 16 ? 8 : 4;
@@ -604,13 +606,14 @@ hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_
 template <bool DIM3>
 hipError_t launch_dense(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                         int64_t M, int64_t N, int D, int K, hipStream_t stream) {
-    if (DIM3 && K <= 32 && B <= 65535 && (M + kWave - 1) / kWave <= INT32_MAX) {
+    const bool lane_grid_ok = (M + kWave - 1) / kWave * B <= INT32_MAX;
+    if (DIM3 && K <= 32 && lane_grid_ok) {
         if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, K, stream);
         if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, K, stream);
         return launch_lane<32>(query, ref, dist, idx, B, M, N, K, stream);
     }
     const bool aligned = (reinterpret_cast<uintptr_t>(query) | reinterpret_cast<uintptr_t>(ref)) % 16 == 0;
-    if (!DIM3 && D == 64 && K <= 32 && aligned && B <= 65535 && (M + kWave - 1) / kWave <= INT32_MAX) {
+    if (!DIM3 && D == 64 && K <= 32 && aligned && lane_grid_ok) {
         if (K <= 8) return launch_feat_lane<8, 64>(query, ref, dist, idx, B, M, N, K, stream);
         if (K <= 16) return launch_feat_lane<16, 64>(query, ref, dist, idx, B, M, N, K, stream);
         return launch_feat_lane<32, 64>(query, ref, dist, idx, B, M, N, K, stream);

@@ -158,6 +158,18 @@ __device__ __forceinline__ uint32_t xcd_local_block(uint32_t hw, uint32_t nblock
     return (hw % kXcds) * per + hw / kXcds;
 }
 
+// (block within its cloud, cloud) of a workgroup of a 1-D launch of
+// per_cloud * B workgroups, dealt by xcd_local_block so that the workgroups
+// of one cloud share an XCD (and its L2 copy of the cloud).
+struct CloudBlock {
+    uint32_t x;  // block within the cloud
+    uint32_t b;  // cloud
+};
+__device__ __forceinline__ CloudBlock cloud_block(uint32_t per_cloud) {
+    const uint32_t blk = xcd_local_block(blockIdx.x, gridDim.x);
+    return {blk % per_cloud, blk / per_cloud};
+}
+
 }  // namespace pointops
 
 // Host-side launch helper: checks the launch and returns its status.
