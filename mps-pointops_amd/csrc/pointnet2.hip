@@ -137,6 +137,12 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_kernel(
 // unknowns of its (batch, channel group).
 constexpr int kTiLdsFloats = 16384;  // 64 KiB of dynamic LDS
 constexpr int kTiSlices = 4;         // unknown-slices per (batch, channel group) in the forward
+#ifndef POINTOPS_TI_BWD_THREADS
+#define POINTOPS_TI_BWD_THREADS 1024
+#endif
+// Backward: one block covers all unknowns of its (batch, channel group), so it
+// is wide to keep enough loads and LDS atomics in flight.
+constexpr int kTiBwdThreads = POINTOPS_TI_BWD_THREADS;
 
 // Copy `count` floats from global memory to LDS with float4 loads, eight in
 // flight per thread (the source is 16-byte aligned when count % 4 == 0).
@@ -194,7 +200,7 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_lds_kernel(
 }
 
 template <int CG>
-__global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_lds_kernel(
+__global__ __launch_bounds__(kTiBwdThreads) void three_interpolate_backward_lds_kernel(
     const float* __restrict__ grad_out, const int32_t* __restrict__ idx,
     const float* __restrict__ weights, float* __restrict__ grad_features, int64_t C, int64_t M,
     int64_t N) {
@@ -202,9 +208,9 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_lds_ker
     const int64_t b = blockIdx.y;
     const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CG;
     const int cg = static_cast<int>(min<int64_t>(CG, C - c0));
-    for (int64_t e = threadIdx.x; e < cg * M; e += kTiThreads) acc[e] = 0.f;
+    for (int64_t e = threadIdx.x; e < cg * M; e += kTiBwdThreads) acc[e] = 0.f;
     __syncthreads();
-    for (int64_t n = threadIdx.x; n < N; n += kTiThreads) {
+    for (int64_t n = threadIdx.x; n < N; n += kTiBwdThreads) {
         const int64_t tri = 3 * (b * N + n);
         const int32_t a0 = idx[tri], a1 = idx[tri + 1], a2 = idx[tri + 2];
         const float w0 = weights[tri], w1 = weights[tri + 1], w2 = weights[tri + 2];
@@ -220,7 +226,110 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_lds_ker
     }
     __syncthreads();
     float* dst = grad_features + (b * C + c0) * M;
-    for (int64_t e = threadIdx.x; e < cg * M; e += kTiThreads) dst[e] = acc[e];
+    for (int64_t e = threadIdx.x; e < cg * M; e += kTiBwdThreads) dst[e] = acc[e];
+}
+
+// Backward as a gather, for M <= 1024 known points and 3N < 65536 entries:
+// the workgroup of (batch, group of CG channels) buckets the batch's 3N
+// (unknown, slot) entries by known index in LDS (counting sort; 16-bit entry
+// ids), sorts each bucket by entry id, then streams grad_out through LDS in
+// tiles of NT unknowns x CG channels; thread m consumes its bucket's entries
+// of the tile in (n, t) order -- the order of a sequential scatter loop, so
+// the result is deterministic -- and writes each gradient element once.  No
+// float atomics (LDS float atomics serialise at about one lane per 3 cycles).
+constexpr int kTiGatherThreads = 1024;
+constexpr int kTiGatherTile = 256;  // unknowns per staged tile
+constexpr int kTiGatherChannels = 16;
+// LDS for the entry list: 64 KiB minus the scan arrays and the tile.
+constexpr int kTiGatherListBytes =
+    65536 - (2 * kTiGatherThreads + 1) * 4 - kTiGatherChannels * kTiGatherTile * 4;
+
+template <int CG>
+__global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_gather_kernel(
+    const float* __restrict__ grad_out, const int32_t* __restrict__ idx,
+    const float* __restrict__ weights, float* __restrict__ grad_features, int64_t C, int64_t M,
+    int64_t N) {
+    constexpr int T = kTiGatherThreads;
+    constexpr int NT = kTiGatherTile;
+    extern __shared__ uint16_t list[];  // 3N entry ids, bucketed by known index
+    __shared__ int start[T + 1];
+    __shared__ int cursor[T];
+    __shared__ float tile[CG][NT];
+    const int tid = threadIdx.x;
+    const int m_count = static_cast<int>(M);
+    const int n_count = static_cast<int>(N);
+    const int e_count = 3 * n_count;
+    const int64_t b = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CG;
+    const int cg = static_cast<int>(min<int64_t>(CG, C - c0));
+    const int32_t* ib = idx + 3 * b * N;
+    const float* wb = weights + 3 * b * N;
+    const float* gb = grad_out + (b * C + c0) * N;
+
+    cursor[tid] = 0;
+    __syncthreads();
+    // Indices outside [0, M) contribute nothing (the callers validate them).
+    for (int e = tid; e < e_count; e += T) {
+        const int a = ib[e];
+        if (static_cast<unsigned>(a) < static_cast<unsigned>(m_count)) atomicAdd(&cursor[a], 1);
+    }
+    __syncthreads();
+    // Exclusive scan of the T counts (Hillis-Steele over start[1..T]).
+    const int own = cursor[tid];
+    start[tid + 1] = own;
+    if (tid == 0) start[0] = 0;
+    __syncthreads();
+    for (int off = 1; off < T; off <<= 1) {
+        const int v = tid >= off ? start[tid + 1 - off] : 0;
+        __syncthreads();
+        start[tid + 1] += v;
+        __syncthreads();
+    }
+    cursor[tid] = start[tid + 1] - own;  // == start[tid]
+    __syncthreads();
+    for (int e = tid; e < e_count; e += T) {
+        const int a = ib[e];
+        if (static_cast<unsigned>(a) < static_cast<unsigned>(m_count))
+            list[atomicAdd(&cursor[a], 1)] = static_cast<uint16_t>(e);
+    }
+    __syncthreads();
+    const int p0 = start[tid], p1 = start[tid + 1];
+    for (int p = p0 + 1; p < p1; ++p) {  // insertion sort: buckets are short
+        const uint16_t v = list[p];
+        int q = p - 1;
+        while (q >= p0 && list[q] > v) {
+            list[q + 1] = list[q];
+            --q;
+        }
+        list[q + 1] = v;
+    }
+    float acc[CG];
+#pragma unroll
+    for (int cc = 0; cc < CG; ++cc) acc[cc] = 0.f;
+    int p = p0;
+    for (int t0 = 0; t0 < n_count; t0 += NT) {
+        __syncthreads();  // the previous tile (and the sorts) are done
+        for (int k = tid; k < CG * NT; k += T) {
+            const int cc = k / NT, j = k % NT;
+            tile[cc][j] = (cc < cg && t0 + j < n_count) ? gb[static_cast<int64_t>(cc) * N + t0 + j]
+                                                        : 0.f;
+        }
+        __syncthreads();
+        const int e_end = 3 * min(t0 + NT, n_count);
+        for (; p < p1; ++p) {
+            const int e = list[p];
+            if (e >= e_end) break;
+            const float w = wb[e];
+            const float* col = &tile[0][e / 3 - t0];
+#pragma unroll
+            for (int cc = 0; cc < CG; ++cc) acc[cc] = acc[cc] + col[cc * NT] * w;
+        }
+    }
+    if (tid < m_count) {
+#pragma unroll
+        for (int cc = 0; cc < CG; ++cc)
+            if (cc < cg) grad_features[(b * C + c0 + cc) * M + tid] = acc[cc];
+    }
 }
 
 // Channels per block so that CG rows of M floats fit the LDS budget (0: too big).
@@ -238,7 +347,7 @@ hipError_t launch_interp_lds(bool backward, const float* a, const int32_t* idx, 
     const uint32_t groups = static_cast<uint32_t>((C + CG - 1) / CG);
     if (backward)
         hipLaunchKernelGGL((three_interpolate_backward_lds_kernel<CG>),
-                           dim3(groups, static_cast<uint32_t>(B), 1), dim3(kTiThreads), shmem,
+                           dim3(groups, static_cast<uint32_t>(B), 1), dim3(kTiBwdThreads), shmem,
                            stream, a, idx, w, o, C, M, N);
     else
         hipLaunchKernelGGL((three_interpolate_lds_kernel<CG>),
@@ -307,6 +416,15 @@ hipError_t pointops_three_interpolate_backward(const float* grad_out, const int3
     if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
     if (B == 0 || C == 0 || N == 0) return hipSuccess;
     if (M == 0 || !grid_fits(B, C, N)) return hipErrorInvalidValue;
+    if (M <= kTiGatherThreads && 3 * N * 2 <= kTiGatherListBytes) {
+        constexpr int CG = kTiGatherChannels;
+        const size_t shmem = static_cast<size_t>(3 * N) * sizeof(uint16_t);
+        hipLaunchKernelGGL((three_interpolate_backward_gather_kernel<CG>),
+                           dim3(static_cast<uint32_t>((C + CG - 1) / CG), static_cast<uint32_t>(B)),
+                           dim3(kTiGatherThreads), shmem, stream, grad_out, idx, weights,
+                           grad_features, C, M, N);
+        return hipGetLastError();
+    }
     if (lds_channel_group(M) > 0)
         return dispatch_interp_lds(true, grad_out, idx, weights, grad_features, B, C, M, N, stream);
     const dim3 grid(static_cast<uint32_t>((N + kTiThreads - 1) / kTiThreads),

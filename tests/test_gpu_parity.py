@@ -455,6 +455,40 @@ def test_three_nn_and_interpolate_c2(cuda_device):
     np.testing.assert_allclose(host(fc.grad), want_g, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("m,n", [(64, 300), (5, 40), (1024, 4096), (3000, 200)])
+def test_three_interpolate_backward_sequential_order(cuda_device, m, n):
+    """The gradient equals a float32 scatter loop over (n, t) in order, bit for
+    bit, and is the same on every call (no float atomics); (3000, 200) is too
+    large for the bucketed kernel and checks the atomic path to a tolerance."""
+    from mps_pointops import three_interpolate
+
+    g = torch.Generator().manual_seed(m * 7 + n)
+    B, C = 2, 5
+    feats = torch.randn(B, C, m, generator=g)
+    idx = torch.randint(0, m, (B, n, 3), generator=g, dtype=torch.int32)
+    idx[:, : n // 3, :] = idx[:, :1, :]  # a hot bucket
+    w = torch.rand(B, n, 3, generator=g)
+    up = torch.randn(B, C, n, generator=g)
+    grads = []
+    for _ in range(2):
+        fc = feats.cuda().requires_grad_()
+        three_interpolate(fc, idx.cuda(), w.cuda()).backward(up.cuda())
+        grads.append(host(fc.grad))
+    want = np.zeros((B, C, m), np.float32)
+    upn, wn, ixn = up.numpy(), w.numpy(), idx.numpy()
+    for b in range(B):
+        for c in range(C):
+            row = want[b, c]
+            prod = (upn[b, c][:, None] * wn[b]).astype(np.float32)  # fl32(g * w) per (n, t)
+            for j, v in zip(ixn[b].reshape(-1), prod.reshape(-1)):
+                row[j] = np.float32(row[j] + v)
+    if m <= 1024 and 6 * n <= 65536 - 2049 * 4 - 16 * 256 * 4:  # the bucketed kernel
+        np.testing.assert_array_equal(grads[0], want)
+        np.testing.assert_array_equal(grads[1], grads[0])
+    else:
+        np.testing.assert_allclose(grads[0], want, rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.parametrize("m", [3, 4, 50, 1025, 2100])
 def test_three_nn_matches_oracle(cuda_device, m):
     from mps_pointops import three_nn
