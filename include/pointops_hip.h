@@ -138,9 +138,11 @@ hipError_t pointops_three_interpolate(const float *features, const int32_t *idx,
                                       const float *weights, float *out, int64_t B, int64_t C,
                                       int64_t M, int64_t N, hipStream_t stream);
 
-/* grad_features[b,c,i_t] += grad_out[b,c,n] * w[b,n,t] (float atomics;
- * summation order, hence the last bits, is not deterministic).  The caller
- * zero-fills grad_features.  Replaces pointnet2.py:179-186
+/* grad_features[b,c,i_t] += grad_out[b,c,n] * w[b,n,t].  For M <= 1024 and
+ * N <= 6826 each element is summed in (n, t) order, the order of a
+ * sequential loop (deterministic); otherwise by float atomics, whose order,
+ * hence the last bits, is not deterministic.  The caller zero-fills
+ * grad_features.  Replaces pointnet2.py:179-186
  * (kernels/pointnet2.metal:85-103). */
 hipError_t pointops_three_interpolate_backward(const float *grad_out, const int32_t *idx,
                                                const float *weights, float *grad_features,
