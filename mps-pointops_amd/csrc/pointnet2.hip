@@ -136,7 +136,7 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_kernel(
 // atomics and writes each row once (no global atomics): the block covers all
 // unknowns of its (batch, channel group).
 constexpr int kTiLdsFloats = 16384;  // 64 KiB of dynamic LDS
-constexpr int kTiSlices = 4;         // unknown-slices per (batch, channel group) in the forward
+constexpr int kTiSlices = 1;         // unknown-slices per (batch, channel group) in the forward
 #ifndef POINTOPS_TI_BWD_THREADS
 #define POINTOPS_TI_BWD_THREADS 1024
 #endif
@@ -334,7 +334,9 @@ __global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_g
 
 // Channels per block so that CG rows of M floats fit the LDS budget (0: too big).
 int lds_channel_group(int64_t M) {
-    for (int cg : {16, 8, 4, 2, 1})
+    // At most 4 rows (16 KiB for M = 1024): more, smaller workgroups keep
+    // more of HBM busy than 16-row groups do (4.4 against 3.6 TB/s at c2).
+    for (int cg : {4, 2, 1})
         if (static_cast<int64_t>(cg) * M <= kTiLdsFloats) return cg;
     return 0;
 }
