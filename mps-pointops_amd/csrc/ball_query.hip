@@ -18,6 +18,8 @@
 //          index == query index before the cap)
 #include <hip/hip_fp16.h>
 
+#include <type_traits>
+
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -169,7 +171,8 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
         for (int k = 0; k < kPer; ++k) tile[k * NWQ * kWave + tid] = pf[k];
         __syncthreads();
         if (base + kTile < n) fetch(base + kTile);  // in flight during the scan
-        if (!done) {
+        // A full tile needs no bounds test (one instantiation each).
+        auto scan = [&](auto full) {
 #pragma unroll
             for (int c = 0; c < kBqLdsDepth; c += 2) {
                 const float4 p0 = tile[c * kWave + lane];
@@ -177,8 +180,8 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
                 const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
                 const float d0 = sqdist3(qx, qy, qz, p0.x, p0.y, p0.z);
                 const float d1 = sqdist3(qx, qy, qz, p1.x, p1.y, p1.z);
-                const bool h0 = j0 < n && d0 < r2;
-                const bool h1 = j1 < n && d1 < r2;
+                const bool h0 = (decltype(full)::value || j0 < n) && d0 < r2;
+                const bool h1 = (decltype(full)::value || j1 < n) && d1 < r2;
                 const uint64_t m0 = ballot(h0), m1 = ballot(h1);
                 if ((m0 | m1) == 0) continue;
                 const int s0 = found + lanes_below(m0);
@@ -194,6 +197,10 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
                 found += __popcll(m0) + __popcll(m1);
                 if (found >= K) break;
             }
+        };
+        if (!done) {
+            if (base + kTile <= n) scan(std::true_type{});
+            else scan(std::false_type{});
             done = found >= K;
         }
         if (lane == 0) done_flags[wave] = done ? 1 : 0;
