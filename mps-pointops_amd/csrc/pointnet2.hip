@@ -1,12 +1,12 @@
 // PointNet++ feature propagation for gfx950: three_nn and three_interpolate.
 //
-// three_nn: one lane per unknown point, the batch's known points staged
-// through LDS in tiles (one float4 per point, broadcast reads).  The three
-// best keys are kept in registers; a key is the squared distance's bit
-// pattern (non-negative floats order like unsigned integers) with NaN mapped
-// above +inf, and known points are visited in index order with a strict `<`,
-// which reproduces the stable argsort of pointnet2.py:54-72 (NaN last, ties by
-// index) and the strict cascade of kernels/pointnet2.metal:24-43.
+// three_nn: one lane per unknown point, 4 waves splitting the known points,
+// which arrive through uniform (scalar) loads.  The three best keys are kept
+// in registers; a key is the squared distance's bit pattern (non-negative
+// floats order like unsigned integers) with NaN mapped above +inf, and known
+// points are visited in index order with a strict `<`, which reproduces the
+// stable argsort of pointnet2.py:54-72 (NaN last, ties by index) and the
+// strict cascade of kernels/pointnet2.metal:24-43.
 //
 // three_interpolate: out[b,c,n] = (f[i0]*w0 + f[i1]*w1) + f[i2]*w2
 // (kernels/pointnet2.metal:52-71).  When a group of feature rows fits LDS
@@ -20,64 +20,101 @@
 namespace pointops {
 namespace {
 
-constexpr int kTnThreads = 256;
-constexpr int kTnTile = 1024;  // known points per LDS tile (16 KiB)
+// three_nn with one lane per unknown point and NW waves per 64 unknowns, each
+// wave scanning a contiguous range of the known points through uniform
+// (scalar) loads in batches of 8, the next batch requested before the current
+// one is tested.  Keys are min(bits(d), 0x7FC00000): non-negative floats and
+// +inf keep their order and every NaN (computed NaNs are quiet, so their
+// bits are at least 0x7FC00000 or negative) becomes one key above +inf.  A lane's three best keys stay sorted in
+// registers (strict `<` in index order); the NW partial lists are merged in
+// range order with the same strict `<`, which keeps ties in index order.
+constexpr uint32_t kNanKey = 0x7FC00000u;
 
-__device__ __forceinline__ uint32_t sort_key(float d) {
-    return (d != d) ? 0x7FC00000u : static_cast<uint32_t>(f2i(d));
-}
-
-__global__ __launch_bounds__(kTnThreads) void three_nn_kernel(const float* __restrict__ unknown,
-                                                              const float* __restrict__ known,
-                                                              float* __restrict__ dist,
-                                                              int32_t* __restrict__ idx, int64_t N,
-                                                              int64_t M) {
-    __shared__ float4 tile[kTnTile];
-    const int64_t b = blockIdx.y;
-    const int64_t n = static_cast<int64_t>(blockIdx.x) * kTnThreads + threadIdx.x;
+template <int NW>
+__global__ __launch_bounds__(NW * kWave) void three_nn_lane_kernel(
+    const float* __restrict__ unknown, const float* __restrict__ known, float* __restrict__ dist,
+    int32_t* __restrict__ idx, int64_t N, int64_t M) {
+    __shared__ uint32_t pub_k[NW][3][kWave];
+    __shared__ int pub_i[NW][3][kWave];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const CloudBlock cb = cloud_block(static_cast<uint32_t>((N + kWave - 1) / kWave));
+    const int64_t b = cb.b;
+    const int64_t n = static_cast<int64_t>(cb.x) * kWave + lane;
     const bool active = n < N;
     const float* up = unknown + 3 * (b * N + (active ? n : 0));
     const float ux = up[0], uy = up[1], uz = up[2];
     const float* kp = known + 3 * b * M;
-    uint32_t k0 = 0xFFFFFFFFu, k1 = 0xFFFFFFFFu, k2 = 0xFFFFFFFFu;
+    const int span = static_cast<int>((M + NW - 1) / NW);
+    const int lo = wave * span;
+    const int hi = static_cast<int>(min<int64_t>(M, static_cast<int64_t>(lo) + span));
+    uint32_t k0 = 0xFFFFFFFFu, k1 = 0xFFFFFFFFu, k2 = active ? 0xFFFFFFFFu : 0u;
     int i0 = -1, i1 = -1, i2 = -1;
-    for (int64_t t0 = 0; t0 < M; t0 += kTnTile) {
-        const int tn = static_cast<int>(min<int64_t>(kTnTile, M - t0));
-        __syncthreads();
-        for (int t = threadIdx.x; t < tn; t += kTnThreads) {
-            const float* s = kp + 3 * (t0 + t);
-            tile[t] = make_float4(s[0], s[1], s[2], 0.f);
+    auto visit = [&](float rx, float ry, float rz, int j) {
+        const uint32_t k = min(static_cast<uint32_t>(f2i(sqdist3(ux, uy, uz, rx, ry, rz))), kNanKey);
+        if (k < k2) {  // rare once three are kept: the masked update is skipped
+            const bool b0 = k < k0, b1 = k < k1;
+            i2 = b1 ? i1 : j;
+            i1 = b0 ? i0 : (b1 ? j : i1);
+            i0 = b0 ? j : i0;
+            k2 = max(k, k1);
+            k1 = b0 ? k0 : (b1 ? k : k1);
+            k0 = min(k, k0);
         }
-        __syncthreads();
-        for (int t = 0; t < tn; ++t) {
-            const float4 c = tile[t];
-            const uint32_t k = sort_key(sqdist3(ux, uy, uz, c.x, c.y, c.z));
-            const bool take = active && k < k2;
-            if (ballot(take) == 0) continue;
-            if (take) {
-                const int j = static_cast<int>(t0) + t;
-                if (k < k0) {
-                    k2 = k1; i2 = i1;
-                    k1 = k0; i1 = i0;
-                    k0 = k;  i0 = j;
-                } else if (k < k1) {
-                    k2 = k1; i2 = i1;
-                    k1 = k;  i1 = j;
-                } else {
-                    k2 = k;  i2 = j;
-                }
+    };
+    constexpr int kBatch = 8;
+    int j0 = lo;
+    float cur[3 * kBatch];
+    if (j0 + kBatch <= hi) {
+#pragma unroll
+        for (int t = 0; t < 3 * kBatch; ++t) cur[t] = kp[3 * static_cast<int64_t>(j0) + t];
+    }
+    for (; j0 + kBatch <= hi; j0 += kBatch) {
+        float nxt[3 * kBatch];
+        const int jn = min(j0 + kBatch, hi - kBatch);  // stays inside the range
+#pragma unroll
+        for (int t = 0; t < 3 * kBatch; ++t) nxt[t] = kp[3 * static_cast<int64_t>(jn) + t];
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) visit(cur[3 * u], cur[3 * u + 1], cur[3 * u + 2], j0 + u);
+#pragma unroll
+        for (int t = 0; t < 3 * kBatch; ++t) cur[t] = nxt[t];
+    }
+    for (; j0 < hi; ++j0) {
+        const float* r = kp + 3 * static_cast<int64_t>(j0);
+        visit(r[0], r[1], r[2], j0);
+    }
+    pub_k[wave][0][lane] = k0;
+    pub_k[wave][1][lane] = k1;
+    pub_k[wave][2][lane] = k2;
+    pub_i[wave][0][lane] = i0;
+    pub_i[wave][1][lane] = i1;
+    pub_i[wave][2][lane] = i2;
+    __syncthreads();
+    if (wave != 0 || !active) return;
+#pragma unroll
+    for (int w = 1; w < NW; ++w) {
+#pragma unroll
+        for (int s = 0; s < 3; ++s) {
+            const uint32_t k = pub_k[w][s][lane];
+            const int j = pub_i[w][s][lane];
+            if (k < k2) {
+                const bool b0 = k < k0, b1 = k < k1;
+                i2 = b1 ? i1 : j;
+                i1 = b0 ? i0 : (b1 ? j : i1);
+                i0 = b0 ? j : i0;
+                k2 = max(k, k1);
+                k1 = b0 ? k0 : (b1 ? k : k1);
+                k0 = min(k, k0);
             }
         }
     }
-    if (active) {
-        const int64_t o = 3 * (b * N + n);
-        dist[o] = sqrtf(i2f(static_cast<int>(k0)));
-        dist[o + 1] = sqrtf(i2f(static_cast<int>(k1)));
-        dist[o + 2] = sqrtf(i2f(static_cast<int>(k2)));
-        idx[o] = i0;
-        idx[o + 1] = i1;
-        idx[o + 2] = i2;
-    }
+    const int64_t o = 3 * (b * N + n);
+    dist[o] = sqrtf(i2f(static_cast<int>(k0)));
+    dist[o + 1] = sqrtf(i2f(static_cast<int>(k1)));
+    dist[o + 2] = sqrtf(i2f(static_cast<int>(k2)));
+    idx[o] = i0;
+    idx[o + 1] = i1;
+    idx[o + 2] = i2;
 }
 
 constexpr int kTiThreads = 256;
@@ -384,14 +421,13 @@ extern "C" {
 
 hipError_t pointops_three_nn(const float* unknown, const float* known, float* dist, int32_t* idx,
                              int64_t B, int64_t N, int64_t M, hipStream_t stream) {
-    if (B < 0 || N < 0 || M < 0 || M > INT32_MAX) return hipErrorInvalidValue;
+    if (B < 0 || N < 0 || M < 0 || M > INT32_MAX - 64) return hipErrorInvalidValue;
     if (B == 0 || N == 0) return hipSuccess;
-    if (M < 3 || B > 65535 || (N + kTnThreads - 1) / kTnThreads > INT32_MAX)
-        return hipErrorInvalidValue;
-    const dim3 grid(static_cast<uint32_t>((N + kTnThreads - 1) / kTnThreads),
-                    static_cast<uint32_t>(B));
-    hipLaunchKernelGGL(three_nn_kernel, grid, dim3(kTnThreads), 0, stream, unknown, known, dist, idx,
-                       N, M);
+    constexpr int NW = 4;
+    const int64_t blocks = (N + kWave - 1) / kWave * B;
+    if (M < 3 || blocks > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((three_nn_lane_kernel<NW>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(NW * kWave), 0, stream, unknown, known, dist, idx, N, M);
     return hipGetLastError();
 }
 

@@ -489,6 +489,30 @@ def test_three_interpolate_backward_sequential_order(cuda_device, m, n):
         np.testing.assert_allclose(grads[0], want, rtol=1e-5, atol=1e-5)
 
 
+def test_three_nn_non_finite(cuda_device):
+    """NaN distances sort last in index order, +inf ones before them; a NaN
+    unknown takes the first three known points (stable argsort)."""
+    from mps_pointops import three_nn
+
+    u = rand_cloud(3, 300, 21)
+    k = rand_cloud(3, 70, 22)
+    k[0, 5] = float("nan")
+    k[0, 9, 1] = float("inf")
+    k[0, 10, 2] = -float("inf")
+    k[1, 2:] = float("nan")  # two finite known points: the third is the first NaN
+    k[2, :, 0] = float("inf")  # every distance is +inf or NaN
+    k[2, 40] = torch.tensor([1.0, 2.0, 3.0])
+    u[0, 3] = float("nan")
+    u[1, 7, 0] = -float("inf")
+    want_d, want_i = O.three_nn(u, k)
+    d, i = three_nn(u.cuda(), k.cuda())
+    np.testing.assert_array_equal(host(i), want_i)
+    got = host(d)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(want_d))
+    fin = ~np.isnan(want_d)
+    same_bits(got[fin], want_d[fin])
+
+
 @pytest.mark.parametrize("m", [3, 4, 50, 1025, 2100])
 def test_three_nn_matches_oracle(cuda_device, m):
     from mps_pointops import three_nn
