@@ -351,8 +351,8 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
     // Per lane and wave: the key of the wave's K-th entry, read by the other
     // waves (one lane's NW keys are contiguous: two 16-byte reads).
-    static_assert(NW == 4 || NW == 8, "admission limit reads NW keys as uint4");
-    __shared__ uint4 taus[kWave][NW / 4];
+    constexpr int kTauRows = (NW + 3) / 4;
+    __shared__ uint4 taus[kWave][kTauRows];
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
     const CloudBlock cb = cloud_block(static_cast<uint32_t>((M + kWave - 1) / kWave));
@@ -385,9 +385,9 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     // equal key from a higher range cannot beat its K-th entry, while an equal
     // key from a lower range can beat a higher range's K-th entry.
     auto limit = [&]() {
-        uint32_t t[NW];
+        uint32_t t[4 * kTauRows];
 #pragma unroll
-        for (int v = 0; v < NW / 4; ++v) {
+        for (int v = 0; v < kTauRows; ++v) {
             const uint4 q4 = taus[lane][v];
             t[4 * v] = q4.x;
             t[4 * v + 1] = q4.y;
