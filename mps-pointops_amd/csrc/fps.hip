@@ -21,8 +21,8 @@
 //   fps_large_kernel<P,T>   one cloud over up to 128 CUs (cooperative launch):
 //                           each workgroup keeps its chunk in VGPRs and
 //                           publishes a tagged (distance, index, xyz) record
-//                           per step; every workgroup polls all records and
-//                           reduces them.
+//                           per step in 8 copies; every workgroup polls all
+//                           records of one copy and reduces them.
 #include <hip/hip_cooperative_groups.h>
 
 #include "pointops_common.hpp"
@@ -274,10 +274,14 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
 // vkey = 0 when the workgroup has no candidate, else float bits + 1 (running
 // distances are >= +0 for candidates, so the bits order like the values and
 // the largest (vkey, ~idx) is the largest value with the smallest index).
-// Thread t of every workgroup polls record t, the wave reduces the keys with
-// two 32-bit DPP maxima, and a barrier combines the waves.  Fewer, larger
-// chunks (128 workgroups for a 1M-point cloud) poll less and measured faster
-// than one workgroup per CU.  Polls are bounded: after kSpinLimit attempts (or when another
+// Every record is written to 8 copies (lane r of the winning wave writes copy
+// r) and workgroup g reads copy g % 8, which spreads the polls of all
+// workgroups over 8 sets of cache lines (one shared copy measured 4.8 us per
+// step, 8 copies 3.6 us).  Thread t of every workgroup polls the key word of
+// record t until it carries the step's tag, then reads the coordinate words;
+// the wave reduces the keys with two 32-bit DPP maxima, and a barrier
+// combines the waves.  Fewer, larger chunks (128 workgroups for a 1M-point
+// cloud) poll less and measured faster than one workgroup per CU.  Polls are bounded: after kSpinLimit attempts (or when another
 // workgroup has given up) the kernel raises a status word and every workgroup
 // returns, so no launch can hang.
 constexpr int kLargeIdxBits = 21;
@@ -292,6 +296,14 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 #endif
 constexpr int kLargeThreads = POINTOPS_FPS_LARGE_THREADS;
 constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread (SoA stride)
+// Every record is written to kLargeReplicas copies, and workgroup g polls copy
+// g % kLargeReplicas, so each copy's cache lines are read by 1/kLargeReplicas
+// of the pollers instead of all of them.
+#ifndef POINTOPS_FPS_LARGE_REPLICAS
+#define POINTOPS_FPS_LARGE_REPLICAS 8
+#endif
+constexpr int kLargeReplicas = POINTOPS_FPS_LARGE_REPLICAS;
+constexpr int64_t kLargeCopyWords = 4 * kLargeMaxGrid;  // one copy: 4 words per record
 constexpr int kLargePreferredGrid = POINTOPS_FPS_LARGE_GRID;
 static_assert(kLargePreferredGrid <= kLargeMaxGrid, "one polled record per thread");
 
@@ -398,32 +410,28 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
         const int par = static_cast<int>(step & 1);
 
         // Local argmax of this workgroup's chunk: first maximum in index order.
-        int v[P], s[P];
+        int v[P];
 #pragma unroll
         for (int k = 0; k < P; ++k) {
-            md[k] = fminf(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
+            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
             v[k] = f2i(md[k]);
-            s[k] = k;
         }
+        int lm = v[0];
 #pragma unroll
-        for (int w = 1; w < P; w <<= 1) {
+        for (int k = 1; k < P; ++k) lm = max(lm, v[k]);
+        int ls = P - 1;  // first slot of this lane holding lm
 #pragma unroll
-            for (int k = 0; k + w < P; k += 2 * w) {
-                const int right = -static_cast<int>(v[k + w] > v[k]);
-                v[k] = max(v[k], v[k + w]);
-                s[k] ^= (s[k] ^ s[k + w]) & right;
-            }
-        }
-        const int wv = wave_max_i32(v[0]);
-        const int wl = static_cast<int>(__builtin_ctzll(ballot(v[0] == wv)));
-        const int wi = (wave * kWave + wl) * P + readlane(s[0], wl);
+        for (int k = P - 2; k >= 0; --k) ls = v[k] == lm ? k : ls;
+        const int wv = wave_max_i32_l63(lm);
+        const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
+        const int wi = (wave * kWave + wl) * P + readlane(ls, wl);
         if (lane == 0) slots[par][wave] = make_int2(wv, wi);
         __syncthreads();
 
         // The wave holding the workgroup's winner publishes its record: the
         // winner's coordinates are read from that lane's registers.
         const uint32_t tag = step_tag(step);
-        uint64_t* base = records + static_cast<int64_t>(par) * 4 * kLargeMaxGrid;
+        uint64_t* base = records + static_cast<int64_t>(par) * kLargeReplicas * kLargeCopyWords;
         int bv = slots[par][0].x, bi = slots[par][0].y;
 #pragma unroll
         for (int w = 1; w < NW; ++w) {
@@ -440,12 +448,12 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
             float ox = i2f(readlane(f2i(px[os]), ol));
             float oy = i2f(readlane(f2i(py[os]), ol));
             float oz = i2f(readlane(f2i(pz[os]), ol));
-            if (lane == 0) {
+            if (lane < kLargeReplicas) {  // lane r writes copy r
                 uint32_t vkey = 0;
                 if (bv != kNegInf) vkey = static_cast<uint32_t>(bv) + 1u;
                 else ox = oy = oz = 0.f;
                 const uint32_t gidx = static_cast<uint32_t>(lo + bi);
-                uint64_t* rec = base + g;
+                uint64_t* rec = base + lane * kLargeCopyWords + g;
                 __hip_atomic_store(rec + 1 * kLargeMaxGrid,
                                    (static_cast<uint64_t>(static_cast<uint32_t>(f2i(ox))) << 32) | tag,
                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -467,24 +475,28 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
         uint32_t khi = 0, klo = 0;
         int rx = 0, ry = 0, rz = 0;
         if (tid < G) {
-            const uint64_t* q = base + tid;
+            const uint64_t* q = base + (g % kLargeReplicas) * kLargeCopyWords + tid;
             for (uint32_t spins = 0;; ++spins) {
-                const RecordPoll r = poll_record(q);
-                if (record_ready(r, tag)) {
-                    take_record(r, khi, klo, rx, ry, rz);
-                    break;
+                // The key word is stored last: poll it alone, then read the
+                // coordinate words once it carries this step's tag.
+                const uint64_t w0 = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (((w0 >> kLargeIdxBits) & 0x7FFu) == tag) {
+                    const RecordPoll r = poll_record(q);
+                    if (record_ready(r, tag)) {
+                        take_record(r, khi, klo, rx, ry, rz);
+                        break;
+                    }
                 }
                 if (poll_give_up(status, spins)) {
                     abort_flag = 1;
                     break;
                 }
-                __builtin_amdgcn_s_sleep(1);
             }
         }
         // Wave maximum of (khi, klo): khi <= 0x7F800001 and klo < 2^21, so both
         // compare correctly as signed ints.
-        const int hmax = wave_max_i32(static_cast<int>(khi));
-        const int lmax = wave_max_i32(static_cast<int>(khi) == hmax ? static_cast<int>(klo) : -1);
+        const int hmax = wave_max_i32_l63(static_cast<int>(khi));
+        const int lmax = wave_max_i32_l63(static_cast<int>(khi) == hmax ? static_cast<int>(klo) : -1);
         const int rl = static_cast<int>(__builtin_ctzll(
             ballot(static_cast<int>(khi) == hmax && static_cast<int>(klo) == lmax)));
         if (lane == 0) {
@@ -625,7 +637,7 @@ size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
     // status word (padded to 256 B) + 2 parities x grid x 4 words
-    return 256 + static_cast<size_t>(2 * kLargeMaxGrid * 4) * sizeof(uint64_t);
+    return 256 + static_cast<size_t>(2 * kLargeReplicas * kLargeCopyWords) * sizeof(uint64_t);
 }
 
 hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,
