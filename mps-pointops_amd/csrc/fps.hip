@@ -18,11 +18,16 @@
 //   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
 //                           LDS: points re-read from L2, running distances in
 //                           a caller-provided scratch array.
-//   fps_large_kernel<P,T>   one cloud over up to 128 CUs (cooperative launch):
-//                           each workgroup keeps its chunk in VGPRs and
-//                           publishes a tagged (distance, index, xyz) record
-//                           per step in 8 copies; every workgroup polls all
-//                           records of one copy and reduces them.
+//   fps_lazy_kernel<P,T>    one cloud over up to 128 CUs (cooperative launch):
+//                           each workgroup keeps its chunk in VGPRs; an
+//                           exchange publishes every wave's best candidates
+//                           and a bound, after which every workgroup takes
+//                           exact steps over the candidates alone until the
+//                           bound could be reached (the product kernel).
+//   fps_large_kernel<P,T>   the same launch with a full exchange per step:
+//                           each workgroup publishes a tagged (distance,
+//                           index, xyz) record per step in 8 copies; every
+//                           workgroup polls all records of one copy.
 #include <hip/hip_cooperative_groups.h>
 
 #include "pointops_common.hpp"
@@ -531,6 +536,252 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
     }
 }
 
+// fps_lazy_kernel<P,T>: the large-cloud FPS with an exchange every few steps
+// instead of every step.  At an exchange every wave publishes its kLazyCand
+// best points (running distance, index, xyz; largest distance first, smaller
+// index first on ties) and the (kLazyCand+1)-th largest running distance of
+// its points, its bound.  Every workgroup then reads all candidates and, on
+// identical data, runs the same sequence of steps over the candidates alone:
+// the first step after an exchange is exact (each wave's first candidate is
+// its maximum, so the best candidate is the global maximum), and a later step
+// is exact while the best candidate's distance is strictly above every
+// bound, since an unpublished point's running distance is at most its wave's
+// bound (distances only decrease).  Candidate distances are updated with the
+// same arithmetic as the points.  The centroids chosen since the last
+// exchange are applied to every workgroup's own points at the next exchange
+// (a running minimum does not depend on the order).  Records carry a tag per
+// 64-bit word and are double-buffered by exchange parity, in kLargeReplicas
+// copies as in fps_large_kernel; polls are bounded.
+constexpr int kLazyCand = 2;           // candidates per wave
+constexpr int kLazyMaxPending = 64;    // steps between exchanges at most
+constexpr int kLazyRecWords = 4 * kLazyCand + 1;
+constexpr int kLazyMaxWaves = kLargeMaxGrid * (kLargeThreads / kWave);
+constexpr int64_t kLazyCopyWords = static_cast<int64_t>(kLazyRecWords) * kLazyMaxWaves;
+
+template <int P, int T>
+__global__ __launch_bounds__(T) void fps_lazy_kernel(
+    const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
+    uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk) {
+    constexpr int NW = T / kWave;
+    static_assert(NW <= 8 && P <= 32, "shape");
+    constexpr int RPT = kLazyMaxWaves / T;  // records read per thread at most
+    constexpr int CPT = RPT * kLazyCand;    // candidates held per thread at most
+    __shared__ float4 pend[kLazyMaxPending];
+    __shared__ WaveBest slots[2][8];
+    __shared__ int wave_bound[NW];
+    __shared__ int abort_flag;
+
+    const int G = gridDim.x;
+    const int waves = G * NW;  // records per exchange
+    const int g = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int lo = g * chunk;
+    const int n = max(0, min(chunk, N - lo));
+    const float* p = xyz + 3 * static_cast<int64_t>(lo);
+
+    // Small P: one spare element so that px[os] is an indexed move, not a
+    // select chain; P = 32 already is (and 33 floats would not stay in VGPRs).
+    constexpr int PA = P <= 8 ? P + 1 : P;
+    float px[PA], py[PA], pz[PA], md[P];
+#pragma unroll
+    for (int k = 0; k < PA; ++k) px[k] = py[k] = pz[k] = 0.f;
+    if (n > 0) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int jj = min(tid * P + k, n - 1);
+            px[k] = p[3 * jj];
+            py[k] = p[3 * jj + 1];
+            pz[k] = p[3 * jj + 2];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid * P + k;
+        const bool valid = j < n;
+        px[k] = valid ? px[k] : 0.f;
+        py[k] = valid ? py[k] : 0.f;
+        pz[k] = valid ? pz[k] : 0.f;
+        md[k] = !valid ? -INFINITY
+                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+    }
+    if (tid == 0) {
+        abort_flag = 0;
+        pend[0] = make_float4(xyz[3 * static_cast<int64_t>(start)],
+                              xyz[3 * static_cast<int64_t>(start) + 1],
+                              xyz[3 * static_cast<int64_t>(start) + 2], 0.f);
+        if (g == 0) out[0] = start;
+    }
+    int npend = 1;
+    int64_t step = 1;
+    int sim_par = 0;
+    for (uint32_t exch = 0; step < npoint; ++exch) {
+        __syncthreads();  // pend[] complete
+        // Apply the centroids chosen since the last exchange.
+        for (int i = 0; i < npend; ++i) {
+            const float4 c = pend[i];
+#pragma unroll
+            for (int k = 0; k < P; ++k)
+                md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z));
+        }
+        npend = 0;
+
+        // This wave's kLazyCand best points and its bound, by repeated wave
+        // maxima (first lane, then first slot, holding the maximum: the
+        // smallest index).
+        const int par = static_cast<int>(exch & 1);
+        const uint32_t tag = (exch & 0x3FFu) | 0x400u;
+        const int gw = g * NW + wave;
+        uint64_t words[kLazyRecWords];
+        uint32_t taken = 0;
+#pragma unroll
+        for (int r = 0; r <= kLazyCand; ++r) {
+            int lm = static_cast<int>(0x80000000u), ls = 0;
+#pragma unroll
+            for (int k = P - 1; k >= 0; --k) {
+                const int v = ((taken >> k) & 1u) ? static_cast<int>(0x80000000u) : f2i(md[k]);
+                ls = v >= lm ? k : ls;
+                lm = max(lm, v);
+            }
+            const int wv = wave_max_i32_l63(lm);
+            const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
+            const int os = readlane(ls, wl);
+            if (r == kLazyCand) {
+                words[4 * kLazyCand] = (static_cast<uint64_t>(static_cast<uint32_t>(wv)) << 32) | tag;
+                break;
+            }
+            const uint32_t gidx = static_cast<uint32_t>(lo + (wave * kWave + wl) * P + os);
+            const uint32_t bx = static_cast<uint32_t>(readlane(f2i(px[os]), wl));
+            const uint32_t by = static_cast<uint32_t>(readlane(f2i(py[os]), wl));
+            const uint32_t bz = static_cast<uint32_t>(readlane(f2i(pz[os]), wl));
+            words[4 * r] = (static_cast<uint64_t>(static_cast<uint32_t>(wv)) << 32) |
+                           (static_cast<uint64_t>(tag) << kLargeIdxBits) | (gidx & kLargeIdxMask);
+            words[4 * r + 1] = (static_cast<uint64_t>(bx) << 32) | tag;
+            words[4 * r + 2] = (static_cast<uint64_t>(by) << 32) | tag;
+            words[4 * r + 3] = (static_cast<uint64_t>(bz) << 32) | tag;
+            if (lane == wl) taken |= 1u << os;
+        }
+        // Lane r writes copy r; the bound word goes last.
+        uint64_t* base = records + static_cast<int64_t>(par) * kLargeReplicas * kLazyCopyWords;
+        if (lane < kLargeReplicas) {
+            uint64_t* rec = base + lane * kLazyCopyWords + gw;
+#pragma unroll
+            for (int w = 0; w < kLazyRecWords; ++w)
+                __hip_atomic_store(rec + static_cast<int64_t>(w) * kLazyMaxWaves, words[w],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+
+        // Read every wave's record (copy g % kLargeReplicas).
+        const uint64_t* copy = base + (g % kLargeReplicas) * kLazyCopyWords;
+        int cmd[CPT], cidx[CPT];
+        float cx_[CPT], cy_[CPT], cz_[CPT];
+        int bmax = static_cast<int>(0x80000000u);
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+            const int rw = tid + j * T;
+#pragma unroll
+            for (int c = 0; c < kLazyCand; ++c) {
+                cmd[j * kLazyCand + c] = static_cast<int>(0x80000000u);
+                cidx[j * kLazyCand + c] = 0x7FFFFFFF;
+                cx_[j * kLazyCand + c] = cy_[j * kLazyCand + c] = cz_[j * kLazyCand + c] = 0.f;
+            }
+            if (rw >= waves) continue;
+            const uint64_t* q = copy + rw;
+            for (uint32_t spins = 0;; ++spins) {
+                const uint64_t wb = __hip_atomic_load(q + static_cast<int64_t>(kLazyRecWords - 1) * kLazyMaxWaves,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (static_cast<uint32_t>(wb) == tag) {
+                    uint64_t rw_[kLazyRecWords - 1];
+                    bool ok = true;
+#pragma unroll
+                    for (int w = 0; w < kLazyRecWords - 1; ++w) {
+                        rw_[w] = __hip_atomic_load(q + static_cast<int64_t>(w) * kLazyMaxWaves,
+                                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                        const uint32_t t = (w % 4 == 0)
+                                               ? static_cast<uint32_t>((rw_[w] >> kLargeIdxBits) & 0x7FFu)
+                                               : static_cast<uint32_t>(rw_[w]);
+                        ok = ok && t == tag;
+                    }
+                    if (ok) {
+                        bmax = max(bmax, static_cast<int>(wb >> 32));
+#pragma unroll
+                        for (int c = 0; c < kLazyCand; ++c) {
+                            cmd[j * kLazyCand + c] = static_cast<int>(rw_[4 * c] >> 32);
+                            cidx[j * kLazyCand + c] = static_cast<int>(rw_[4 * c] & kLargeIdxMask);
+                            cx_[j * kLazyCand + c] = i2f(static_cast<int>(rw_[4 * c + 1] >> 32));
+                            cy_[j * kLazyCand + c] = i2f(static_cast<int>(rw_[4 * c + 2] >> 32));
+                            cz_[j * kLazyCand + c] = i2f(static_cast<int>(rw_[4 * c + 3] >> 32));
+                        }
+                        break;
+                    }
+                }
+                if (poll_give_up(status, spins)) {
+                    abort_flag = 1;
+                    break;
+                }
+            }
+        }
+        bmax = wave_max_i32_l63(bmax);
+        if (lane == 0) wave_bound[wave] = bmax;
+        __syncthreads();
+        if (abort_flag) return;  // uniform: written before the barrier
+        int bound = wave_bound[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) bound = max(bound, wave_bound[w]);
+
+        // Steps over the candidates alone.
+        for (bool first = true; step < npoint; first = false) {
+            int bv = static_cast<int>(0x80000000u), bi = 0x7FFFFFFF;
+            float bx = 0.f, by = 0.f, bz = 0.f;
+#pragma unroll
+            for (int j = 0; j < CPT; ++j) {
+                const bool better = cmd[j] > bv || (cmd[j] == bv && cidx[j] < bi);
+                bv = better ? cmd[j] : bv;
+                bi = better ? cidx[j] : bi;
+                bx = better ? cx_[j] : bx;
+                by = better ? cy_[j] : by;
+                bz = better ? cz_[j] : bz;
+            }
+            const int wv = wave_max_i32_l63(bv);
+            const int wneg = wave_max_i32_l63(bv == wv ? -bi : static_cast<int>(0x80000000u));
+            const int wl = static_cast<int>(__builtin_ctzll(ballot(bv == wv && -bi == wneg)));
+            WaveBest* buf = slots[sim_par];
+            sim_par ^= 1;
+            const float wx = i2f(readlane(f2i(bx), wl));
+            const float wy = i2f(readlane(f2i(by), wl));
+            const float wz = i2f(readlane(f2i(bz), wl));
+            if (lane == 0) {
+                WaveBest e;
+                e.key = wv;
+                e.index = -wneg;
+                e.x = wx;
+                e.y = wy;
+                e.z = wz;
+                e.pad[0] = e.pad[1] = e.pad[2] = 0;
+                buf[wave] = e;
+            }
+            __syncthreads();
+            WaveBest best = buf[0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                const WaveBest e = buf[w];
+                if (e.key > best.key || (e.key == best.key && e.index < best.index)) best = e;
+            }
+            if (!first && !(best.key > bound)) break;  // an unpublished point may tie or beat it
+            if (g == 0 && tid == 0) out[step] = best.index;
+            if (tid == 0) pend[npend] = make_float4(best.x, best.y, best.z, 0.f);
+            ++npend;
+            ++step;
+#pragma unroll
+            for (int j = 0; j < CPT; ++j)
+                cmd[j] = f2i(running_min(i2f(cmd[j]),
+                                         sqdist3(cx_[j], cy_[j], cz_[j], best.x, best.y, best.z)));
+            if (npend == kLazyMaxPending) break;
+        }
+    }
+}
+
 // ------------------------------------------------------------ dispatch
 
 constexpr int kRegsThreads = 512;  // 8 waves: two per SIMD hide each other's reduction latency
@@ -568,23 +819,31 @@ hipError_t launch_fps(const float* xyz, const int64_t* ptr, const int64_t* out_p
     return hipGetLastError();
 }
 
+#ifndef POINTOPS_FPS_LAZY
+#define POINTOPS_FPS_LAZY 1
+#endif
+
+// The persistent large-cloud kernel for P points per thread.
+template <int P>
+const void* large_kernel() {
+    if (POINTOPS_FPS_LAZY) return reinterpret_cast<const void*>(&fps_lazy_kernel<P, kLargeThreads>);
+    return reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>);
+}
+
 template <int P>
 hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint32_t* status,
                         int N, int64_t npoint, int start, int skip, int chunk, int grid,
                         hipStream_t stream) {
     void* args[] = {(void*)&xyz, (void*)&out, (void*)&records, (void*)&status, (void*)&N,
                     (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk};
-    return hipLaunchCooperativeKernel(
-        reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>), dim3(grid),
-        dim3(kLargeThreads), args, 0, stream);
+    return hipLaunchCooperativeKernel(large_kernel<P>(), dim3(grid), dim3(kLargeThreads), args, 0,
+                                      stream);
 }
 
 template <int P>
 int large_capacity(int device) {
     int per_cu = 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &per_cu, reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>),
-            kLargeThreads, 0) !=
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, large_kernel<P>(), kLargeThreads, 0) !=
         hipSuccess)
         return 0;
     int cus = 0;
@@ -636,8 +895,9 @@ hipError_t pointops_fps_flat(const float* x, const int64_t* ptr, const int64_t* 
 size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
-    // status word (padded to 256 B) + 2 parities x grid x 4 words
-    return 256 + static_cast<size_t>(2 * kLargeReplicas * kLargeCopyWords) * sizeof(uint64_t);
+    // status word (padded to 256 B) + 2 parities x copies x records
+    const int64_t words = 2 * kLargeReplicas * (POINTOPS_FPS_LAZY ? kLazyCopyWords : kLargeCopyWords);
+    return 256 + static_cast<size_t>(words) * sizeof(uint64_t);
 }
 
 hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,

@@ -243,6 +243,31 @@ def test_fps_large_matches_oracle(cuda_device, n):
         np.testing.assert_array_equal(host(got), want)
 
 
+@pytest.mark.parametrize("case", ["long", "exhausted", "mostly_skipped"])
+def test_fps_large_long_runs(cuda_device, case):
+    """Many exchanges of the persistent kernel: a long run on a random cloud,
+    a run past the number of distinct points (every remaining distance ties
+    at zero), and a cloud whose points are nearly all skipped."""
+    import mps_pointops as mp
+
+    g = torch.Generator().manual_seed({"long": 1, "exhausted": 2, "mostly_skipped": 3}[case])
+    skip = case == "mostly_skipped"
+    if case == "long":
+        xyz = torch.randn(1, 100_000, 3, generator=g)
+        npoint, start = 3000, 12345
+    elif case == "exhausted":
+        base = torch.randn(400, 3, generator=g)
+        xyz = base[torch.randint(0, 400, (20_000,), generator=g)][None].contiguous()
+        npoint, start = 600, 7
+    else:
+        xyz = torch.randn(1, 30_000, 3, generator=g) * 1e-3
+        xyz[0, ::1000] = torch.randn(30, 3, generator=g)
+        npoint, start = 100, 0
+    want = O.fps(xyz, npoint, start, skip)
+    got = mp.furthest_point_sample(xyz.cuda(), npoint, start, skip, strategy="multigroup")
+    np.testing.assert_array_equal(host(got), want)
+
+
 def test_fps_skip_near_origin_boundary(cuda_device):
     """tests/test_compat.py:96-111: points just inside the 1e-3 radius are
     never picked, the one just outside is."""
