@@ -20,7 +20,7 @@
 //                           a caller-provided scratch array.
 //   fps_lazy_kernel<P,T>    one cloud over up to 128 CUs (cooperative launch):
 //                           each workgroup keeps its chunk in VGPRs; an
-//                           exchange publishes every wave's best candidates
+//                           exchange publishes every wave's best candidate
 //                           and a bound, after which every workgroup takes
 //                           exact steps over the candidates alone until the
 //                           bound could be reached (the product kernel).
@@ -285,8 +285,9 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
 // step, 8 copies 3.6 us).  Thread t of every workgroup polls the key word of
 // record t until it carries the step's tag, then reads the coordinate words;
 // the wave reduces the keys with two 32-bit DPP maxima, and a barrier
-// combines the waves.  Fewer, larger chunks (128 workgroups for a 1M-point
-// cloud) poll less and measured faster than one workgroup per CU.  Polls are bounded: after kSpinLimit attempts (or when another
+// combines the waves.  (With an exchange per step, 128 workgroups for a
+// 1M-point cloud polled less and measured faster than 256; the lazy kernel
+// below exchanges rarely and uses one workgroup per CU.)  Polls are bounded: after kSpinLimit attempts (or when another
 // workgroup has given up) the kernel raises a status word and every workgroup
 // returns, so no launch can hang.
 constexpr int kLargeIdxBits = 21;
@@ -297,7 +298,7 @@ constexpr uint32_t kSpinLimit = 1u << 22;
 #define POINTOPS_FPS_LARGE_THREADS 256
 #endif
 #ifndef POINTOPS_FPS_LARGE_GRID
-#define POINTOPS_FPS_LARGE_GRID 128  // fewer, larger chunks: less poll traffic per step
+#define POINTOPS_FPS_LARGE_GRID 256  // one workgroup per CU (the lazy exchange is rare)
 #endif
 constexpr int kLargeThreads = POINTOPS_FPS_LARGE_THREADS;
 constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread (SoA stride)
@@ -552,8 +553,14 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
 // (a running minimum does not depend on the order).  Records carry a tag per
 // 64-bit word and are double-buffered by exchange parity, in kLargeReplicas
 // copies as in fps_large_kernel; polls are bounded.
-constexpr int kLazyCand = 2;           // candidates per wave
-constexpr int kLazyMaxPending = 64;    // steps between exchanges at most
+#ifndef POINTOPS_FPS_LAZY_CAND
+#define POINTOPS_FPS_LAZY_CAND 1
+#endif
+#ifndef POINTOPS_FPS_LAZY_PENDING
+#define POINTOPS_FPS_LAZY_PENDING 64
+#endif
+constexpr int kLazyCand = POINTOPS_FPS_LAZY_CAND;           // candidates per wave
+constexpr int kLazyMaxPending = POINTOPS_FPS_LAZY_PENDING;  // steps between exchanges at most
 constexpr int kLazyRecWords = 4 * kLazyCand + 1;
 constexpr int kLazyMaxWaves = kLargeMaxGrid * (kLargeThreads / kWave);
 constexpr int64_t kLazyCopyWords = static_cast<int64_t>(kLazyRecWords) * kLazyMaxWaves;
