@@ -213,6 +213,141 @@ __global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ x
     }
 }
 
+// fps_lazy_regs_kernel<P,T>: the batched kernel with the exchange of
+// fps_lazy_kernel inside one workgroup.  At an exchange every wave extracts
+// its KC = 64 / NW best points (largest running distance, then smallest
+// index) and the (KC+1)-th largest running distance, its bound, into LDS;
+// after one barrier every wave holds all 64 candidates, one per lane, and
+// takes steps on its own -- no barrier -- choosing the candidate with the
+// largest distance (smallest index on ties), updating its own points and the
+// candidates with it, while the choice is provably the exact argmax: always
+// for the first step after an exchange, and afterwards while the chosen
+// distance is strictly above every wave's bound.  All waves see the same
+// candidates, so they take the same steps.
+template <int P, int T>
+__global__ __launch_bounds__(T) void fps_lazy_regs_kernel(const float* __restrict__ xyz,
+                                                          const int64_t* __restrict__ ptr,
+                                                          const int64_t* __restrict__ out_ptr,
+                                                          const int64_t* __restrict__ starts,
+                                                          int64_t* __restrict__ out, int64_t N,
+                                                          int64_t npoint, int64_t start, int skip) {
+    constexpr int NW = T / kWave;
+    constexpr int KC = kWave / NW;  // candidates per wave
+    static_assert(KC * NW == kWave && KC + 1 <= kWave, "one candidate per lane");
+    __shared__ WaveBest cands[kWave];
+    __shared__ int bounds[NW];
+
+    const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
+    if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
+    const float* p = xyz + 3 * seg.in_lo;
+    int64_t* o = out + seg.out_lo;
+    const int n = static_cast<int>(seg.n);
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+
+    constexpr int PA = P <= 8 ? P + 1 : P;  // see fps_lazy_kernel
+    float px[PA], py[PA], pz[PA];
+    float md[P];
+#pragma unroll
+    for (int k = 0; k < PA; ++k) px[k] = py[k] = pz[k] = 0.f;
+    const int far0 = static_cast<int>(seg.start);
+    float cx = 0.f, cy = 0.f, cz = 0.f;
+    if (n > 0) {
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            const int jj = min(tid * P + k, n - 1);
+            px[k] = p[3 * jj];
+            py[k] = p[3 * jj + 1];
+            pz[k] = p[3 * jj + 2];
+        }
+        const int f = min(max(far0, 0), n - 1);
+        cx = p[3 * f];
+        cy = p[3 * f + 1];
+        cz = p[3 * f + 2];
+    }
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = tid * P + k;
+        const bool valid = j < n;
+        px[k] = valid ? px[k] : 0.f;
+        py[k] = valid ? py[k] : 0.f;
+        pz[k] = valid ? pz[k] : 0.f;
+        md[k] = !valid ? -INFINITY
+                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+        md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
+    }
+    if (tid == 0) o[0] = seg.base + far0;
+    int64_t step = 1;
+    while (step < seg.cnt) {
+        // Exchange: this wave's KC best points and its bound.
+        uint32_t taken = 0;
+        int bound = 0;
+#pragma unroll
+        for (int r = 0; r <= KC; ++r) {
+            int lm = static_cast<int>(0x80000000u), ls = 0;
+#pragma unroll
+            for (int k = P - 1; k >= 0; --k) {
+                const int v = ((taken >> k) & 1u) ? static_cast<int>(0x80000000u) : f2i(md[k]);
+                ls = v >= lm ? k : ls;
+                lm = max(lm, v);
+            }
+            const int wv = wave_max_i32_l63(lm);
+            const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
+            const int os = readlane(ls, wl);
+            if (r == KC) {
+                bound = wv;
+                break;
+            }
+            const float bx = i2f(readlane(f2i(px[os]), wl));
+            const float by = i2f(readlane(f2i(py[os]), wl));
+            const float bz = i2f(readlane(f2i(pz[os]), wl));
+            if (lane == 0) {
+                WaveBest e;
+                e.key = wv;
+                e.index = (wave * kWave + wl) * P + os;
+                e.x = bx;
+                e.y = by;
+                e.z = bz;
+                e.pad[0] = e.pad[1] = e.pad[2] = 0;
+                cands[wave * KC + r] = e;
+            }
+            if (lane == wl) taken |= 1u << os;
+        }
+        if (lane == 0) bounds[wave] = bound;
+        __syncthreads();
+        const WaveBest mine = cands[lane];
+        int maxb = bounds[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) maxb = max(maxb, bounds[w]);
+        __syncthreads();  // every wave has read the candidates before any rewrites them
+        int cmd = mine.key;
+        const int cidx = mine.index;
+        const float ccx = mine.x, ccy = mine.y, ccz = mine.z;
+        for (bool first = true; step < seg.cnt; first = false) {
+            const int wv = wave_max_i32_l63(cmd);
+            if (!first && !(wv > maxb)) break;  // an unpublished point may tie or beat it
+            // Ties (rare) go to the smallest index, whatever lane holds it.
+            const uint64_t at_max = ballot(cmd == wv);
+            int wl = static_cast<int>(__builtin_ctzll(at_max));
+            if (__popcll(at_max) > 1) {
+                const int wneg = wave_max_i32_l63(cmd == wv ? -cidx : static_cast<int>(0x80000000u));
+                wl = static_cast<int>(__builtin_ctzll(ballot(cmd == wv && -cidx == wneg)));
+            }
+            const int fidx = readlane(cidx, wl);
+            const float fx = i2f(readlane(f2i(ccx), wl));
+            const float fy = i2f(readlane(f2i(ccy), wl));
+            const float fz = i2f(readlane(f2i(ccz), wl));
+            if (tid == 0) o[step] = seg.base + fidx;
+            ++step;
+#pragma unroll
+            for (int k = 0; k < P; ++k)
+                md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], fx, fy, fz));
+            cmd = f2i(running_min(i2f(cmd), sqdist3(ccx, ccy, ccz, fx, fy, fz)));
+        }
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__ xyz,
                                                        const int64_t* __restrict__ ptr,
@@ -799,9 +934,17 @@ template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream) {
-    hipLaunchKernelGGL((fps_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
-                       dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                       start, skip);
+#ifndef POINTOPS_FPS_LAZY_REGS
+#define POINTOPS_FPS_LAZY_REGS 1
+#endif
+    if (POINTOPS_FPS_LAZY_REGS)
+        hipLaunchKernelGGL((fps_lazy_regs_kernel<P, kRegsThreads>),
+                           dim3(static_cast<uint32_t>(blocks)), dim3(kRegsThreads), 0, stream, xyz,
+                           ptr, out_ptr, starts, out, N, npoint, start, skip);
+    else
+        hipLaunchKernelGGL((fps_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                           start, skip);
     return hipGetLastError();
 }
 

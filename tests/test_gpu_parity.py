@@ -243,6 +243,22 @@ def test_fps_large_matches_oracle(cuda_device, n):
         np.testing.assert_array_equal(host(got), want)
 
 
+@pytest.mark.parametrize("n,distinct", [(4096, 300), (1000, 40), (8192, 3000)])
+def test_fps_dense_repeated_points(cuda_device, n, distinct):
+    """Clouds built from few distinct points (equal distances everywhere, and
+    more samples than distinct points): ties must go to the smallest index."""
+    import mps_pointops as mp
+
+    g = torch.Generator().manual_seed(n + distinct)
+    base = torch.randn(distinct, 3, generator=g)
+    xyz = base[torch.randint(0, distinct, (3, n), generator=g)].contiguous()
+    npoint = min(n, distinct + 200)
+    for start, skip in ((0, False), (n // 3, False), (5, True)):
+        want = O.fps(xyz, npoint, start, skip)
+        got = mp.furthest_point_sample(xyz.cuda(), npoint, start, skip)
+        np.testing.assert_array_equal(host(got), want)
+
+
 @pytest.mark.parametrize("case", ["long", "exhausted", "mostly_skipped"])
 def test_fps_large_long_runs(cuda_device, case):
     """Many exchanges of the persistent kernel: a long run on a random cloud,
