@@ -280,18 +280,20 @@ __global__ __launch_bounds__(T) void fps_lazy_regs_kernel(const float* __restric
     if (tid == 0) o[0] = seg.base + far0;
     int64_t step = 1;
     while (step < seg.cnt) {
-        // Exchange: this wave's KC best points and its bound.
-        uint32_t taken = 0;
+        // Exchange: this wave's KC best points and its bound.  av[] holds
+        // the running distances not yet taken (taken ones read INT_MIN).
+        int av[PA];
+#pragma unroll
+        for (int k = 0; k < PA; ++k) av[k] = k < P ? f2i(md[k]) : static_cast<int>(0x80000000u);
         int bound = 0;
 #pragma unroll
         for (int r = 0; r <= KC; ++r) {
-            int lm = static_cast<int>(0x80000000u), ls = 0;
+            int lm = av[0];
 #pragma unroll
-            for (int k = P - 1; k >= 0; --k) {
-                const int v = ((taken >> k) & 1u) ? static_cast<int>(0x80000000u) : f2i(md[k]);
-                ls = v >= lm ? k : ls;
-                lm = max(lm, v);
-            }
+            for (int k = 1; k < P; ++k) lm = max(lm, av[k]);
+            int ls = P - 1;
+#pragma unroll
+            for (int k = P - 2; k >= 0; --k) ls = av[k] == lm ? k : ls;
             const int wv = wave_max_i32_l63(lm);
             const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
             const int os = readlane(ls, wl);
@@ -312,7 +314,7 @@ __global__ __launch_bounds__(T) void fps_lazy_regs_kernel(const float* __restric
                 e.pad[0] = e.pad[1] = e.pad[2] = 0;
                 cands[wave * KC + r] = e;
             }
-            if (lane == wl) taken |= 1u << os;
+            av[os] = lane == wl ? static_cast<int>(0x80000000u) : av[os];
         }
         if (lane == 0) bounds[wave] = bound;
         __syncthreads();
