@@ -75,6 +75,19 @@ __device__ __forceinline__ float wave_max(float v) {
     return fmaxf(fmaxf(a, b), fmaxf(c, d));
 }
 
+// Minimum over the wave of a float with no NaN; every lane gets the result.
+__device__ __forceinline__ float wave_min(float v) {
+    v = fminf(v, i2f(dpp<kDppQuadXor1>(f2i(v))));
+    v = fminf(v, i2f(dpp<kDppQuadXor2>(f2i(v))));
+    v = fminf(v, i2f(dpp<kDppRowHalfMirror>(f2i(v))));
+    v = fminf(v, i2f(dpp<kDppRowMirror>(f2i(v))));
+    const float a = i2f(readlane(f2i(v), 0));
+    const float b = i2f(readlane(f2i(v), 16));
+    const float c = i2f(readlane(f2i(v), 32));
+    const float d = i2f(readlane(f2i(v), 48));
+    return fminf(fminf(a, b), fminf(c, d));
+}
+
 // Maximum over the wave of a signed int; every lane gets the result.
 __device__ __forceinline__ int wave_max_i32(int v) {
     v = max(v, dpp<kDppQuadXor1>(v));
