@@ -76,6 +76,18 @@ hipError_t pointops_fps_flat(const float *x, const int64_t *ptr, const int64_t *
 hipError_t pointops_knn3(const float *query, const float *ref, float *dist, int64_t *idx,
                          int64_t B, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
+/* The same search (identical results) over a uniform grid, for large clouds
+ * and 1 <= K <= 32: the references and queries are counting-sorted by cell
+ * into `workspace` (pointops_knn3_grid_workspace_bytes(B, M, N) bytes, no
+ * initialisation needed; B <= 65535) and each query scans the box of cells
+ * around it, grown face by face until no unscanned reference can be nearer
+ * than its K-th neighbour.  Replaces ops.py:195-199
+ * (kernels/knn.metal:32-140), like pointops_knn3. */
+size_t pointops_knn3_grid_workspace_bytes(int64_t B, int64_t M, int64_t N);
+hipError_t pointops_knn3_grid(const float *query, const float *ref, float *dist, int64_t *idx,
+                              void *workspace, int64_t B, int64_t M, int64_t N, int64_t K,
+                              hipStream_t stream);
+
 /* Dense exact kNN in D dimensions (sequential per-dimension accumulation).
  * Replaces ops.py:200-204 (kernels/feature_knn.metal:133-164).  Non-finite
  * queries and non-finite distances never match; unfilled slots are (inf, -1). */

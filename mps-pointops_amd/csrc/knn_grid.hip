@@ -1,0 +1,760 @@
+// Exact 3-D kNN over a uniform grid, for large clouds (K <= 32).
+//
+// The result is the brute-force one of kernels/knn.metal:32-140 (neighbours
+// sorted by float32 squared distance, then index; NaN distances never match;
+// unfilled slots (inf, 2^32-1)); the grid only decides which references are
+// examined.  Every comparison uses the (key, index) pair, key = bits of the
+// squared distance, so the visit order does not matter.
+//
+// Per batch, in a caller-provided workspace:
+//   1. grid_bounds_kernel: bounding box of the finite references, a cell side
+//      for about grid_per_cell(K) references per cell, and the count of
+//      references with a non-finite coordinate;
+//   2. counting sort of the references by cell (x fastest), the non-finite
+//      ones in an overflow cell after the last, and of the queries by
+//      2 x 2 x 2 block of cells;
+//   3. knn3_grid_kernel: one lane per query, 64 consecutive queries of the
+//      sorted order (neighbours in space) per wave.  Each lane scans the
+//      3 x 3 x 3 box of cells around its own query and stops once its K-th
+//      squared distance is below that of the nearest unscanned cell face,
+//      less a slack for float rounding (box_bound), else grows the box by
+//      that face.  A non-finite query, a batch with
+//      non-finite references, or a lane that needs more than kGridMaxGrow
+//      faces make the wave scan every reference.
+#include <algorithm>
+
+#include "pointops_common.hpp"
+#include "pointops_hip.h"
+
+namespace pointops {
+namespace {
+
+constexpr int kGridPrepThreads = 256;
+constexpr int kGridBoundBlocks = 256;  // bounding-box partials per batch, at most
+constexpr int kGridScanTile = 8 * kGridPrepThreads;
+constexpr int kGridMaxDim = 1024;
+constexpr int kGridSearchWaves = 4;
+constexpr int kGridCap = 16;  // buffered candidates per lane
+constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
+constexpr int kGridTile = 256;  // references per LDS tile (4 KiB per wave)
+constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
+constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
+
+struct alignas(16) GridParams {
+    float lo[3];
+    float inv_h;
+    int dims[3];
+    int cells;
+    int nonfinite;
+    int pad[7];
+};
+static_assert(sizeof(GridParams) == 64, "workspace layout");
+
+// Cell capacity of one batch's grid (the overflow cell comes after it).
+__host__ __device__ inline int64_t grid_cell_cap(int64_t N) { return N / 2 > 64 ? N / 2 : 64; }
+
+// References per cell the grid aims at for K neighbours: the 3 x 3 x 3 box
+// around a query then holds about 27 of them and, for evenly spread points,
+// almost always the K nearest (the ball of radius one cell side holds about
+// 4.2 of them).
+__host__ __device__ inline double grid_per_cell(int K) { return K * 0.4 > 3.0 ? K * 0.4 : 3.0; }
+
+struct GridLayout {
+    GridParams* params;
+    float* partial;  // [B][kGridBoundBlocks][8]: bounding-box partials
+    int* ref_off;    // [B][stride]: cell counts, then offsets
+    int* q_off;      // [B][stride]
+    int* tile_sum;   // [B][2][tiles]: per-tile totals of the two scans
+    int* ref_rank;   // [B][N]: rank of each reference within its cell
+    int* q_rank;     // [B][M]
+    float4* sorted;  // [B][N]: x, y, z, index bits
+    int* q_order;    // [B][M]
+    int64_t stride;  // cap + 2 rounded up to whole 16-byte words
+    int64_t tiles;   // scan tiles per array
+};
+
+__host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
+
+__host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_t N,
+                                                    GridLayout* out, char* base) {
+    const int64_t stride = (grid_cell_cap(N) + 2 + 3) & ~int64_t(3);
+    const int64_t tiles = (stride + kGridScanTile - 1) / kGridScanTile;
+    size_t o = 0;
+    auto take = [&](size_t bytes) {
+        const size_t at = o;
+        o = align256(o + bytes);
+        return at;
+    };
+    const size_t p_params = take(static_cast<size_t>(B) * sizeof(GridParams));
+    const size_t p_part = take(static_cast<size_t>(B) * kGridBoundBlocks * 8 * sizeof(float));
+    const size_t p_roff = take(static_cast<size_t>(B * stride) * sizeof(int));
+    const size_t p_qoff = take(static_cast<size_t>(B * stride) * sizeof(int));
+    const size_t p_tsum = take(static_cast<size_t>(B * 2 * tiles) * sizeof(int));
+    const size_t p_rrank = take(static_cast<size_t>(B * N) * sizeof(int));
+    const size_t p_qrank = take(static_cast<size_t>(B * M) * sizeof(int));
+    const size_t p_sorted = take(static_cast<size_t>(B * N) * sizeof(float4));
+    const size_t p_qord = take(static_cast<size_t>(B * M) * sizeof(int));
+    if (out != nullptr) {
+        out->params = reinterpret_cast<GridParams*>(base + p_params);
+        out->partial = reinterpret_cast<float*>(base + p_part);
+        out->ref_off = reinterpret_cast<int*>(base + p_roff);
+        out->q_off = reinterpret_cast<int*>(base + p_qoff);
+        out->tile_sum = reinterpret_cast<int*>(base + p_tsum);
+        out->ref_rank = reinterpret_cast<int*>(base + p_rrank);
+        out->q_rank = reinterpret_cast<int*>(base + p_qrank);
+        out->sorted = reinterpret_cast<float4*>(base + p_sorted);
+        out->q_order = reinterpret_cast<int*>(base + p_qord);
+        out->stride = stride;
+        out->tiles = tiles;
+    }
+    return o;
+}
+
+__device__ __forceinline__ bool finite3(float x, float y, float z) {
+    return isfinite(x) && isfinite(y) && isfinite(z);
+}
+
+__device__ __forceinline__ int cell_axis(float v, float lo, float inv_h, int dim) {
+    const float t = floorf((v - lo) * inv_h);
+    return static_cast<int>(fminf(fmaxf(t, 0.f), static_cast<float>(dim - 1)));
+}
+
+// Query order key: the 2 x 2 x 2 block of cells holding the point (blocks
+// in x-fastest order), so that 64 consecutive queries form a compact group;
+// non-finite queries go to block 0.  Keys stay below the cell count.
+__device__ __forceinline__ int query_key(const GridParams& P, float x, float y, float z) {
+    if (!finite3(x, y, z)) return 0;
+    const int bx = cell_axis(x, P.lo[0], P.inv_h, P.dims[0]) >> 1;
+    const int by = cell_axis(y, P.lo[1], P.inv_h, P.dims[1]) >> 1;
+    const int bz = cell_axis(z, P.lo[2], P.inv_h, P.dims[2]) >> 1;
+    const int nbx = (P.dims[0] + 1) >> 1, nby = (P.dims[1] + 1) >> 1;
+    return bx + nbx * (by + nby * bz);
+}
+
+// Cell of a point; non-finite points go to the overflow cell `cells`.
+__device__ __forceinline__ int cell_of(const GridParams& P, float x, float y, float z) {
+    if (!finite3(x, y, z)) return P.cells;
+    const int cx = cell_axis(x, P.lo[0], P.inv_h, P.dims[0]);
+    const int cy = cell_axis(y, P.lo[1], P.inv_h, P.dims[1]);
+    const int cz = cell_axis(z, P.lo[2], P.inv_h, P.dims[2]);
+    return cx + P.dims[0] * (cy + P.dims[1] * cz);
+}
+
+// Per (block, batch): zero a share of the two count arrays and reduce a
+// share of the references to a bounding-box partial (min xyz, max xyz, count
+// of references with a non-finite coordinate).
+__global__ __launch_bounds__(kGridPrepThreads) void grid_bounds_kernel(const float* __restrict__ ref,
+                                                                       GridLayout L, int64_t N) {
+    __shared__ float red[7][kGridPrepThreads / kWave];
+    const int64_t b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int64_t first = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + tid;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kGridPrepThreads;
+    for (int64_t e = first; e < L.stride; e += step) {
+        L.ref_off[b * L.stride + e] = 0;
+        L.q_off[b * L.stride + e] = 0;
+    }
+    const float* r = ref + 3 * b * N;
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    int bad = 0;
+    for (int64_t j = first; j < N; j += step) {
+        const float x = r[3 * j], y = r[3 * j + 1], z = r[3 * j + 2];
+        if (finite3(x, y, z)) {
+            mn[0] = fminf(mn[0], x); mx[0] = fmaxf(mx[0], x);
+            mn[1] = fminf(mn[1], y); mx[1] = fmaxf(mx[1], y);
+            mn[2] = fminf(mn[2], z); mx[2] = fmaxf(mx[2], z);
+        } else {
+            ++bad;
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float wmn = wave_min(mn[a]), wmx = wave_max(mx[a]);
+        if (lane == 0) {
+            red[a][wave] = wmn;
+            red[3 + a][wave] = wmx;
+        }
+    }
+    int nb = bad;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) nb += __shfl_xor(nb, d);
+    if (lane == 0) red[6][wave] = i2f(nb);
+    __syncthreads();
+    if (tid >= 8) return;
+    float v;
+    if (tid < 6) {
+        v = red[tid][0];
+        for (int w = 1; w < kGridPrepThreads / kWave; ++w)
+            v = tid < 3 ? fminf(v, red[tid][w]) : fmaxf(v, red[tid][w]);
+    } else if (tid == 6) {
+        int t = 0;
+        for (int w = 0; w < kGridPrepThreads / kWave; ++w) t += f2i(red[6][w]);
+        v = i2f(t);
+    } else {
+        v = 0.f;
+    }
+    L.partial[(b * kGridBoundBlocks + blockIdx.x) * 8 + tid] = v;
+}
+
+// One wave per batch: combine the `parts` partials into the bounding box of
+// the finite references and choose the grid.
+__global__ __launch_bounds__(kWave) void grid_params_kernel(GridLayout L, int64_t N, int parts,
+                                                            int K) {
+    const int64_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    int nonfinite = 0;
+    for (int i = lane; i < parts; i += kWave) {
+        const float* t = L.partial + (b * kGridBoundBlocks + i) * 8;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            mn[a] = fminf(mn[a], t[a]);
+            mx[a] = fmaxf(mx[a], t[3 + a]);
+        }
+        nonfinite += f2i(t[6]);
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        mn[a] = wave_min(mn[a]);
+        mx[a] = wave_max(mx[a]);
+    }
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) nonfinite += __shfl_xor(nonfinite, d);
+    if (lane != 0) return;
+    float lo[3], ext[3];
+    bool any = true;
+    for (int a = 0; a < 3; ++a) {
+        any = any && mn[a] <= mx[a];
+        lo[a] = any ? mn[a] : 0.f;
+        ext[a] = any ? mx[a] - mn[a] : 0.f;
+    }
+    GridParams P;
+    const int64_t cap = grid_cell_cap(N);
+    const float emax = fmaxf(fmaxf(ext[0], ext[1]), ext[2]);
+    float hside = 1.f;
+    if (any && emax > 0.f && emax < INFINITY) {
+        const float thin = emax * 1e-3f;
+        const double vol = static_cast<double>(fmaxf(ext[0], thin)) * fmaxf(ext[1], thin) *
+                           fmaxf(ext[2], thin);
+        const double target = fmax(1.0, fmin(static_cast<double>(cap),
+                                             static_cast<double>(N) / grid_per_cell(K)));
+        hside = static_cast<float>(cbrt(vol / target));
+        if (!(hside > 0.f)) hside = emax;
+    }
+    int dims[3] = {1, 1, 1};
+    bool fits = false;
+    for (int it = 0; it < 200 && !fits; ++it) {
+        int64_t total = 1;
+        for (int a = 0; a < 3; ++a) {
+            const float t = ext[a] / hside;
+            dims[a] = (t < static_cast<float>(kGridMaxDim - 1)) ? static_cast<int>(t) + 1 : kGridMaxDim;
+            total *= dims[a];
+        }
+        fits = total <= cap;
+        hside *= 1.25f;
+    }
+    if (!fits) {  // extents too large for float cell arithmetic: one cell
+        dims[0] = dims[1] = dims[2] = 1;
+        hside = 1.f;
+    } else {
+        hside /= 1.25f;
+    }
+    for (int a = 0; a < 3; ++a) {
+        P.lo[a] = lo[a];
+        P.dims[a] = dims[a];
+    }
+    P.inv_h = 1.f / hside;
+    P.cells = dims[0] * dims[1] * dims[2];
+    P.nonfinite = nonfinite;
+    for (int i = 0; i < 7; ++i) P.pad[i] = 0;
+    L.params[b] = P;
+}
+
+// Cell counts of references (queries = 0) or queries (queries = 1); each
+// point keeps its rank among the points of its cell.
+__global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const float* __restrict__ pts,
+                                                                      GridLayout L, int64_t n,
+                                                                      int queries) {
+    const int64_t b = blockIdx.y;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + threadIdx.x;
+    if (j >= n) return;
+    const GridParams P = L.params[b];
+    const float* p = pts + 3 * (b * n + j);
+    const int c = queries ? query_key(P, p[0], p[1], p[2]) : cell_of(P, p[0], p[1], p[2]);
+    const int rank = atomicAdd((queries ? L.q_off : L.ref_off) + b * L.stride + c, 1);
+    (queries ? L.q_rank : L.ref_rank)[b * n + j] = rank;
+}
+
+// Sum of `v` over a workgroup of kGridPrepThreads threads (every thread gets
+// it); `red` holds one int per wave.
+__device__ __forceinline__ int block_sum(int v, int* red) {
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) v += __shfl_xor(v, d);
+    const int wave = threadIdx.x / kWave;
+    __syncthreads();
+    if (threadIdx.x % kWave == 0) red[wave] = v;
+    __syncthreads();
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < kGridPrepThreads / kWave; ++w) t += red[w];
+    return t;
+}
+
+// The scans cover entries [0, cells + 2) of a batch's count array (the
+// overflow cell is entry `cells`; entry cells + 1 stays 0 and receives the
+// total), in tiles of kGridScanTile entries, 8 per thread.  blockIdx.y is
+// the batch, blockIdx.z 1 for the queries' array.
+__device__ __forceinline__ int scan_entries(const GridLayout& L, int64_t b) {
+    return L.params[b].cells + 2;
+}
+
+__device__ __forceinline__ void load8(const int* a, int at, int count, int (&v)[8]) {
+    if (at + 8 <= count) {
+        const int4 x = *reinterpret_cast<const int4*>(a + at);
+        const int4 y = *reinterpret_cast<const int4*>(a + at + 4);
+        v[0] = x.x; v[1] = x.y; v[2] = x.z; v[3] = x.w;
+        v[4] = y.x; v[5] = y.y; v[6] = y.z; v[7] = y.w;
+    } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = at + u < count ? a[at + u] : 0;
+    }
+}
+
+// Pass 1: the total of each tile.
+__global__ __launch_bounds__(kGridPrepThreads) void grid_tile_sum_kernel(GridLayout L) {
+    __shared__ int red[kGridPrepThreads / kWave];
+    const int64_t b = blockIdx.y;
+    const bool queries = blockIdx.z != 0;
+    const int count = scan_entries(L, b);
+    const int t0 = blockIdx.x * kGridScanTile;
+    if (t0 >= count) return;  // whole workgroup
+    const int* a = (queries ? L.q_off : L.ref_off) + b * L.stride;
+    int v[8];
+    load8(a, t0 + threadIdx.x * 8, count, v);
+    int s = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) s += v[u];
+    s = block_sum(s, red);
+    if (threadIdx.x == 0) L.tile_sum[(b * 2 + queries) * L.tiles + blockIdx.x] = s;
+}
+
+// Pass 2: exclusive offsets of each tile's entries, in place, after the
+// totals of the tiles before it.
+__global__ __launch_bounds__(kGridPrepThreads) void grid_tile_scan_kernel(GridLayout L) {
+    __shared__ int red[kGridPrepThreads / kWave];
+    __shared__ int wsum[kGridPrepThreads / kWave];
+    const int64_t b = blockIdx.y;
+    const bool queries = blockIdx.z != 0;
+    const int count = scan_entries(L, b);
+    const int t0 = blockIdx.x * kGridScanTile;
+    if (t0 >= count) return;  // whole workgroup
+    int* a = (queries ? L.q_off : L.ref_off) + b * L.stride;
+    const int* ts = L.tile_sum + (b * 2 + queries) * L.tiles;
+    int before = 0;
+    for (int t = threadIdx.x; t < static_cast<int>(blockIdx.x); t += kGridPrepThreads) before += ts[t];
+    before = block_sum(before, red);
+    const int at = t0 + threadIdx.x * 8;
+    int v[8];
+    load8(a, at, count, v);
+    int mine = 0;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) mine += v[u];
+    // Inclusive scan of the per-thread totals within the wave, then across
+    // the waves of the workgroup.
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    int inc = mine;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int o = __shfl_up(inc, d);
+        if (lane >= d) inc += o;
+    }
+    if (lane == kWave - 1) wsum[wave] = inc;
+    __syncthreads();
+    int run = before + inc - mine;
+    for (int w = 0; w < wave; ++w) run += wsum[w];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+        const int c = v[u];
+        v[u] = run;
+        run += c;
+    }
+    if (at + 8 <= count) {
+        *reinterpret_cast<int4*>(a + at) = make_int4(v[0], v[1], v[2], v[3]);
+        *reinterpret_cast<int4*>(a + at + 4) = make_int4(v[4], v[5], v[6], v[7]);
+    } else {
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (at + u < count) a[at + u] = v[u];
+    }
+}
+
+// Place every point at its cell's offset plus its rank: the references with
+// their index in the sorted array, the queries' indices in q_order.
+__global__ __launch_bounds__(kGridPrepThreads) void grid_scatter_kernel(const float* __restrict__ pts,
+                                                                        GridLayout L, int64_t n,
+                                                                        int queries) {
+    const int64_t b = blockIdx.y;
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + threadIdx.x;
+    if (j >= n) return;
+    const GridParams P = L.params[b];
+    const float* p = pts + 3 * (b * n + j);
+    const float x = p[0], y = p[1], z = p[2];
+    if (queries) {
+        const int q = L.q_off[b * L.stride + query_key(P, x, y, z)] + L.q_rank[b * n + j];
+        L.q_order[b * n + q] = static_cast<int>(j);
+    } else {
+        const int q = L.ref_off[b * L.stride + cell_of(P, x, y, z)] + L.ref_rank[b * n + j];
+        L.sorted[b * n + q] = make_float4(x, y, z, i2f(static_cast<int>(j)));
+    }
+}
+
+// Composite neighbour word: key (bits of the squared distance) in the high
+// half, reference index in the low half, so that one unsigned 64-bit compare
+// orders by distance, then index.
+__device__ __forceinline__ uint64_t grid_word(uint32_t key, uint32_t ix) {
+    return (static_cast<uint64_t>(key) << 32) | ix;
+}
+
+// Insert this lane's `cnt` buffered candidates into its ascending list (the
+// wave runs while any lane has entries left); tau = the last slot.
+template <int KMAX>
+__device__ __forceinline__ void grid_merge(uint64_t (&lst)[KMAX], uint64_t& tau, const uint2* buf,
+                                           int lane, int cnt) {
+    for (int e = 0;; ++e) {
+        const bool has = e < cnt;
+        if (ballot(has) == 0) break;
+        const uint2 c = buf[e * kWave + lane];  // row e < max(cnt) <= kGridCap
+        const uint64_t cw = grid_word(c.x, c.y);
+        const bool take = has && cw < tau;
+        if (ballot(take) == 0) continue;
+        const uint64_t v = take ? cw : ~0ull;
+        bool here = v < lst[KMAX - 1];
+#pragma unroll
+        for (int s = KMAX - 1; s > 0; --s) {
+            const bool prev = v < lst[s - 1];
+            lst[s] = prev ? lst[s - 1] : (here ? v : lst[s]);
+            here = prev;
+        }
+        lst[0] = here ? v : lst[0];
+        tau = lst[KMAX - 1];
+    }
+}
+
+// The cells a lane has scanned always form a box bl[a] <= cell[a] <= bh[a].
+// It starts as the 3 x 3 x 3 box around the query's cell (clipped to the
+// grid) and grows one face at a time by a slab of cells one cell thick.
+// Scan units are segments, flat cell ranges [c0, c1] within one x-row:
+//   face -1  the starting box: its nine x-rows, the query's own row first;
+//   face 0/1 the x = bl[0] / x = bh[0] slab: one cell per (y, z);
+//   face 2/3 the y = bl[1] / y = bh[1] slab: one x-row per z;
+//   face 4/5 the z = bl[2] / z = bh[2] slab: one x-row per y.
+struct GridBox {
+    int bl[3], bh[3];
+};
+
+__device__ __forceinline__ int box_segments(const GridBox& X, int face) {
+    const int ny = X.bh[1] - X.bl[1] + 1, nz = X.bh[2] - X.bl[2] + 1;
+    return face < 0 ? 9 : (face < 2 ? ny * nz : (face < 4 ? nz : ny));
+}
+
+// Segment g of `face`; false when it lies outside the grid (only rows of the
+// starting box can).
+__device__ __forceinline__ bool box_segment(const GridParams& P, const GridBox& X,
+                                            const int (&c)[3], int face, int g, int& c0,
+                                            int& c1) {
+    int x0 = X.bl[0], x1 = X.bh[0], y, z;
+    if (face < 0) {
+        const int t = g == 0 ? 4 : (g <= 4 ? g - 1 : g);
+        y = c[1] + t % 3 - 1;
+        z = c[2] + t / 3 - 1;
+        if (y < 0 || y >= P.dims[1] || z < 0 || z >= P.dims[2]) return false;
+    } else if (face < 2) {
+        const int ny = X.bh[1] - X.bl[1] + 1;
+        x0 = x1 = (face & 1) ? X.bh[0] : X.bl[0];
+        y = X.bl[1] + g % ny;
+        z = X.bl[2] + g / ny;
+    } else if (face < 4) {
+        y = (face & 1) ? X.bh[1] : X.bl[1];
+        z = X.bl[2] + g;
+    } else {
+        y = X.bl[1] + g;
+        z = (face & 1) ? X.bh[2] : X.bl[2];
+    }
+    const int row = P.dims[0] * (y + P.dims[1] * z);
+    c0 = row + x0;
+    c1 = row + x1;
+    return true;
+}
+
+// Distance from query q to the box face `f` (2a: low side of axis a, 2a + 1:
+// high side), +inf for a face on the grid's edge (references beyond an edge
+// are clamped into the edge cell, so none lie outside it).
+__device__ __forceinline__ float face_distance(const GridParams& P, float h, const float (&q)[3],
+                                               const GridBox& X, int f) {
+    const int a = f >> 1;
+    if (f & 1)
+        return X.bh[a] < P.dims[a] - 1
+                   ? (P.lo[a] + static_cast<float>(X.bh[a] + 1) * h) - q[a]
+                   : INFINITY;
+    return X.bl[a] > 0 ? q[a] - (P.lo[a] + static_cast<float>(X.bl[a]) * h) : INFINITY;
+}
+
+// Lower bound on the distance from q to every finite reference outside the
+// box: the nearest face, less a slack of 2^-18 of the grid's coordinate
+// magnitude, far above the float rounding of the faces and of the cell
+// assignment floor((v - lo) * inv_h).  +inf when the box is the whole grid.
+__device__ __forceinline__ float box_bound(const GridParams& P, float h, const float (&q)[3],
+                                           const GridBox& X) {
+    float b = INFINITY;
+#pragma unroll
+    for (int f = 0; f < 6; ++f) {
+        const int a = f >> 1;
+        const float slack = (fabsf(P.lo[a]) + static_cast<float>(P.dims[a]) * h) * 0x1p-18f;
+        b = fminf(b, face_distance(P, h, q, X, f) - slack);
+    }
+    return b;
+}
+
+template <int KMAX>
+__global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
+    const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
+    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K) {
+    __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
+    __shared__ float4 tiles[kGridSearchWaves][kGridTile];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t groups = (M + kWave - 1) / kWave;
+    const int64_t gw = static_cast<int64_t>(blockIdx.x) * kGridSearchWaves + wave;
+    if (gw >= B * groups) return;  // whole wave; no barriers in this kernel
+    const int64_t b = gw / groups;
+    const int64_t pos = (gw - b * groups) * kWave + lane;
+    const bool active = pos < M;
+    const int m = active ? L.q_order[b * M + pos] : 0;
+    const float* qp = query + 3 * (b * M + m);
+    const float q[3] = {qp[0], qp[1], qp[2]};
+    const GridParams P = L.params[b];
+    const int* off = L.ref_off + b * L.stride;
+    const float4* srt = L.sorted + b * N;
+    uint2* buf = &bufs[wave][0][0];
+    float4* tile = tiles[wave];
+
+    // Ascending list of KMAX words; with K < KMAX the first KMAX - K slots
+    // hold zero words that every candidate sorts after, so the K results are
+    // the last K slots and tau (the admission bound) is always the last slot.
+    // Inactive lanes hold zeros and admit nothing.
+    uint64_t lst[KMAX];
+    auto reset = [&]() {
+#pragma unroll
+        for (int s = 0; s < KMAX; ++s) lst[s] = (active && s >= KMAX - K) ? ~0ull : 0ull;
+    };
+    reset();
+    uint64_t tau = lst[KMAX - 1];
+    int cnt = 0;
+
+    auto admit8 = [&](const float4 (&r)[8], int n) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t key = static_cast<uint32_t>(f2i(sqdist3(r[u].x, r[u].y, r[u].z, q[0], q[1], q[2])));
+            const uint32_t ix = static_cast<uint32_t>(f2i(r[u].w));
+            if (u < n && key < kGridMatchLimit && grid_word(key, ix) < tau) {
+                buf[cnt * kWave + lane] = make_uint2(key, ix);
+                ++cnt;
+            }
+        }
+    };
+    auto drain = [&](bool extra) {
+        if (ballot(cnt > kGridCap - 8 || extra) != 0) {
+            grid_merge<KMAX>(lst, tau, buf, lane, cnt);
+            cnt = 0;
+        }
+    };
+
+    const bool qfinite = finite3(q[0], q[1], q[2]);
+    bool full = P.nonfinite > 0 || ballot(active && !qfinite) != 0;
+    if (!full) {
+        // Each lane scans the box around its own query, streaming 8
+        // references of its current segment per step, with the bounds of its
+        // next segment fetched one segment ahead.  When the box is done the
+        // lane stops if its K-th key is below the squared bound of everything
+        // outside; otherwise it grows the box by its nearest face.  A lane
+        // that needs more than kGridMaxGrow faces sends the wave to the full
+        // scan.
+        const float h = 1.f / P.inv_h;
+        int c[3];
+        GridBox X;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            c[a] = cell_axis(q[a], P.lo[a], P.inv_h, P.dims[a]);
+            X.bl[a] = max(c[a] - 1, 0);
+            X.bh[a] = min(c[a] + 1, P.dims[a] - 1);
+        }
+        int face = -1, grow = 0, g = 0, p = 0, e = 0, np = 0, ne = 0;
+        auto fetch = [&]() {
+            int c0, c1;
+            const bool ok = box_segment(P, X, c, face, g, c0, c1);
+            np = ok ? off[c0] : 0;
+            ne = ok ? off[c1 + 1] : 0;
+        };
+        bool done = !active, want = false;
+        if (!done) fetch();
+        for (;;) {
+            drain(want);
+            want = false;
+            bool escalate = false;
+            while (!done && !want && p >= e) {
+                const int nseg = box_segments(X, face);
+                if (g < nseg) {
+                    p = np;
+                    e = ne;
+                    ++g;
+                    if (g < nseg) fetch();
+                    continue;
+                }
+                const float bnd = box_bound(P, h, q, X);
+                const float kth = i2f(static_cast<int>(tau >> 32));
+                if (!(bnd < INFINITY) ||
+                    (tau != ~0ull && bnd > 0.f && kth < bnd * bnd * (1.f - 0x1p-20f))) {
+                    done = true;
+                } else if (cnt > 0) {
+                    want = true;  // merge first, then check again
+                } else if (grow == kGridMaxGrow) {
+                    escalate = true;
+                    done = true;
+                } else {
+                    float best = INFINITY;
+                    int bf = 0;
+#pragma unroll
+                    for (int f = 0; f < 6; ++f) {
+                        const float d = face_distance(P, h, q, X, f);
+                        if (d < best) {
+                            best = d;
+                            bf = f;
+                        }
+                    }
+#pragma unroll
+                    for (int a = 0; a < 3; ++a) {  // constant indices keep X in registers
+                        X.bl[a] -= bf == 2 * a;
+                        X.bh[a] += bf == 2 * a + 1;
+                    }
+                    face = bf;
+                    ++grow;
+                    g = 0;
+                    fetch();
+                }
+            }
+            if (ballot(escalate) != 0) {
+                full = true;
+                break;
+            }
+            if (ballot(!done) == 0) break;
+            const bool has = p < e;
+            const int base = has ? p : 0, last = has ? e - 1 : 0;
+            float4 rv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + u, last)];
+            admit8(rv, has ? e - p : 0);
+            if (has) p += 8;
+        }
+    }
+    if (full) {
+        // Every reference (the finite ones and the overflow cell), in tiles
+        // of kGridTile loaded by the whole wave into its LDS tile and read
+        // back with broadcast loads.  A list may hold references already, so
+        // start over rather than insert duplicates.
+        reset();
+        tau = lst[KMAX - 1];
+        cnt = 0;
+        const int hi = off[P.cells + 1];
+        for (int t0 = 0; t0 < hi; t0 += kGridTile) {
+            const int nt = min(kGridTile, hi - t0);
+            float4 v[kGridTile / kWave];
+#pragma unroll
+            for (int u = 0; u < kGridTile / kWave; ++u) {
+                const int j = u * kWave + lane;
+                v[u] = j < nt ? srt[t0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int u = 0; u < kGridTile / kWave; ++u) tile[u * kWave + lane] = v[u];
+            __builtin_amdgcn_wave_barrier();
+            for (int e0 = 0; e0 < nt; e0 += 8) {
+                drain(false);
+                float4 rv[8];
+#pragma unroll
+                for (int u = 0; u < 8; ++u) rv[u] = tile[min(e0 + u, nt - 1)];
+                admit8(rv, nt - e0);
+            }
+            __builtin_amdgcn_wave_barrier();
+        }
+    }
+    grid_merge<KMAX>(lst, tau, buf, lane, cnt);
+    if (!active) return;
+    const int64_t row = (b * M + m) * K;
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) {
+        if (s >= KMAX - K) {
+            const uint32_t key = static_cast<uint32_t>(lst[s] >> 32);
+            const uint32_t ix = static_cast<uint32_t>(lst[s]);
+            out_dist[row + s - (KMAX - K)] = lst[s] == ~0ull ? INFINITY : sqrtf(i2f(static_cast<int>(key)));
+            out_idx[row + s - (KMAX - K)] = static_cast<int64_t>(ix);
+        }
+    }
+}
+
+}  // namespace
+}  // namespace pointops
+
+using namespace pointops;
+
+extern "C" {
+
+size_t pointops_knn3_grid_workspace_bytes(int64_t B, int64_t M, int64_t N) {
+    if (B <= 0 || M <= 0 || N <= 0) return 0;
+    return grid_layout_bytes(B, M, N, nullptr, nullptr);
+}
+
+hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist, int64_t* idx,
+                              void* workspace, int64_t B, int64_t M, int64_t N, int64_t K,
+                              hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0 || K < 0 || K > 32 || K > N) return hipErrorInvalidValue;
+    if (B == 0 || M == 0 || K == 0) return hipSuccess;
+    if (N >= (int64_t(1) << 31) - 64 || M >= (int64_t(1) << 31) - 64 || B > 65535 ||
+        workspace == nullptr)
+        return hipErrorInvalidValue;
+    GridLayout L;
+    grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
+    const uint32_t nb = static_cast<uint32_t>(B);
+    const dim3 ref_grid(static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads), nb);
+    const dim3 q_grid(static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads), nb);
+    const dim3 scan_grid(static_cast<uint32_t>(L.tiles), nb, 2);
+    const int parts = static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
+    const dim3 prep(kGridPrepThreads);
+    hipLaunchKernelGGL(grid_bounds_kernel, dim3(static_cast<uint32_t>(parts), nb), prep, 0, stream,
+                       ref, L, N);
+    hipLaunchKernelGGL(grid_params_kernel, dim3(nb), dim3(kWave), 0, stream, L, N, parts,
+                       static_cast<int>(K));
+    hipLaunchKernelGGL(grid_count_kernel, ref_grid, prep, 0, stream, ref, L, N, 0);
+    hipLaunchKernelGGL(grid_count_kernel, q_grid, prep, 0, stream, query, L, M, 1);
+    hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
+    hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
+    hipLaunchKernelGGL(grid_scatter_kernel, ref_grid, prep, 0, stream, ref, L, N, 0);
+    hipLaunchKernelGGL(grid_scatter_kernel, q_grid, prep, 0, stream, query, L, M, 1);
+    const int64_t waves = B * ((M + kWave - 1) / kWave);
+    const int64_t blocks = (waves + kGridSearchWaves - 1) / kGridSearchWaves;
+    if (blocks > INT32_MAX) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<uint32_t>(blocks));
+    const int k = static_cast<int>(K);
+    if (K <= 8)
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
+                           query, L, dist, idx, B, M, N, k);
+    else if (K <= 16)
+        hipLaunchKernelGGL((knn3_grid_kernel<16>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
+                           query, L, dist, idx, B, M, N, k);
+    else
+        hipLaunchKernelGGL((knn3_grid_kernel<32>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
+                           query, L, dist, idx, B, M, N, k);
+    return hipGetLastError();
+}
+
+}  // extern "C"

@@ -24,6 +24,10 @@ _FPS_LARGE_MAX_N = 1 << 21
 _FPS_MULTIGROUP_MIN_N = 65_536
 # Same limit as the reference kernel (ops.py:30).
 _KNN_MAX_K = 256
+# 3-D kNN with at most this many neighbours over at least this many
+# references per cloud uses the grid search (same results as brute force).
+_KNN_GRID_MAX_K = 32
+_KNN_GRID_MIN_N = 32_768
 
 
 def furthest_point_sample(
@@ -125,7 +129,12 @@ def knn(query: Tensor, ref: Tensor, k: int) -> tuple[Tensor, Tensor]:
         return dist, idx
     query, ref = query.contiguous(), ref.contiguous()
     stream = _native.stream(query.device)
-    if D == 3:
+    if D == 3 and k <= _KNN_GRID_MAX_K and N >= _KNN_GRID_MIN_N and B <= 65_535:
+        size = _native.size_query("pointops_knn3_grid_workspace_bytes", B, M, N)
+        workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
+        _native.call("pointops_knn3_grid", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
+                     idx.data_ptr(), workspace.data_ptr(), B, M, N, k, stream)
+    elif D == 3:
         _native.call("pointops_knn3", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
                      idx.data_ptr(), B, M, N, k, stream)
     else:

@@ -339,6 +339,92 @@ def test_knn3_spatially_sorted_reference(cuda_device, descending):
     same_bits(host(d), want_d)
 
 
+def _knn3_grid(query: torch.Tensor, ref: torch.Tensor, k: int):
+    """pointops_knn3_grid through the C ABI (any cloud size)."""
+    from mps_pointops import _native
+
+    q, r = query.cuda().contiguous(), ref.cuda().contiguous()
+    B, M, _ = q.shape
+    N = r.shape[1]
+    dist = torch.empty(B, M, k, device="cuda")
+    idx = torch.empty(B, M, k, dtype=torch.long, device="cuda")
+    size = _native.size_query("pointops_knn3_grid_workspace_bytes", B, M, N)
+    ws = torch.empty(size, dtype=torch.uint8, device="cuda")
+    _native.call("pointops_knn3_grid", q.data_ptr(), r.data_ptr(), dist.data_ptr(), idx.data_ptr(),
+                 ws.data_ptr(), B, M, N, k, _native.stream(q.device))
+    return host(dist), host(idx)
+
+
+def _grid_case(name: str):
+    g = torch.Generator().manual_seed(sum(map(ord, name)))
+    if name == "uniform":
+        ref = torch.rand(2, 40_000, 3, generator=g) * 10
+        query = torch.rand(2, 3000, 3, generator=g) * 10
+    elif name == "slab":
+        ref = bench.make_c3(N=60_000)
+        query = ref[:, torch.randperm(60_000, generator=g)[:2000]].clone()
+    elif name == "ties":  # integer lattice: many equal distances, duplicates
+        ref = torch.randint(0, 12, (1, 30_000, 3), generator=g).float()
+        query = torch.randint(-1, 13, (1, 1500, 3), generator=g).float() + 0.5 * (
+            torch.rand(1, 1500, 1, generator=g) < 0.5).float()
+    elif name == "far_queries":  # queries outside the references' box
+        ref = torch.rand(1, 20_000, 3, generator=g)
+        query = torch.cat([torch.rand(1, 500, 3, generator=g) * 40 - 20,
+                           torch.rand(1, 100, 3, generator=g)], 1)
+    elif name == "sparse_clusters":  # few references per occupied cell, wide gaps
+        centres = torch.rand(1, 40, 3, generator=g) * 100
+        ref = (centres.repeat_interleave(50, 1) + torch.randn(1, 2000, 3, generator=g) * 0.1)
+        query = torch.rand(1, 700, 3, generator=g) * 100
+    elif name == "flat":  # zero extent in z
+        ref = torch.cat([torch.rand(1, 10_000, 2, generator=g), torch.zeros(1, 10_000, 1)], 2)
+        query = torch.cat([torch.rand(1, 400, 2, generator=g), torch.rand(1, 400, 1, generator=g)], 2)
+    elif name == "one_point":  # every reference identical
+        ref = torch.full((1, 5000, 3), 0.25)
+        query = torch.rand(1, 100, 3, generator=g)
+    elif name == "non_finite_refs":
+        ref = torch.rand(2, 8000, 3, generator=g)
+        ref[0, 7] = float("nan")
+        ref[0, 100, 1] = float("inf")
+        ref[1, :7990] = float("nan")  # ten finite references: K=16 pads
+        query = torch.rand(2, 300, 3, generator=g)
+    else:  # non_finite_queries
+        ref = torch.rand(1, 8000, 3, generator=g)
+        query = torch.rand(1, 300, 3, generator=g)
+        query[0, 5] = float("nan")
+        query[0, 70, 2] = -float("inf")
+    return query.contiguous(), ref.contiguous()
+
+
+@pytest.mark.parametrize("name", ["uniform", "slab", "ties", "far_queries", "sparse_clusters",
+                                  "flat", "one_point", "non_finite_refs", "non_finite_queries"])
+@pytest.mark.parametrize("k", [1, 5, 16, 32])
+def test_knn3_grid_matches_oracle(cuda_device, name, k):
+    """The grid search returns the brute-force answer bit for bit."""
+    query, ref = _grid_case(name)
+    want_d, want_i = O.knn3(query, ref, k)
+    d, i = _knn3_grid(query, ref, k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
+
+
+def test_knn3_grid_public_path(cuda_device):
+    """ops.knn uses the grid search for large clouds; results match the
+    brute-force kernel on the same inputs."""
+    import mps_pointops as mp
+    from mps_pointops import _native
+
+    g = torch.Generator().manual_seed(11)
+    ref = torch.rand(1, 70_000, 3, generator=g).cuda()
+    query = torch.rand(1, 4000, 3, generator=g).cuda()
+    d, i = mp.knn(query, ref, 16)
+    bd = torch.empty_like(d)
+    bi = torch.empty_like(i)
+    _native.call("pointops_knn3", query.data_ptr(), ref.data_ptr(), bd.data_ptr(), bi.data_ptr(),
+                 1, 4000, 70_000, 16, _native.stream(query.device))
+    np.testing.assert_array_equal(host(i), host(bi))
+    same_bits(host(d), host(bd))
+
+
 def test_knn3_nan_padding_matches_reference_kernel(cuda_device):
     """kernels/knn.metal semantics: NaN distances never insert; unfilled slots
     stay (inf, 2^32-1); inf distances are ordinary candidates."""
