@@ -36,7 +36,7 @@ constexpr int kGridMaxDim = 1024;
 constexpr int kGridSearchWaves = 4;
 constexpr int kGridCap = 16;  // buffered candidates per lane
 constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
-constexpr int kGridTile = 256;  // references per LDS tile (4 KiB per wave)
+constexpr int kGridQueriesPerWave = kWave / 4;  // one quad of lanes per query
 constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
 
@@ -416,28 +416,60 @@ __device__ __forceinline__ uint64_t grid_word(uint32_t key, uint32_t ix) {
     return (static_cast<uint64_t>(key) << 32) | ix;
 }
 
-// Insert this lane's `cnt` buffered candidates into its ascending list (the
-// wave runs while any lane has entries left); tau = the last slot.
-template <int KMAX>
-__device__ __forceinline__ void grid_merge(uint64_t (&lst)[KMAX], uint64_t& tau, const uint2* buf,
+template <int CTRL>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    const uint32_t lo = static_cast<uint32_t>(dpp<CTRL>(static_cast<int>(static_cast<uint32_t>(v))));
+    const uint32_t hi = static_cast<uint32_t>(dpp<CTRL>(static_cast<int>(static_cast<uint32_t>(v >> 32))));
+    return (static_cast<uint64_t>(hi) << 32) | lo;
+}
+
+constexpr int kDppQuadPrev = 0x90;  // quad_perm [0,0,1,2]: lane j <- lane j - 1
+constexpr int quad_bcast(int j) { return j * 0x55; }  // quad_perm [j,j,j,j]
+
+// A query's neighbour list is shared by the four lanes of its quad: an
+// ascending list of 4S words of which lane j holds ranks S*j .. S*j + S - 1.
+// Insert v (the same word on the four lanes); the last word drops out.  A v
+// not below the last word changes nothing.  Called with the whole wave
+// active (DPP reads neighbouring lanes).
+template <int S>
+__device__ __forceinline__ void quad_insert(uint64_t (&slot)[S], uint64_t v, int qi) {
+    const uint64_t pl = dpp64<kDppQuadPrev>(slot[S - 1]);  // rank S*j - 1
+    bool lt[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) lt[s] = v < slot[s];
+    const bool ltp = qi != 0 && v < pl;
+#pragma unroll
+    for (int s = S - 1; s > 0; --s) slot[s] = lt[s - 1] ? slot[s - 1] : (lt[s] ? v : slot[s]);
+    slot[0] = ltp ? pl : (lt[0] ? v : slot[0]);
+}
+
+// Insert lane J's word of each quad into that quad's list.
+template <int J, int S>
+__device__ __forceinline__ void quad_insert_from(uint64_t (&slot)[S], uint64_t tau, uint64_t mine,
+                                                 int qi) {
+    const uint64_t v = dpp64<quad_bcast(J)>(mine);
+    if (ballot(v < tau) != 0) quad_insert<S>(slot, v, qi);
+}
+
+// Insert every lane's `cnt` buffered candidates into its quad's list, one
+// source lane of the quad at a time; tau = the list's last word on all four
+// lanes (refreshed once per buffer row: a stale tau only lets a no-op insert
+// through).  Whole wave active.
+template <int S>
+__device__ __forceinline__ void quad_merge(uint64_t (&slot)[S], uint64_t& tau, const uint2* buf,
                                            int lane, int cnt) {
+    const int qi = lane & 3;
     for (int e = 0;; ++e) {
         const bool has = e < cnt;
         if (ballot(has) == 0) break;
         const uint2 c = buf[e * kWave + lane];  // row e < max(cnt) <= kGridCap
-        const uint64_t cw = grid_word(c.x, c.y);
-        const bool take = has && cw < tau;
-        if (ballot(take) == 0) continue;
-        const uint64_t v = take ? cw : ~0ull;
-        bool here = v < lst[KMAX - 1];
-#pragma unroll
-        for (int s = KMAX - 1; s > 0; --s) {
-            const bool prev = v < lst[s - 1];
-            lst[s] = prev ? lst[s - 1] : (here ? v : lst[s]);
-            here = prev;
-        }
-        lst[0] = here ? v : lst[0];
-        tau = lst[KMAX - 1];
+        const uint64_t mine = has ? grid_word(c.x, c.y) : ~0ull;
+        if (ballot(mine < tau) == 0) continue;
+        quad_insert_from<0, S>(slot, tau, mine, qi);
+        quad_insert_from<1, S>(slot, tau, mine, qi);
+        quad_insert_from<2, S>(slot, tau, mine, qi);
+        quad_insert_from<3, S>(slot, tau, mine, qi);
+        tau = dpp64<quad_bcast(3)>(slot[S - 1]);
     }
 }
 
@@ -516,19 +548,22 @@ __device__ __forceinline__ float box_bound(const GridParams& P, float h, const f
     return b;
 }
 
-template <int KMAX>
+template <int S>
 __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
     int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K) {
+    constexpr int KMAX = 4 * S;
     __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
-    __shared__ float4 tiles[kGridSearchWaves][kGridTile];
     const int lane = lane_id();
+    const int qi = lane & 3;
     const int wave = uniform(threadIdx.x / kWave);
-    const int64_t groups = (M + kWave - 1) / kWave;
-    const int64_t gw = static_cast<int64_t>(blockIdx.x) * kGridSearchWaves + wave;
+    const int64_t groups = (M + kGridQueriesPerWave - 1) / kGridQueriesPerWave;
+    // Consecutive query groups (neighbours in space) share an XCD and the
+    // references they read stay in its L2.
+    const int64_t gw = static_cast<int64_t>(xcd_local_block(blockIdx.x, gridDim.x)) * kGridSearchWaves + wave;
     if (gw >= B * groups) return;  // whole wave; no barriers in this kernel
     const int64_t b = gw / groups;
-    const int64_t pos = (gw - b * groups) * kWave + lane;
+    const int64_t pos = (gw - b * groups) * kGridQueriesPerWave + (lane >> 2);
     const bool active = pos < M;
     const int m = active ? L.q_order[b * M + pos] : 0;
     const float* qp = query + 3 * (b * M + m);
@@ -537,21 +572,21 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const int* off = L.ref_off + b * L.stride;
     const float4* srt = L.sorted + b * N;
     uint2* buf = &bufs[wave][0][0];
-    float4* tile = tiles[wave];
 
-    // Ascending list of KMAX words; with K < KMAX the first KMAX - K slots
-    // hold zero words that every candidate sorts after, so the K results are
-    // the last K slots and tau (the admission bound) is always the last slot.
-    // Inactive lanes hold zeros and admit nothing.
-    uint64_t lst[KMAX];
+    // With K < KMAX the first KMAX - K ranks hold zero words that every
+    // candidate sorts after, so the K results are the last K ranks and tau
+    // (the admission bound) is always the last rank.  Inactive quads hold
+    // zeros and admit nothing.
+    uint64_t slot[S];
     auto reset = [&]() {
 #pragma unroll
-        for (int s = 0; s < KMAX; ++s) lst[s] = (active && s >= KMAX - K) ? ~0ull : 0ull;
+        for (int s = 0; s < S; ++s) slot[s] = (active && S * qi + s >= KMAX - K) ? ~0ull : 0ull;
     };
     reset();
-    uint64_t tau = lst[KMAX - 1];
+    uint64_t tau = active ? ~0ull : 0ull;
     int cnt = 0;
 
+    // Admit up to n of 8 references into this lane's buffer.
     auto admit8 = [&](const float4 (&r)[8], int n) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -565,7 +600,7 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     };
     auto drain = [&](bool extra) {
         if (ballot(cnt > kGridCap - 8 || extra) != 0) {
-            grid_merge<KMAX>(lst, tau, buf, lane, cnt);
+            quad_merge<S>(slot, tau, buf, lane, cnt);
             cnt = 0;
         }
     };
@@ -573,13 +608,13 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const bool qfinite = finite3(q[0], q[1], q[2]);
     bool full = P.nonfinite > 0 || ballot(active && !qfinite) != 0;
     if (!full) {
-        // Each lane scans the box around its own query, streaming 8
-        // references of its current segment per step, with the bounds of its
-        // next segment fetched one segment ahead.  When the box is done the
-        // lane stops if its K-th key is below the squared bound of everything
-        // outside; otherwise it grows the box by its nearest face.  A lane
-        // that needs more than kGridMaxGrow faces sends the wave to the full
-        // scan.
+        // The quad scans the box around its query, 32 references of its
+        // current segment per step (8 per lane), with the bounds of the next
+        // segment fetched one segment ahead; the four lanes keep identical
+        // copies of the walk's state.  When the box is done the quad stops if
+        // its K-th key is below the squared bound of everything outside;
+        // otherwise it grows the box by its nearest face.  A quad that needs
+        // more than kGridMaxGrow faces sends the wave to the full scan.
         const float h = 1.f / P.inv_h;
         int c[3];
         GridBox X;
@@ -601,8 +636,10 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
         for (;;) {
             drain(want);
             want = false;
+            int qc = cnt | dpp<kDppQuadXor1>(cnt);
+            qc |= dpp<kDppQuadXor2>(qc);
             bool escalate = false;
-            while (!done && !want && p >= e) {
+            while (!done && !want && p >= e) {  // uniform within each quad
                 const int nseg = box_segments(X, face);
                 if (g < nseg) {
                     p = np;
@@ -616,7 +653,7 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
                 if (!(bnd < INFINITY) ||
                     (tau != ~0ull && bnd > 0.f && kth < bnd * bnd * (1.f - 0x1p-20f))) {
                     done = true;
-                } else if (cnt > 0) {
+                } else if (qc != 0) {
                     want = true;  // merge first, then check again
                 } else if (grow == kGridMaxGrow) {
                     escalate = true;
@@ -649,55 +686,41 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             }
             if (ballot(!done) == 0) break;
             const bool has = p < e;
-            const int base = has ? p : 0, last = has ? e - 1 : 0;
+            const int base = has ? p + 8 * qi : 0, last = has ? e - 1 : 0;
             float4 rv[8];
 #pragma unroll
             for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + u, last)];
-            admit8(rv, has ? e - p : 0);
-            if (has) p += 8;
+            admit8(rv, has ? e - base : 0);
+            if (has) p += 32;
         }
     }
     if (full) {
-        // Every reference (the finite ones and the overflow cell), in tiles
-        // of kGridTile loaded by the whole wave into its LDS tile and read
-        // back with broadcast loads.  A list may hold references already, so
-        // start over rather than insert duplicates.
+        // Every reference (the finite ones and the overflow cell), 32 per
+        // step per quad.  A list may hold references already, so start over
+        // rather than insert duplicates.
         reset();
-        tau = lst[KMAX - 1];
+        tau = active ? ~0ull : 0ull;
         cnt = 0;
         const int hi = off[P.cells + 1];
-        for (int t0 = 0; t0 < hi; t0 += kGridTile) {
-            const int nt = min(kGridTile, hi - t0);
-            float4 v[kGridTile / kWave];
+        for (int g0 = 0; g0 < hi; g0 += 32) {
+            drain(false);
+            const int base = g0 + 8 * qi;
+            float4 rv[8];
 #pragma unroll
-            for (int u = 0; u < kGridTile / kWave; ++u) {
-                const int j = u * kWave + lane;
-                v[u] = j < nt ? srt[t0 + j] : make_float4(0.f, 0.f, 0.f, 0.f);
-            }
-            __builtin_amdgcn_wave_barrier();
-#pragma unroll
-            for (int u = 0; u < kGridTile / kWave; ++u) tile[u * kWave + lane] = v[u];
-            __builtin_amdgcn_wave_barrier();
-            for (int e0 = 0; e0 < nt; e0 += 8) {
-                drain(false);
-                float4 rv[8];
-#pragma unroll
-                for (int u = 0; u < 8; ++u) rv[u] = tile[min(e0 + u, nt - 1)];
-                admit8(rv, nt - e0);
-            }
-            __builtin_amdgcn_wave_barrier();
+            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + u, hi - 1)];
+            admit8(rv, hi - base);
         }
     }
-    grid_merge<KMAX>(lst, tau, buf, lane, cnt);
+    quad_merge<S>(slot, tau, buf, lane, cnt);
     if (!active) return;
     const int64_t row = (b * M + m) * K;
 #pragma unroll
-    for (int s = 0; s < KMAX; ++s) {
-        if (s >= KMAX - K) {
-            const uint32_t key = static_cast<uint32_t>(lst[s] >> 32);
-            const uint32_t ix = static_cast<uint32_t>(lst[s]);
-            out_dist[row + s - (KMAX - K)] = lst[s] == ~0ull ? INFINITY : sqrtf(i2f(static_cast<int>(key)));
-            out_idx[row + s - (KMAX - K)] = static_cast<int64_t>(ix);
+    for (int s = 0; s < S; ++s) {
+        const int r = S * qi + s - (KMAX - K);
+        if (r >= 0) {
+            const uint32_t key = static_cast<uint32_t>(slot[s] >> 32);
+            out_dist[row + r] = slot[s] == ~0ull ? INFINITY : sqrtf(i2f(static_cast<int>(key)));
+            out_idx[row + r] = static_cast<int64_t>(static_cast<uint32_t>(slot[s]));
         }
     }
 }
@@ -740,20 +763,19 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
     hipLaunchKernelGGL(grid_scatter_kernel, ref_grid, prep, 0, stream, ref, L, N, 0);
     hipLaunchKernelGGL(grid_scatter_kernel, q_grid, prep, 0, stream, query, L, M, 1);
-    const int64_t waves = B * ((M + kWave - 1) / kWave);
-    const int64_t blocks = (waves + kGridSearchWaves - 1) / kGridSearchWaves;
+    const int64_t waves = B * ((M + kGridQueriesPerWave - 1) / kGridQueriesPerWave);
+    const int64_t blocks = ((waves + kGridSearchWaves - 1) / kGridSearchWaves + 7) / 8 * 8;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<uint32_t>(blocks));
+    const dim3 grid(static_cast<uint32_t>(blocks)), block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
-    if (K <= 8)
-        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
-                           query, L, dist, idx, B, M, N, k);
+    if (K <= 4)
+        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+    else if (K <= 8)
+        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
     else if (K <= 16)
-        hipLaunchKernelGGL((knn3_grid_kernel<16>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
-                           query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
     else
-        hipLaunchKernelGGL((knn3_grid_kernel<32>), grid, dim3(kGridSearchWaves * kWave), 0, stream,
-                           query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
     return hipGetLastError();
 }
 

@@ -24,10 +24,13 @@ _FPS_LARGE_MAX_N = 1 << 21
 _FPS_MULTIGROUP_MIN_N = 65_536
 # Same limit as the reference kernel (ops.py:30).
 _KNN_MAX_K = 256
-# 3-D kNN with at most this many neighbours over at least this many
-# references per cloud uses the grid search (same results as brute force).
+# 3-D kNN with at most this many neighbours, at least this many references
+# per cloud and at least this many query-reference pairs in all uses the grid
+# search (same results as brute force); below them the brute-force kernel is
+# faster than building the grid.
 _KNN_GRID_MAX_K = 32
 _KNN_GRID_MIN_N = 32_768
+_KNN_GRID_MIN_PAIRS = 1 << 26
 
 
 def furthest_point_sample(
@@ -129,7 +132,8 @@ def knn(query: Tensor, ref: Tensor, k: int) -> tuple[Tensor, Tensor]:
         return dist, idx
     query, ref = query.contiguous(), ref.contiguous()
     stream = _native.stream(query.device)
-    if D == 3 and k <= _KNN_GRID_MAX_K and N >= _KNN_GRID_MIN_N and B <= 65_535:
+    if (D == 3 and k <= _KNN_GRID_MAX_K and N >= _KNN_GRID_MIN_N and B <= 65_535
+            and B * M * N >= _KNN_GRID_MIN_PAIRS):
         size = _native.size_query("pointops_knn3_grid_workspace_bytes", B, M, N)
         workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
         _native.call("pointops_knn3_grid", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
