@@ -7,12 +7,13 @@
 // squared distance, so the visit order does not matter.
 //
 // Per batch, in a caller-provided workspace:
-//   1. grid_bounds_kernel: bounding box of the finite references, a cell side
-//      for about grid_per_cell(K) references per cell, and the count of
-//      references with a non-finite coordinate;
-//   2. counting sort of the references by cell (x fastest), the non-finite
-//      ones in an overflow cell after the last, and of the queries by
-//      2 x 2 x 2 block of cells;
+//   1. grid_bounds_kernel: partial bounding boxes of the finite references
+//      and counts of references with a non-finite coordinate; from them
+//      (grid_params) a cell side for about grid_per_cell(K) references per
+//      cell;
+//   2. counting sort (count with ranks, two-pass tiled scan, scatter) of the
+//      references by cell (x fastest), the non-finite ones in an overflow
+//      cell after the last, and of the queries by 2 x 2 x 2 block of cells;
 //   3. knn3_grid_kernel: one lane per query, 64 consecutive queries of the
 //      sorted order (neighbours in space) per wave.  Each lane scans the
 //      3 x 3 x 3 box of cells around its own query and stops once its K-th
@@ -197,11 +198,11 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_bounds_kernel(const flo
     L.partial[(b * kGridBoundBlocks + blockIdx.x) * 8 + tid] = v;
 }
 
-// One wave per batch: combine the `parts` partials into the bounding box of
-// the finite references and choose the grid.
-__global__ __launch_bounds__(kWave) void grid_params_kernel(GridLayout L, int64_t N, int parts,
-                                                            int K) {
-    const int64_t b = blockIdx.x;
+// Run by the first wave of a workgroup: combine batch b's `parts` partials
+// into the bounding box of its finite references and choose the grid; lane 0
+// stores it to *out.
+__device__ void grid_params(const GridLayout& L, int64_t b, int64_t N, int parts, int K,
+                            GridParams* out) {
     const int lane = threadIdx.x;
     float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
     int nonfinite = 0;
@@ -268,22 +269,44 @@ __global__ __launch_bounds__(kWave) void grid_params_kernel(GridLayout L, int64_
     P.cells = dims[0] * dims[1] * dims[2];
     P.nonfinite = nonfinite;
     for (int i = 0; i < 7; ++i) P.pad[i] = 0;
-    L.params[b] = P;
+    *out = P;
 }
 
-// Cell counts of references (queries = 0) or queries (queries = 1); each
-// point keeps its rank among the points of its cell.
-__global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const float* __restrict__ pts,
-                                                                      GridLayout L, int64_t n,
-                                                                      int queries) {
+// Workgroups [0, ref_blocks) of a count or scatter launch cover the
+// references of batch blockIdx.y, the rest its queries.
+struct PrepItem {
+    const float* pts;
+    int64_t n, j;
+    bool queries;
+};
+__device__ __forceinline__ PrepItem prep_item(const float* ref, const float* query, int64_t N,
+                                              int64_t M, uint32_t ref_blocks) {
+    const bool queries = blockIdx.x >= ref_blocks;
+    const int64_t blk = queries ? blockIdx.x - ref_blocks : blockIdx.x;
+    return {queries ? query : ref, queries ? M : N, blk * kGridPrepThreads + threadIdx.x, queries};
+}
+
+// Cell counts of the references and the queries (by query_key); each point
+// keeps its rank among the points of its cell.  Every workgroup derives the
+// grid from the bounding-box partials (the same arithmetic, so the same
+// grid); the first of each batch stores it for the later kernels.
+__global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const float* __restrict__ ref,
+                                                                      const float* __restrict__ query,
+                                                                      GridLayout L, int64_t N, int64_t M,
+                                                                      uint32_t ref_blocks, int parts,
+                                                                      int K) {
+    __shared__ GridParams shared_params;
     const int64_t b = blockIdx.y;
-    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + threadIdx.x;
-    if (j >= n) return;
-    const GridParams P = L.params[b];
-    const float* p = pts + 3 * (b * n + j);
-    const int c = queries ? query_key(P, p[0], p[1], p[2]) : cell_of(P, p[0], p[1], p[2]);
-    const int rank = atomicAdd((queries ? L.q_off : L.ref_off) + b * L.stride + c, 1);
-    (queries ? L.q_rank : L.ref_rank)[b * n + j] = rank;
+    if (threadIdx.x < kWave) grid_params(L, b, N, parts, K, &shared_params);
+    __syncthreads();
+    const GridParams P = shared_params;
+    if (blockIdx.x == 0 && threadIdx.x == 0) L.params[b] = P;
+    const PrepItem it = prep_item(ref, query, N, M, ref_blocks);
+    if (it.j >= it.n) return;
+    const float* p = it.pts + 3 * (b * it.n + it.j);
+    const int c = it.queries ? query_key(P, p[0], p[1], p[2]) : cell_of(P, p[0], p[1], p[2]);
+    const int rank = atomicAdd((it.queries ? L.q_off : L.ref_off) + b * L.stride + c, 1);
+    (it.queries ? L.q_rank : L.ref_rank)[b * it.n + it.j] = rank;
 }
 
 // Sum of `v` over a workgroup of kGridPrepThreads threads (every thread gets
@@ -391,21 +414,22 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_tile_scan_kernel(GridLa
 
 // Place every point at its cell's offset plus its rank: the references with
 // their index in the sorted array, the queries' indices in q_order.
-__global__ __launch_bounds__(kGridPrepThreads) void grid_scatter_kernel(const float* __restrict__ pts,
-                                                                        GridLayout L, int64_t n,
-                                                                        int queries) {
+__global__ __launch_bounds__(kGridPrepThreads) void grid_scatter_kernel(const float* __restrict__ ref,
+                                                                        const float* __restrict__ query,
+                                                                        GridLayout L, int64_t N, int64_t M,
+                                                                        uint32_t ref_blocks) {
+    const PrepItem it = prep_item(ref, query, N, M, ref_blocks);
+    if (it.j >= it.n) return;
     const int64_t b = blockIdx.y;
-    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + threadIdx.x;
-    if (j >= n) return;
     const GridParams P = L.params[b];
-    const float* p = pts + 3 * (b * n + j);
+    const float* p = it.pts + 3 * (b * it.n + it.j);
     const float x = p[0], y = p[1], z = p[2];
-    if (queries) {
-        const int q = L.q_off[b * L.stride + query_key(P, x, y, z)] + L.q_rank[b * n + j];
-        L.q_order[b * n + q] = static_cast<int>(j);
+    if (it.queries) {
+        const int q = L.q_off[b * L.stride + query_key(P, x, y, z)] + L.q_rank[b * M + it.j];
+        L.q_order[b * M + q] = static_cast<int>(it.j);
     } else {
-        const int q = L.ref_off[b * L.stride + cell_of(P, x, y, z)] + L.ref_rank[b * n + j];
-        L.sorted[b * n + q] = make_float4(x, y, z, i2f(static_cast<int>(j)));
+        const int q = L.ref_off[b * L.stride + cell_of(P, x, y, z)] + L.ref_rank[b * N + it.j];
+        L.sorted[b * N + q] = make_float4(x, y, z, i2f(static_cast<int>(it.j)));
     }
 }
 
@@ -748,21 +772,19 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     const uint32_t nb = static_cast<uint32_t>(B);
-    const dim3 ref_grid(static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads), nb);
-    const dim3 q_grid(static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads), nb);
+    const uint32_t ref_blocks = static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads);
+    const uint32_t q_blocks = static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads);
+    const dim3 point_grid(ref_blocks + q_blocks, nb);
     const dim3 scan_grid(static_cast<uint32_t>(L.tiles), nb, 2);
     const int parts = static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
     const dim3 prep(kGridPrepThreads);
     hipLaunchKernelGGL(grid_bounds_kernel, dim3(static_cast<uint32_t>(parts), nb), prep, 0, stream,
                        ref, L, N);
-    hipLaunchKernelGGL(grid_params_kernel, dim3(nb), dim3(kWave), 0, stream, L, N, parts,
-                       static_cast<int>(K));
-    hipLaunchKernelGGL(grid_count_kernel, ref_grid, prep, 0, stream, ref, L, N, 0);
-    hipLaunchKernelGGL(grid_count_kernel, q_grid, prep, 0, stream, query, L, M, 1);
+    hipLaunchKernelGGL(grid_count_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks,
+                       parts, static_cast<int>(K));
     hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
     hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
-    hipLaunchKernelGGL(grid_scatter_kernel, ref_grid, prep, 0, stream, ref, L, N, 0);
-    hipLaunchKernelGGL(grid_scatter_kernel, q_grid, prep, 0, stream, query, L, M, 1);
+    hipLaunchKernelGGL(grid_scatter_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks);
     const int64_t waves = B * ((M + kGridQueriesPerWave - 1) / kGridQueriesPerWave);
     const int64_t blocks = ((waves + kGridSearchWaves - 1) / kGridSearchWaves + 7) / 8 * 8;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
