@@ -161,6 +161,43 @@ hipError_t pointops_three_interpolate_backward(const float *grad_out, const int3
                                                int64_t B, int64_t C, int64_t M, int64_t N,
                                                hipStream_t stream);
 
+/* --------------------------------------------------- PointNet++ grouping */
+
+/* out[b,c,p] = features[b,c,idx[b,p]]: features (B,C,N), idx (B,P) int32
+ * (idx_bits 32) or int64 (64) in [0,N) -> out (B,C,P).  With P = npoint it is
+ * gather_operation, with P = npoint*nsample (idx (B,npoint,nsample) read
+ * flat) grouping_operation; both replace compat.py:62-73 (torch.gather along
+ * the point axis).  Indices outside [0,N) are clamped (callers check them). */
+hipError_t pointops_group_points(const float *features, const void *idx, int idx_bits, float *out,
+                                 int64_t B, int64_t C, int64_t N, int64_t P, hipStream_t stream);
+
+/* The gradient of that gather (compat.py:62-73, torch.gather's scatter-add):
+ * grad_features[b,c,n] = the float sum of grad_out[b,c,p] over the p with
+ * idx[b,p] = n, added in increasing p (deterministic; 0 for a point never
+ * gathered; every element is written).  grad_out channel c of batch b starts
+ * at grad_out + b*grad_batch_stride + c*P (grad_batch_stride >= C*P, so a
+ * channel slice of a larger tensor can be passed).  `workspace` holds
+ * pointops_group_points_backward_workspace_bytes(B, C, N, P) bytes (the
+ * inverse index and a transposed copy of grad_out; no initialisation
+ * needed). */
+size_t pointops_group_points_backward_workspace_bytes(int64_t B, int64_t C, int64_t N, int64_t P);
+hipError_t pointops_group_points_backward(const float *grad_out, int64_t grad_batch_stride,
+                                          const void *idx, int idx_bits, float *grad_features,
+                                          void *workspace, int64_t B, int64_t C, int64_t N,
+                                          int64_t P, hipStream_t stream);
+
+/* Fused set-abstraction grouping (tests/test_pointnet2_e2e.py:36-45, the
+ * QueryAndGroup step after compat.ball_query): out (B,3+C,M,S) with
+ * channels 0-2 = xyz[b,idx[b,m,s],a] - centres[b,m,a] and channels 3.. =
+ * features[b,c,idx[b,m,s]].  xyz (B,N,3), centres (B,M,3), features (B,C,N)
+ * (may be NULL when C = 0), idx (B,M,S) int32/int64 in [0,N).  Replaces the
+ * two grouping_operation calls, the subtraction and the concatenation of
+ * that layer. */
+hipError_t pointops_group_points_rel(const float *xyz, const float *centres, const float *features,
+                                     const void *idx, int idx_bits, float *out, int64_t B,
+                                     int64_t C, int64_t N, int64_t M, int64_t S,
+                                     hipStream_t stream);
+
 /* -------------------------------------------------------------- Chamfer */
 
 /* Nearest reference per query (K = 1), first minimum index on ties, under

@@ -43,6 +43,9 @@ _SIGNATURES: dict[str, list] = {
     "pointops_three_nn": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
+    "pointops_group_points": [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _vp],
+    "pointops_group_points_backward": [_vp, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
+    "pointops_group_points_rel": [_vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
     "pointops_chamfer_nearest_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "pointops_chamfer_nearest_f64": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "pointops_chamfer_backward_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
@@ -53,6 +56,7 @@ _SIZE_QUERIES: dict[str, list] = {
     "pointops_fps_large_workspace_bytes": [_i64, _i64],
     "pointops_fps_flat_scratch_bytes": [_i64, _i64],
     "pointops_knn3_grid_workspace_bytes": [_i64, _i64, _i64],
+    "pointops_group_points_backward_workspace_bytes": [_i64, _i64, _i64, _i64],
 }
 
 

@@ -13,7 +13,8 @@ Call ``install()`` before importing code that uses them::
 A name that is already importable (for example the real CUDA package) is left
 alone unless ``force=True``.  Covered: ``furthest_point_sample``,
 ``gather_operation``, ``grouping_operation`` and ``ball_query`` from
-``pointnet2_utils``; ``KNN`` from ``knn_cuda``; ``fps``, ``knn``, ``radius``,
+``pointnet2_utils``, plus its ``QueryAndGroup`` and ``GroupAll`` modules on
+the fused grouping kernel (not in the reference's stand-in); ``KNN`` from ``knn_cuda``; ``fps``, ``knn``, ``radius``,
 ``knn_graph`` and ``radius_graph`` from ``torch_cluster``.  The reference's
 graph/cluster extras (graclus, grid, random_walk, nearest) and the Pointcept
 registration are outside this package's scope.
@@ -29,7 +30,7 @@ from importlib.machinery import ModuleSpec
 import torch
 from torch import Tensor
 
-from . import flat, ops
+from . import flat, group, ops
 
 
 def furthest_point_sample(xyz: Tensor, npoint: int) -> Tensor:
@@ -40,17 +41,19 @@ def furthest_point_sample(xyz: Tensor, npoint: int) -> Tensor:
 
 
 def gather_operation(features: Tensor, idx: Tensor) -> Tensor:
-    """(B, C, N), (B, npoint) -> (B, C, npoint) (compat.py:62-65)."""
-    B, C, _ = features.shape
-    return features.gather(2, idx.long().unsqueeze(1).expand(B, C, -1))
+    """(B, C, N), (B, npoint) -> (B, C, npoint) (compat.py:62-65): the
+    native gather on the GPU, with its scatter-add gradient."""
+    return group.group_points(features, idx)
 
 
 def grouping_operation(features: Tensor, idx: Tensor) -> Tensor:
-    """(B, C, N), (B, npoint, nsample) -> (B, C, npoint, nsample) (compat.py:68-73)."""
-    B, C, _ = features.shape
-    _, npoint, nsample = idx.shape
-    index = idx.long().reshape(B, 1, npoint * nsample).expand(B, C, -1)
-    return features.gather(2, index).reshape(B, C, npoint, nsample)
+    """(B, C, N), (B, npoint, nsample) -> (B, C, npoint, nsample)
+    (compat.py:68-73): the same gather over the flattened index."""
+    if idx.ndim != 3:
+        raise ValueError("indices must have shape (B, npoint, nsample)")
+    B, npoint, nsample = idx.shape
+    out = group.group_points(features, idx.reshape(B, npoint * nsample))
+    return out.reshape(B, features.shape[1], npoint, nsample)
 
 
 def ball_query(radius: float, nsample: int, xyz: Tensor, new_xyz: Tensor) -> Tensor:
@@ -103,6 +106,8 @@ def install(force: bool = False) -> list[str]:
         gather_operation=gather_operation,
         grouping_operation=grouping_operation,
         ball_query=ball_query,
+        QueryAndGroup=group.QueryAndGroup,
+        GroupAll=group.GroupAll,
     )
     packages = {
         "pointnet2_ops": {

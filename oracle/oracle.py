@@ -25,6 +25,11 @@ Every function restates /root/reference/mps_pointops arithmetic bit for bit
   three_nn selections in the segmentation fixture.
 * ``chamfer_nearest``: tests/test_chamfer.py / test_chamfer_nd.py known
   answers and a numpy argmin brute force.
+* ``group_points`` / ``group_points_backward`` / ``group_points_rel``: the
+  known answer of tests/test_compat.py:134-137 (gradient of a gather with a
+  repeated index), the element identities of tests/test_compat.py:121-131,
+  numpy fancy indexing and ``np.add.at``, and the invariant that a centre
+  grouped with itself is 0 in the relative channels.
 """
 
 from __future__ import annotations
@@ -72,6 +77,10 @@ def _load():
                                            ctypes.c_float, ctypes.c_int, _i64p]
         lib.oracle_three_nn.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _f32p, _i32p]
         lib.oracle_three_interpolate.argtypes = [_f32p, _i64p, _f32p, _i64, _i64, _i64, _i64, _f32p]
+        lib.oracle_group_points.argtypes = [_f32p, _i64p, _i64, _i64, _i64, _i64, _f32p]
+        lib.oracle_group_points_backward.argtypes = [_f32p, _i64p, _i64, _i64, _i64, _i64, _f32p]
+        lib.oracle_group_points_rel.argtypes = [_f32p, _f32p, _f32p, _i64p, _i64, _i64, _i64, _i64,
+                                                _i64, _f32p]
         lib.oracle_three_interpolate_backward.argtypes = [_f32p, _i64p, _f32p, _i64, _i64, _i64,
                                                           _i64, _f64p]
         lib.oracle_chamfer_nearest_f32.argtypes = [_f32p, _f32p, _i64p, _i64p, _i64, _i64, _i64,
@@ -236,6 +245,42 @@ def three_interpolate_backward(grad_out, indices, weights, M: int) -> np.ndarray
     if B and C and M:
         _load().oracle_three_interpolate_backward(_p(g, _f32p), _p(ix, _i64p), _p(w, _f32p),
                                                   B, C, M, N, _p(out, _f64p))
+    return out
+
+
+def group_points(features, idx) -> np.ndarray:
+    """(B,C,N) features gathered at (B,P) indices -> (B,C,P)."""
+    f, ix = _arr(features, np.float32), _arr(idx, np.int64)
+    B, C, N = f.shape
+    P = ix.shape[1]
+    out = np.zeros((B, C, P), np.float32)
+    if out.size:
+        _load().oracle_group_points(_p(f, _f32p), _p(ix, _i64p), B, C, N, P, _p(out, _f32p))
+    return out
+
+
+def group_points_backward(grad_out, idx, N: int) -> np.ndarray:
+    """Scatter-add of (B,C,P) gradients into (B,C,N), float32, p ascending."""
+    g, ix = _arr(grad_out, np.float32), _arr(idx, np.int64)
+    B, C, P = g.shape
+    out = np.zeros((B, C, N), np.float32)
+    if out.size:
+        _load().oracle_group_points_backward(_p(g, _f32p), _p(ix, _i64p), B, C, N, P,
+                                             _p(out, _f32p))
+    return out
+
+
+def group_points_rel(xyz, centres, features, idx) -> np.ndarray:
+    """(B,N,3), (B,M,3), (B,C,N) or None, (B,M,S) -> (B,3+C,M,S)."""
+    x, c, ix = _arr(xyz, np.float32), _arr(centres, np.float32), _arr(idx, np.int64)
+    B, N, _ = x.shape
+    _, M, S = ix.shape
+    f = np.zeros((B, 0, N), np.float32) if features is None else _arr(features, np.float32)
+    C = f.shape[1]
+    out = np.zeros((B, 3 + C, M, S), np.float32)
+    if out.size:
+        _load().oracle_group_points_rel(_p(x, _f32p), _p(c, _f32p), _p(f, _f32p), _p(ix, _i64p),
+                                        B, C, N, M, S, _p(out, _f32p))
     return out
 
 

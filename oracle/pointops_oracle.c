@@ -469,6 +469,50 @@ void oracle_three_interpolate_backward(const float *grad_out, const int64_t *ind
     }
 }
 
+/* ------------------------------------------------- PointNet++ grouping */
+
+/* out[b,c,p] = features[b,c,idx[b,p]]: compat.py:62-73 (gather_operation and
+ * grouping_operation are torch.gather along the point axis; grouping reads
+ * its (B, npoint, nsample) index flat). */
+void oracle_group_points(const float *features, const int64_t *idx, int64_t B, int64_t C,
+                         int64_t N, int64_t P, float *out) {
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t c = 0; c < C; ++c)
+            for (int64_t p = 0; p < P; ++p)
+                out[(b * C + c) * P + p] = features[(b * C + c) * N + idx[b * P + p]];
+}
+
+/* The gradient of that gather, grad_features[b,c,idx[b,p]] += grad_out[b,c,p]
+ * in float, p ascending: torch.gather's scatter-add backward as a
+ * sequential loop. */
+void oracle_group_points_backward(const float *grad_out, const int64_t *idx, int64_t B, int64_t C,
+                                  int64_t N, int64_t P, float *grad_features) {
+    for (int64_t i = 0; i < B * C * N; ++i) grad_features[i] = 0.0f;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t c = 0; c < C; ++c)
+            for (int64_t p = 0; p < P; ++p)
+                grad_features[(b * C + c) * N + idx[b * P + p]] += grad_out[(b * C + c) * P + p];
+}
+
+/* The set-abstraction grouping of tests/test_pointnet2_e2e.py:36-45:
+ * channels 0-2 = grouping_operation(xyz^T, idx) - new_xyz^T[..., None] (one
+ * float subtraction), channels 3.. = grouping_operation(features, idx),
+ * concatenated: out (B, 3+C, M, S) for xyz (B,N,3), centres (B,M,3),
+ * features (B,C,N), idx (B,M,S). */
+void oracle_group_points_rel(const float *xyz, const float *centres, const float *features,
+                             const int64_t *idx, int64_t B, int64_t C, int64_t N, int64_t M,
+                             int64_t S, float *out) {
+    const int64_t P = M * S, CT = C + 3;
+    for (int64_t b = 0; b < B; ++b)
+        for (int64_t p = 0; p < P; ++p) {
+            const int64_t j = idx[b * P + p], m = p / S;
+            for (int a = 0; a < 3; ++a)
+                out[(b * CT + a) * P + p] = xyz[(b * N + j) * 3 + a] - centres[(b * M + m) * 3 + a];
+            for (int64_t c = 0; c < C; ++c)
+                out[(b * CT + 3 + c) * P + p] = features[(b * C + c) * N + j];
+        }
+}
+
 /* -------------------------------------------------------------- Chamfer */
 
 /*

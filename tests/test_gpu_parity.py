@@ -766,3 +766,87 @@ def test_repeated_dispatch_is_stable(cuda_device):
         assert torch.equal(mp.furthest_point_sample(x, 256), first)
         assert torch.equal(mp.ball_query(c, x, 0.2, 32)[1], bq)
         assert torch.equal(mp.knn(c, x, 16)[1], kn)
+
+
+# ------------------------------------------------------- PointNet++ grouping
+
+
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("B,C,N,P", [(3, 67, 500, 1000), (2, 16, 4096, 32 * 33), (1, 1, 7, 1)])
+def test_group_points_matches_oracle(cuda_device, bits, B, C, N, P):
+    """Forward and backward (a sequential scatter-add in p order; points
+    gathered many times) bit for bit."""
+    from mps_pointops import group
+
+    g = torch.Generator().manual_seed(B * 1000 + C + P)
+    f = torch.randn(B, C, N, generator=g)
+    idx = torch.randint(0, min(N, 37), (B, P), generator=g, dtype=torch.int64)
+    idx = idx.to(torch.int32 if bits == 32 else torch.int64)
+    fc = f.cuda().requires_grad_()
+    out = group.group_points(fc, idx.cuda())
+    np.testing.assert_array_equal(host(out), O.group_points(f.numpy(), idx.numpy()))
+    go = torch.randn(B, C, P, generator=g)
+    out.backward(go.cuda())
+    same_bits(host(fc.grad), O.group_points_backward(go.numpy(), idx.numpy(), N))
+
+
+def test_compat_gather_grouping_known_answers(cuda_device):
+    """tests/test_compat.py:121-137 on the GPU path."""
+    from mps_pointops import compat
+
+    features = torch.randn(2, 4, 30).cuda()
+    idx = torch.randint(0, 30, (2, 7), dtype=torch.int32).cuda()
+    out = compat.gather_operation(features, idx)
+    assert out.shape == (2, 4, 7)
+    assert torch.equal(out[1, :, 3], features[1, :, idx[1, 3]])
+    gidx = torch.randint(0, 30, (2, 7, 5), dtype=torch.int32).cuda()
+    out = compat.grouping_operation(features, gidx)
+    assert out.shape == (2, 4, 7, 5)
+    assert torch.equal(out[0, :, 6, 2], features[0, :, gidx[0, 6, 2]])
+    leaf = torch.randn(1, 3, 10).cuda().requires_grad_()
+    compat.gather_operation(leaf, torch.tensor([[2, 2, 5]]).cuda()).sum().backward()
+    assert leaf.grad[0, 0].tolist() == [0, 0, 2, 0, 0, 1, 0, 0, 0, 0]
+    with pytest.raises(IndexError):
+        compat.gather_operation(features, torch.tensor([[0, 30]] * 2).cuda())
+
+
+def test_query_and_group_matches_oracle_and_composition(cuda_device):
+    """The fused grouping equals the oracle bit for bit and the reference
+    layer's composition (tests/test_pointnet2_e2e.py:38-44: gather, ball
+    query, two groupings, subtraction, concatenation); gradients match the
+    composition's autograd on the CPU."""
+    from mps_pointops import compat, group
+
+    x = bench.make_c2(B=4, N=1024)
+    feats = torch.randn(4, 19, 1024, generator=torch.Generator().manual_seed(9))
+    xc, fc = x.cuda(), feats.cuda()
+    sampled = compat.furthest_point_sample(xc, 128)
+    new_xyz = compat.gather_operation(xc.transpose(1, 2).contiguous(), sampled).transpose(1, 2).contiguous()
+    idx = compat.ball_query(0.2, 24, xc, new_xyz)
+    fused = group.QueryAndGroup(0.2, 24)(xc, new_xyz, fc)
+    want = O.group_points_rel(x.numpy(), host(new_xyz), feats.numpy(), host(idx))
+    np.testing.assert_array_equal(host(fused), want)
+    gx = compat.grouping_operation(xc.transpose(1, 2).contiguous(), idx) - new_xyz.transpose(1, 2).unsqueeze(-1)
+    composed = torch.cat((gx, compat.grouping_operation(fc, idx)), dim=1)
+    assert torch.equal(fused, composed)
+    # Centres are cloud points: wherever a centre is grouped with its own
+    # point the relative channels are exactly 0.
+    own = host(idx) == host(sampled)[:, :, None]
+    assert own.any()
+    assert (host(fused)[:, :3][np.broadcast_to(own[:, None], (4, 3) + own.shape[1:])] == 0).all()
+    assert group.QueryAndGroup(0.2, 24, use_xyz=False)(xc, new_xyz, fc).shape == (4, 19, 128, 24)
+    # Gradients to xyz, centres and features.
+    a = xc.clone().requires_grad_()
+    c = new_xyz.clone().requires_grad_()
+    f = fc.clone().requires_grad_()
+    go = torch.randn(fused.shape, generator=torch.Generator().manual_seed(10))
+    group.query_and_group(a, c, f, idx).backward(go.cuda())
+    ac, cc, fcp = (t.detach().cpu().requires_grad_() for t in (xc, new_xyz, fc))
+    il = host(idx).astype(np.int64)
+    B, M, S = il.shape
+    flat = torch.from_numpy(il).reshape(B, 1, M * S)
+    rel = ac.transpose(1, 2).gather(2, flat.expand(B, 3, -1)).reshape(B, 3, M, S) - cc.transpose(1, 2).unsqueeze(-1)
+    ref_out = torch.cat((rel, fcp.gather(2, flat.expand(B, 19, -1)).reshape(B, 19, M, S)), 1)
+    ref_out.backward(go)
+    for got, ref in ((a, ac), (c, cc), (f, fcp)):
+        np.testing.assert_allclose(host(got.grad), ref.grad.numpy(), rtol=1e-5, atol=1e-5)

@@ -468,3 +468,66 @@ def test_mutants_fail_the_goldens():
     fused = (a[:, 1].astype(np.float64) * a[:, 1] + fused).astype(np.float32)
     fused = (a[:, 2].astype(np.float64) * a[:, 2] + fused).astype(np.float32)
     assert (unfused != fused).any()
+
+
+# ------------------------------------------------------- PointNet++ grouping
+
+
+def test_group_points_backward_known_answer():
+    """tests/test_compat.py:134-137: the gradient of a gather with index
+    [[2, 2, 5]] under sum() is 2 at point 2 and 1 at point 5, per channel."""
+    grad = O.group_points_backward(np.ones((1, 3, 3), np.float32), [[2, 2, 5]], 10)
+    assert grad[0, 0].tolist() == [0, 0, 2, 0, 0, 1, 0, 0, 0, 0]
+    assert (grad[0] == grad[0, 0]).all()
+
+
+def test_group_points_matches_indexing():
+    """tests/test_compat.py:121-131 element identities over whole arrays, for
+    the flat (gather) and the (npoint, nsample) (grouping) index."""
+    rng = np.random.default_rng(3)
+    f = rng.standard_normal((2, 4, 30)).astype(np.float32)
+    idx = rng.integers(0, 30, size=(2, 7))
+    out = O.group_points(f, idx)
+    assert out.shape == (2, 4, 7)
+    np.testing.assert_array_equal(out[1, :, 3], f[1, :, idx[1, 3]])
+    np.testing.assert_array_equal(out, np.stack([f[b][:, idx[b]] for b in range(2)]))
+    gidx = rng.integers(0, 30, size=(2, 7, 5))
+    grouped = O.group_points(f, gidx.reshape(2, 35)).reshape(2, 4, 7, 5)
+    np.testing.assert_array_equal(grouped[0, :, 6, 2], f[0, :, gidx[0, 6, 2]])
+
+
+def test_group_points_backward_matches_add_at():
+    """np.add.at adds in index order, in float32: the sequential
+    scatter-add the oracle restates, bit for bit."""
+    rng = np.random.default_rng(4)
+    g = rng.standard_normal((2, 3, 40)).astype(np.float32)
+    idx = rng.integers(0, 9, size=(2, 40))  # heavy repetition
+    want = np.zeros((2, 3, 9), np.float32)
+    for b in range(2):
+        for c in range(3):
+            np.add.at(want[b, c], idx[b], g[b, c])
+    np.testing.assert_array_equal(O.group_points_backward(g, idx, 9), want)
+    # Conservation: every gradient element lands somewhere exactly once.
+    np.testing.assert_allclose(O.group_points_backward(g, idx, 9).sum(-1, dtype=np.float64),
+                               g.astype(np.float64).sum(-1), rtol=1e-5)
+
+
+def test_group_points_rel_matches_composition_and_self_zero():
+    """Channels 0-2 are grouped xyz minus the centre (one float32
+    subtraction), then the grouped features; a centre grouped with its own
+    point is exactly 0 in the relative channels."""
+    rng = np.random.default_rng(5)
+    xyz = rng.standard_normal((2, 50, 3)).astype(np.float32)
+    sel = rng.integers(0, 50, size=(2, 6))
+    centres = np.stack([xyz[b, sel[b]] for b in range(2)])
+    feats = rng.standard_normal((2, 4, 50)).astype(np.float32)
+    idx = rng.integers(0, 50, size=(2, 6, 5))
+    idx[:, :, 0] = sel
+    out = O.group_points_rel(xyz, centres, feats, idx)
+    assert out.shape == (2, 7, 6, 5)
+    gx = np.stack([xyz[b, idx[b]] for b in range(2)])  # (B,M,S,3)
+    want_rel = (gx - centres[:, :, None, :]).transpose(0, 3, 1, 2)
+    np.testing.assert_array_equal(out[:, :3], want_rel)
+    np.testing.assert_array_equal(out[:, 3:], np.stack([feats[b][:, idx[b]] for b in range(2)]))
+    assert (out[:, :3, :, 0] == 0).all()
+    assert O.group_points_rel(xyz, centres, None, idx).shape == (2, 3, 6, 5)
