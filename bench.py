@@ -298,10 +298,37 @@ def run(args) -> dict:
     t_ti = timer.time(lambda: three_interpolate(feats, tn_i, w), reps)
     t_tib = timer.time(interp_fwd_bwd, reps)
     interp_bytes = 4 * (B * 128 * C2_NPOINT + 2 * B * N * 3 + B * 128 * N)
+    # Set-abstraction grouping after the r=0.2 ball query (not part of the
+    # metric): grouped xyz - centre and C=64 grouped features in one fused
+    # kernel, forward and forward+backward (bytes = output written + index,
+    # features and xyz read once).
+    from mps_pointops import group as grouping
+    from mps_pointops import compat
+
+    sa_feats = torch.randn(B, 64, N, generator=g).to(device)
+    sa_idx = compat.ball_query(0.2, 32, xyz, centres)
+    sa_leaf = sa_feats.clone().requires_grad_()
+    sa_up = torch.randn(B, 67, C2_NPOINT, 32, generator=g).to(device)
+
+    def group_fwd():
+        return grouping.query_and_group(xyz, centres, sa_feats, sa_idx, check=False)
+
+    def group_fwd_bwd():
+        sa_leaf.grad = None
+        grouping.query_and_group(xyz, centres, sa_leaf, sa_idx, check=False).backward(sa_up)
+
+    group_fwd()
+    group_fwd_bwd()
+    torch.cuda.synchronize()
+    t_gf = timer.time(group_fwd, reps)
+    t_gfb = timer.time(group_fwd_bwd, reps)
+    group_bytes = 4 * (B * 67 * C2_NPOINT * 32 + B * C2_NPOINT * 32 + B * 64 * N + B * N * 3)
     propagation = {
         "three_nn": {"ms": t_tn * 1e3, "tops": PAIR_OPS * B * N * C2_NPOINT / t_tn / 1e12},
         "three_interpolate": {"ms": t_ti * 1e3, "gbps": interp_bytes / t_ti / 1e9},
         "three_interpolate_fwd_bwd": {"ms": t_tib * 1e3, "gbps": 2 * interp_bytes / t_tib / 1e9},
+        "query_and_group_C64_S32": {"ms": t_gf * 1e3, "gbps": group_bytes / t_gf / 1e9},
+        "query_and_group_fwd_bwd": {"ms": t_gfb * 1e3},
     }
 
     kernel = fps_kernel_name(N)
