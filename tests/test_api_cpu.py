@@ -321,3 +321,17 @@ def test_torch_port_matches_oracle():
     # cdist may take a matrix-multiply path: self-distances come out ~1e-3
     # instead of 0 (README.md:295-297 documents this inexactness).
     np.testing.assert_allclose(d.numpy(), od, rtol=1e-4, atol=2e-3)
+
+
+def test_pytorch3d_adapter_argument_errors():
+    """tests/test_pytorch3d_adapter.py:121-133: dtype and flag errors come
+    before any device work."""
+    from mps_pointops.pytorch3d import ball_query
+
+    points = torch.zeros((1, 2, 3))
+    with pytest.raises(TypeError, match="float32"):
+        ball_query(points.half(), points.half(), K=1, radius=1.0)
+    with pytest.raises(TypeError, match="bool"):
+        ball_query(points, points, K=1, radius=1.0, skip_points_outside_cube=1)
+    with pytest.raises(ValueError, match="shapes"):
+        ball_query(points[0], points, K=1, radius=1.0)

@@ -850,3 +850,77 @@ def test_query_and_group_matches_oracle_and_composition(cuda_device):
     ref_out.backward(go)
     for got, ref in ((a, ac), (c, cc), (f, fcp)):
         np.testing.assert_allclose(host(got.grad), ref.grad.numpy(), rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------ PyTorch3D-style ball query
+# Known answers of tests/test_pytorch3d_adapter.py, on the ROCm device.
+
+
+def test_pytorch3d_defaults_and_zero_padded_neighbors(cuda_device):
+    from mps_pointops.pytorch3d import KNN, ball_query
+
+    queries = torch.zeros((1, 1, 3), device="cuda")
+    points = torch.tensor([[[0.125, 0.0, 0.0], [2.0, 0.0, 0.0]]], device="cuda")
+    result = ball_query(queries, points)
+    assert isinstance(result, KNN)
+    assert result._fields == ("dists", "idx", "knn")
+    assert result.dists.shape == result.idx.shape == (1, 1, 500)
+    assert result.knn.shape == (1, 1, 500, 3)
+    assert result.dists.dtype == torch.float32 and result.idx.dtype == torch.int64
+    assert result.idx[0, 0, 0].item() == 0 and torch.all(result.idx[0, 0, 1:] == -1)
+    assert result.dists[0, 0, 0].item() == 0.015625 and torch.all(result.dists[0, 0, 1:] == 0)
+    assert torch.equal(result.knn[0, 0, 0], points[0, 0])
+    assert torch.all(result.knn[0, 0, 1:] == 0)
+
+
+def test_pytorch3d_ragged_lengths_and_cube_hint(cuda_device):
+    from mps_pointops.pytorch3d import ball_query
+
+    queries = torch.tensor([[[0.0, 0, 0], [0.0, 0, 0]], [[3.0, 0, 0], [0.0, 0, 0]]], device="cuda")
+    points = torch.tensor([[[0.5, 0, 0], [0.25, 0, 0], [0.125, 0, 0], [2.0, 0, 0]],
+                           [[0.125, 0, 0], [0.25, 0, 0], [2.0, 0, 0], [3.0, 0, 0]]], device="cuda")
+    l1 = torch.tensor([1, 2], device="cuda")
+    l2 = torch.tensor([2, 1], device="cuda")
+    default = ball_query(queries, points, l1, l2, 3, 1.0, True, False)
+    cube = ball_query(queries, points, l1, l2, 3, 1.0, True, True)
+    no_nn = ball_query(queries, points, l1, l2, 3, 1.0, False, True)
+    assert default.idx.cpu().tolist() == [[[0, 1, -1], [-1, -1, -1]], [[-1, -1, -1], [0, -1, -1]]]
+    assert default.dists.cpu().tolist() == [[[0.25, 0.0625, 0], [0, 0, 0]], [[0, 0, 0], [0.015625, 0, 0]]]
+    assert torch.equal(cube.idx, default.idx) and torch.equal(cube.dists, default.dists)
+    assert no_nn.knn is None
+    assert default.knn[0, 0, 0, 0].item() == 0.5 and default.knn[0, 0, 1, 0].item() == 0.25
+    assert torch.all(default.knn[default.idx == -1] == 0)
+
+
+@pytest.mark.parametrize("B,Q,P,k", [(1, 2, 0, 3), (1, 2, 2, 0), (1, 0, 2, 3), (0, 2, 2, 3)])
+def test_pytorch3d_empty_dimensions(cuda_device, B, Q, P, k):
+    from mps_pointops.pytorch3d import ball_query
+
+    result = ball_query(torch.zeros((B, Q, 3), device="cuda"), torch.zeros((B, P, 3), device="cuda"),
+                        K=k, radius=1.0)
+    assert result.dists.shape == result.idx.shape == (B, Q, k)
+    assert result.knn.shape == (B, Q, k, 3)
+    assert torch.all(result.idx == -1) and torch.all(result.dists == 0) and torch.all(result.knn == 0)
+
+
+def test_pytorch3d_gradients(cuda_device):
+    from mps_pointops.pytorch3d import ball_query
+
+    q = torch.zeros((1, 1, 3), device="cuda", requires_grad=True)
+    p = torch.tensor([[[0.25, 0.0, 0.0]]], device="cuda", requires_grad=True)
+    r = ball_query(q, p, K=2, radius=1.0)
+    (r.dists.sum() + r.knn.sum()).backward()
+    assert q.grad.cpu().tolist() == [[[-0.5, 0.0, 0.0]]]
+    assert p.grad.cpu().tolist() == [[[1.5, 1.0, 1.0]]]
+    for P, k in ((0, 2), (2, 0)):
+        pts = torch.zeros((1, P, 3), device="cuda", requires_grad=True)
+        ball_query(torch.zeros((1, 1, 3), device="cuda"), pts, K=k, radius=1.0).knn.sum().backward()
+        assert pts.grad is not None and torch.all(pts.grad == 0)
+
+
+def test_pytorch3d_rejects_invalid_lengths(cuda_device):
+    from mps_pointops.pytorch3d import ball_query
+
+    points = torch.zeros((1, 2, 3), device="cuda")
+    with pytest.raises(ValueError, match="lengths1|query_lengths"):
+        ball_query(points, points, lengths1=torch.tensor([3], device="cuda"), K=1, radius=1.0)
