@@ -16,8 +16,9 @@ alone unless ``force=True``.  Covered: ``furthest_point_sample``,
 ``pointnet2_utils``, plus its ``QueryAndGroup`` and ``GroupAll`` modules on
 the fused grouping kernel (not in the reference's stand-in); ``KNN`` from ``knn_cuda``; ``fps``, ``knn``, ``radius``,
 ``knn_graph`` and ``radius_graph`` from ``torch_cluster``.  The reference's
-graph/cluster extras (graclus, grid, random_walk, nearest) and the Pointcept
-registration are outside this package's scope.
+graph/cluster extras (graclus, grid, random_walk, nearest) are outside this
+package's scope; ``install(pointcept=True)`` adds the Pointcept v1.2.1 PTv1
+``pointops`` module (``mps_pointops.pointcept``).
 """
 
 from __future__ import annotations
@@ -31,6 +32,7 @@ import torch
 from torch import Tensor
 
 from . import flat, group, ops
+from . import pointcept as pointcept_ops
 
 
 def furthest_point_sample(xyz: Tensor, npoint: int) -> Tensor:
@@ -98,8 +100,9 @@ def _module(name: str, **attrs) -> types.ModuleType:
     return module
 
 
-def install(force: bool = False) -> list[str]:
-    """Register the stand-ins in ``sys.modules`` (compat.py:125-172)."""
+def install(force: bool = False, *, pointcept: bool = False) -> list[str]:
+    """Register the stand-ins in ``sys.modules`` (compat.py:125-172); with
+    ``pointcept=True`` also the Pointcept v1.2.1 PTv1 ``pointops`` surface."""
     pointnet2_utils = _module(
         "pointnet2_ops.pointnet2_utils",
         furthest_point_sample=furthest_point_sample,
@@ -126,6 +129,17 @@ def install(force: bool = False) -> list[str]:
             )
         },
     }
+    if pointcept:
+        packages["pointops"] = {
+            "pointops": _module(
+                "pointops",
+                farthest_point_sampling=pointcept_ops.farthest_point_sampling,
+                knn_query=pointcept_ops.knn_query,
+                grouping=pointcept_ops.grouping,
+                knn_query_and_group=pointcept_ops.knn_query_and_group,
+                interpolation=pointcept_ops.interpolation,
+            ),
+        }
     installed = []
     for top, modules in packages.items():
         if not force and (top in sys.modules or importlib.util.find_spec(top) is not None):

@@ -335,3 +335,28 @@ def test_pytorch3d_adapter_argument_errors():
         ball_query(points, points, K=1, radius=1.0, skip_points_outside_cube=1)
     with pytest.raises(ValueError, match="shapes"):
         ball_query(points[0], points, K=1, radius=1.0)
+
+
+def test_pointcept_offsets_and_optional_registration():
+    """tests/test_pointcept.py:146-168: offset errors precede device work;
+    install() adds ``pointops`` only with pointcept=True."""
+    from mps_pointops import compat, pointcept
+
+    xyz = torch.zeros((3, 3))
+    with pytest.raises(ValueError, match="end at"):
+        pointcept.farthest_point_sampling(xyz, torch.tensor([2]), torch.tensor([1]))
+    with pytest.raises(ValueError, match="more FPS"):
+        pointcept.farthest_point_sampling(xyz, torch.tensor([3]), torch.tensor([4]))
+    names = ("pointnet2_ops", "pointnet2_ops.pointnet2_utils", "knn_cuda", "torch_cluster", "pointops")
+    saved = {name: sys.modules.pop(name) for name in names if name in sys.modules}
+    try:
+        assert "pointops" not in compat.install()
+        assert "pointops" in compat.install(force=True, pointcept=True)
+        import pointops
+
+        assert pointops.knn_query is pointcept.knn_query
+        assert pointops.interpolation is pointcept.interpolation
+    finally:
+        for name in names:
+            sys.modules.pop(name, None)
+        sys.modules.update(saved)

@@ -924,3 +924,115 @@ def test_pytorch3d_rejects_invalid_lengths(cuda_device):
     points = torch.zeros((1, 2, 3), device="cuda")
     with pytest.raises(ValueError, match="lengths1|query_lengths"):
         ball_query(points, points, lengths1=torch.tensor([3], device="cuda"), K=1, radius=1.0)
+
+
+# ------------------------------------------------------- Pointcept shim
+# Known answers of tests/test_pointcept.py, on the ROCm device.
+
+
+def test_pointcept_fps_offsets_and_int32(cuda_device):
+    from mps_pointops import pointcept
+
+    xyz = torch.tensor([[0., 0, 0], [1., 0, 0], [4., 0, 0], [9., 0, 0], [10., 0, 0], [11., 0, 0],
+                        [15., 0, 0]], device="cuda")
+    out = pointcept.farthest_point_sampling(xyz, torch.tensor([4, 7], dtype=torch.int32, device="cuda"),
+                                            torch.tensor([2, 4], dtype=torch.int32, device="cuda"))
+    assert out.dtype == torch.int32 and out.cpu().tolist() == [0, 3, 4, 6]
+
+
+def test_pointcept_knn_padding_ties_ceiling_nonfinite(cuda_device):
+    from mps_pointops import pointcept
+
+    xyz = torch.tensor([[0., 0, 0], [2., 0, 0], [10., 0, 0], [12., 0, 0], [14., 0, 0]],
+                       device="cuda", requires_grad=True)
+    query = torch.tensor([[0.5, 0, 0], [11., 0, 0]], device="cuda", requires_grad=True)
+    idx, dist = pointcept.knn_query(4, xyz, torch.tensor([2, 5], device="cuda"), query,
+                                    torch.tensor([1, 2], dtype=torch.int32, device="cuda"))
+    assert idx.dtype == torch.int32 and idx.cpu().tolist() == [[0, 1, -1, -1], [2, 3, 4, -1]]
+    assert dist.cpu().tolist() == [[0.5, 1.5, 1e5, 1e5], [1., 1., 3., 1e5]]
+    assert not dist.requires_grad
+    x = torch.arange(16, dtype=torch.float32, device="cuda") * 0.25
+    line = torch.stack((x, torch.zeros_like(x), torch.zeros_like(x)), dim=1)
+    idx, dist = pointcept.knn_query(8, line, torch.tensor([16], dtype=torch.int32, device="cuda"))
+    assert idx[2].cpu().tolist() == [2, 1, 3, 0, 4, 5, 6, 7]
+    assert dist[2].cpu().tolist() == [0., 0.25, 0.25, 0.5, 0.5, 0.75, 1., 1.25]
+    far = torch.tensor([[99_999., 0, 0], [100_000., 0, 0], [100_001., 0, 0]], device="cuda")
+    one = torch.tensor([1], dtype=torch.int32, device="cuda")
+    idx, dist = pointcept.knn_query(3, far, torch.tensor([3], dtype=torch.int32, device="cuda"),
+                                    torch.zeros((1, 3), device="cuda"), one)
+    assert idx.cpu().tolist() == [[0, -1, -1]]
+    assert dist.cpu().tolist() == [[99_999., 100_000., 100_000.]]
+    q0 = torch.zeros((1, 3), device="cuda")
+    nb = torch.tensor([0, 1], dtype=torch.int32, device="cuda")
+    for bad in (float("nan"), float("inf")):
+        pts = torch.tensor([[0., 0, 0], [bad, 0, 0]], device="cuda")
+        idx, dist = pointcept.knn_query(1, pts, torch.tensor([1, 2], dtype=torch.int32, device="cuda"), q0, nb)
+        assert idx.cpu().tolist() == [[-1]] and dist.cpu().tolist() == [[100_000.]]
+        pts = torch.tensor([[0., 0, 0], [bad, 0, 0], [1., 0, 0]], device="cuda")
+        idx, dist = pointcept.knn_query(2, pts, torch.tensor([1, 3], dtype=torch.int32, device="cuda"), q0, nb)
+        assert idx.cpu().tolist() == [[2, -1]] and dist.cpu().tolist() == [[1., 100_000.]]
+
+
+def test_pointcept_grouping_query_and_group_interpolation(cuda_device):
+    from mps_pointops import pointcept
+
+    xyz = torch.tensor([[0., 0, 0], [1., 0, 0], [2., 0, 0]], device="cuda", requires_grad=True)
+    feat = torch.tensor([[1., 2.], [3., 4.], [5., 6.]], device="cuda", requires_grad=True)
+    query = torch.tensor([[1., 0, 0]], device="cuda", requires_grad=True)
+    idx = torch.tensor([[2, -1, 2]], dtype=torch.int32, device="cuda")
+    result = pointcept.grouping(idx, feat, xyz, query, with_xyz=True)
+    assert result.shape == (1, 3, 5)
+    assert result[0, 1].cpu().tolist() == [0.] * 5 and result[0, 0].cpu().tolist() == [1., 0, 0, 5, 6]
+    result.sum().backward()
+    assert feat.grad.cpu().tolist() == [[0., 0], [0, 0], [2, 2]]
+    assert xyz.grad.cpu().tolist() == [[0., 0, 0], [0, 0, 0], [2, 2, 2]]
+    assert query.grad.cpu().tolist() == [[-2., -2, -2]]
+
+    xyz = torch.tensor([[0., 0, 0], [2., 0, 0]], device="cuda", requires_grad=True)
+    feat = torch.tensor([[2.], [10.]], device="cuda", requires_grad=True)
+    query = torch.tensor([[0.5, 0, 0]], device="cuda", requires_grad=True)
+    off = torch.tensor([2], dtype=torch.int32, device="cuda")
+    noff = torch.tensor([1], dtype=torch.int32, device="cuda")
+    grouped, idx = pointcept.knn_query_and_group(feat, xyz, off, query, noff, nsample=3, with_xyz=True)
+    assert idx.cpu().tolist() == [[0, 1, -1]]
+    reused, same = pointcept.knn_query_and_group(feat, xyz, idx=idx, new_xyz=query)
+    assert same is idx and torch.equal(reused, grouped[..., 3:])
+    out = pointcept.interpolation(xyz, query, feat, off, noff, k=3)
+    torch.testing.assert_close(out.cpu(), torch.tensor([[4.]]), atol=1e-5, rtol=1e-5)
+    out.sum().backward()
+    torch.testing.assert_close(feat.grad.cpu(), torch.tensor([[0.75], [0.25]]), atol=1e-5, rtol=1e-5)
+    assert xyz.grad is None and query.grad is None
+    # An empty reference batch interpolates to 0.
+    feat = torch.tensor([[3.]], device="cuda", requires_grad=True)
+    out = pointcept.interpolation(torch.tensor([[10., 0, 0]], device="cuda"),
+                                  torch.tensor([[0., 0, 0], [10., 0, 0]], device="cuda"), feat,
+                                  torch.tensor([0, 1], dtype=torch.int32, device="cuda"),
+                                  torch.tensor([1, 2], dtype=torch.int32, device="cuda"))
+    assert out.cpu().tolist() == [[0.], [3.]]
+    out.sum().backward()
+    assert feat.grad.cpu().tolist() == [[1.]]
+
+
+def test_pointcept_knn_matches_oracle_ragged(cuda_device):
+    """Random ragged batches against the oracle's flat kNN (global indices,
+    (squared distance, index) order), with the 1e5 padding of short batches."""
+    from mps_pointops import pointcept
+
+    g = torch.Generator().manual_seed(21)
+    counts, qcounts = [300, 0, 7, 1000], [50, 20, 30, 40]
+    xyz = torch.rand(sum(counts), 3, generator=g)
+    q = torch.rand(sum(qcounts), 3, generator=g)
+    ends = torch.tensor(counts).cumsum(0)
+    qends = torch.tensor(qcounts).cumsum(0)
+    idx, dist = pointcept.knn_query(16, xyz.cuda(), ends.cuda(), q.cuda(), qends.cuda())
+    ptr_x = np.concatenate([[0], ends.numpy()])
+    ptr_y = np.concatenate([[0], qends.numpy()])
+    want = O.knn_flat(xyz.numpy(), q.numpy(), ptr_x, ptr_y, 16)
+    np.testing.assert_array_equal(host(idx), want)
+    d = host(dist)
+    assert (d[want < 0] == 1e5).all()
+    sel = want >= 0
+    qq = np.repeat(q.numpy()[:, None, :], 16, 1)[sel]
+    delta = (qq - xyz.numpy()[want[sel]]).astype(np.float32)
+    squared = (delta[:, 0] * delta[:, 0] + delta[:, 1] * delta[:, 1]) + delta[:, 2] * delta[:, 2]
+    same_bits(d[sel], np.sqrt(squared))
