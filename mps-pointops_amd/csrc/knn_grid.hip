@@ -610,13 +610,15 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     uint64_t tau = active ? ~0ull : 0ull;
     int cnt = 0;
 
-    // Admit up to n of 8 references into this lane's buffer.
-    auto admit8 = [&](const float4 (&r)[8], int n) {
+    // Admit references base, base + 4, ..., base + 28 into this lane's
+    // buffer (the quad's lanes interleaved, so one load instruction covers 4
+    // consecutive references per quad): slot u while 4u < n.
+    auto admit8s = [&](const float4 (&r)[8], int n) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const uint32_t key = static_cast<uint32_t>(f2i(sqdist3(r[u].x, r[u].y, r[u].z, q[0], q[1], q[2])));
             const uint32_t ix = static_cast<uint32_t>(f2i(r[u].w));
-            if (u < n && key < kGridMatchLimit && grid_word(key, ix) < tau) {
+            if (4 * u < n && key < kGridMatchLimit && grid_word(key, ix) < tau) {
                 buf[cnt * kWave + lane] = make_uint2(key, ix);
                 ++cnt;
             }
@@ -633,7 +635,8 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     bool full = P.nonfinite > 0 || ballot(active && !qfinite) != 0;
     if (!full) {
         // The quad scans the box around its query, 32 references of its
-        // current segment per step (8 per lane), with the bounds of the next
+        // current segment per step (lane j of the quad takes every fourth
+        // from the j-th), with the bounds of the next
         // segment fetched one segment ahead; the four lanes keep identical
         // copies of the walk's state.  When the box is done the quad stops if
         // its K-th key is below the squared bound of everything outside;
@@ -710,11 +713,11 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             }
             if (ballot(!done) == 0) break;
             const bool has = p < e;
-            const int base = has ? p + 8 * qi : 0, last = has ? e - 1 : 0;
+            const int base = has ? p + qi : 0, last = has ? e - 1 : 0;
             float4 rv[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + u, last)];
-            admit8(rv, has ? e - base : 0);
+            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + 4 * u, last)];
+            admit8s(rv, has ? e - base : 0);
             if (has) p += 32;
         }
     }
@@ -728,11 +731,11 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
         const int hi = off[P.cells + 1];
         for (int g0 = 0; g0 < hi; g0 += 32) {
             drain(false);
-            const int base = g0 + 8 * qi;
+            const int base = g0 + qi;
             float4 rv[8];
 #pragma unroll
-            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + u, hi - 1)];
-            admit8(rv, hi - base);
+            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + 4 * u, hi - 1)];
+            admit8s(rv, hi - base);
         }
     }
     quad_merge<S>(slot, tau, buf, lane, cnt);
