@@ -173,8 +173,9 @@ hipError_t pointops_group_points(const float *features, const void *idx, int idx
 
 /* The gradient of that gather (compat.py:62-73, torch.gather's scatter-add):
  * grad_features[b,c,n] = the float sum of grad_out[b,c,p] over the p with
- * idx[b,p] = n, added in increasing p (deterministic; 0 for a point never
- * gathered; every element is written).  grad_out channel c of batch b starts
+ * idx[b,p] = n, added in increasing p for a point gathered at most 256 times
+ * (deterministic), in an unspecified order for one gathered more often; 0
+ * for a point never gathered; every element is written.  grad_out channel c of batch b starts
  * at grad_out + b*grad_batch_stride + c*P (grad_batch_stride >= C*P, so a
  * channel slice of a larger tensor can be passed).  `workspace` holds
  * pointops_group_points_backward_workspace_bytes(B, C, N, P) bytes (the

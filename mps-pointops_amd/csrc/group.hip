@@ -77,8 +77,9 @@ __global__ __launch_bounds__(kGroupThreads) void group_points_rel_kernel(
 }
 
 // Backward: grad_features[b,c,n] = sum of grad_out[b,c,p] over the p with
-// idx[b,p] = n, added in increasing p (the order of a sequential loop), so
-// the result is deterministic.  The inverse of the index is built per call
+// idx[b,p] = n, added in increasing p (the order of a sequential loop, so
+// the result is deterministic) for points gathered at most 256 times; a
+// point gathered more often sums in an unspecified order.  The inverse of the index is built per call
 // in the workspace: per batch, counts of each point (the atomic return value
 // is the entry's rank), an exclusive scan into offsets, placement of each p
 // at offset + rank (in no particular order within a point), grad_out
@@ -192,9 +193,9 @@ __global__ __launch_bounds__(kGroupThreads) void group_place_kernel(const I* __r
 // One wave per (b, n, 64 channels), lane = channel: the wave walks the
 // point's entries in increasing p -- each step takes the smallest entry
 // above the previous one (a wave minimum over the entries, held four per lane
-// for lists of up to 256, else re-read from the list) -- and adds that
-// entry's gradient to every lane's channel.  Entries are distinct, so the
-// walk visits each once, in order, without sorting the list.
+// for lists of up to 256) -- and adds that entry's gradient to every lane's
+// channel.  Entries are distinct, so the walk visits each once, in order,
+// without sorting the list.
 constexpr int kGroupListRegs = 4;
 __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
     GroupInverse V, float* __restrict__ gf, int64_t C, int64_t N, int64_t P, int64_t chunks) {
@@ -227,15 +228,10 @@ __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
             acc = acc + gc[static_cast<int64_t>(last) * C];
         }
     } else {
-        for (int t = 0; t < L; ++t) {
-            int m = INT_MAX;
-            for (int i = lane; i < L; i += kWave) {
-                const int v = l[i];
-                m = min(m, v > last ? v : INT_MAX);
-            }
-            last = wave_min(m);
-            acc = acc + gc[static_cast<int64_t>(last) * C];
-        }
+        // A point gathered more than 256 times: its entries in list order
+        // (the order the counting pass placed them, which varies between
+        // runs), O(L) rather than an O(L^2) ordered walk.
+        for (int i = 0; i < L; ++i) acc = acc + gc[static_cast<int64_t>(l[i]) * C];
     }
     if (live) gf[(b * C + c) * N + n] = acc;
 }

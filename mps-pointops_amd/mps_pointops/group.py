@@ -13,7 +13,8 @@ float32 GPU tensors (``device='cuda'``) run ``libpointops_hip.so``; other
 devices and dtypes keep the reference's ``torch.gather`` formulation.  Index
 gradients are none; feature and xyz gradients are float sums over each
 point's entries in increasing entry order (deterministic), like a sequential
-scatter-add.
+scatter-add, for points gathered at most 256 times; a point gathered more
+often sums in an unspecified order.
 """
 
 from __future__ import annotations

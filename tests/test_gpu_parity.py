@@ -1036,3 +1036,20 @@ def test_pointcept_knn_matches_oracle_ragged(cuda_device):
     delta = (qq - xyz.numpy()[want[sel]]).astype(np.float32)
     squared = (delta[:, 0] * delta[:, 0] + delta[:, 1] * delta[:, 1]) + delta[:, 2] * delta[:, 2]
     same_bits(d[sel], np.sqrt(squared))
+
+
+def test_group_points_backward_heavily_repeated_point(cuda_device):
+    """A point gathered far more than 256 times (all-zero indices, as the
+    pointnet2 padding of queries without neighbours produces) sums in an
+    unspecified order; with quarter-integer gradients every order is exact,
+    so the result still equals the sequential oracle bit for bit (a dropped
+    or repeated term would not)."""
+    from mps_pointops import group
+
+    g = torch.Generator().manual_seed(31)
+    f = torch.randn(2, 70, 100, generator=g).cuda().requires_grad_()
+    idx = torch.zeros(2, 40_000, dtype=torch.int32)
+    idx[:, ::7] = torch.randint(0, 100, (2, len(range(0, 40_000, 7))), generator=g, dtype=torch.int32)
+    go = torch.randint(-8, 9, (2, 70, 40_000), generator=g).float() / 4
+    group.group_points(f, idx.cuda()).backward(go.cuda())
+    same_bits(host(f.grad), O.group_points_backward(go.numpy(), idx.numpy(), 100))
