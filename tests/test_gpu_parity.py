@@ -1053,3 +1053,41 @@ def test_group_points_backward_heavily_repeated_point(cuda_device):
     go = torch.randint(-8, 9, (2, 70, 40_000), generator=g).float() / 4
     group.group_points(f, idx.cuda()).backward(go.cuda())
     same_bits(host(f.grad), O.group_points_backward(go.numpy(), idx.numpy(), 100))
+
+
+def _grid_sweep_case(seed: int):
+    """Random shapes and distributions for the grid search: uniform boxes,
+    Gaussian blobs, sphere surfaces, points on a line (degenerate extents)
+    and heavily duplicated points."""
+    g = torch.Generator().manual_seed(1000 + seed)
+    B = int(torch.randint(1, 4, (1,), generator=g))
+    N = int(torch.randint(2000, 40_000, (1,), generator=g))
+    M = int(torch.randint(50, 2500, (1,), generator=g))
+    kind = seed % 5
+    if kind == 0:
+        ref = torch.rand(B, N, 3, generator=g) * float(torch.rand(1, generator=g) * 100 + 0.01)
+    elif kind == 1:
+        cen = torch.randn(B, 8, 3, generator=g) * 5
+        ref = cen[:, torch.randint(0, 8, (N,), generator=g)] + torch.randn(B, N, 3, generator=g) * 0.3
+    elif kind == 2:
+        d = torch.randn(B, N, 3, generator=g)
+        ref = d / d.norm(dim=-1, keepdim=True)
+    elif kind == 3:
+        t = torch.rand(B, N, 1, generator=g)
+        ref = t * torch.tensor([1.0, 2.0, -0.5]) + 3.0
+    else:
+        base = torch.rand(B, N // 50 + 1, 3, generator=g)
+        ref = base[:, torch.randint(0, base.shape[1], (N,), generator=g)]
+    pick = torch.randint(0, N, (M,), generator=g)
+    query = ref[:, pick] + torch.randn(B, M, 3, generator=g) * 0.05
+    return query.contiguous(), ref.contiguous()
+
+
+@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("k", [3, 12, 32])
+def test_knn3_grid_random_sweep(cuda_device, seed, k):
+    query, ref = _grid_sweep_case(seed)
+    want_d, want_i = O.knn3(query, ref, k)
+    d, i = _knn3_grid(query, ref, k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
