@@ -202,7 +202,7 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_bounds_kernel(const flo
 // into the bounding box of its finite references and choose the grid; lane 0
 // stores it to *out.
 __device__ void grid_params(const GridLayout& L, int64_t b, int64_t N, int parts, int K,
-                            GridParams* out) {
+                            float hmin, GridParams* out) {
     const int lane = threadIdx.x;
     float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
     int nonfinite = 0;
@@ -242,6 +242,7 @@ __device__ void grid_params(const GridLayout& L, int64_t b, int64_t N, int parts
                                              static_cast<double>(N) / grid_per_cell(K)));
         hside = static_cast<float>(cbrt(vol / target));
         if (!(hside > 0.f)) hside = emax;
+        if (hside < hmin) hside = hmin;  // a caller's smallest useful cell (ball radius)
     }
     int dims[3] = {1, 1, 1};
     bool fits = false;
@@ -294,10 +295,10 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const floa
                                                                       const float* __restrict__ query,
                                                                       GridLayout L, int64_t N, int64_t M,
                                                                       uint32_t ref_blocks, int parts,
-                                                                      int K) {
+                                                                      int K, float hmin) {
     __shared__ GridParams shared_params;
     const int64_t b = blockIdx.y;
-    if (threadIdx.x < kWave) grid_params(L, b, N, parts, K, &shared_params);
+    if (threadIdx.x < kWave) grid_params(L, b, N, parts, K, hmin, &shared_params);
     __syncthreads();
     const GridParams P = shared_params;
     if (blockIdx.x == 0 && threadIdx.x == 0) L.params[b] = P;
@@ -752,10 +753,217 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     }
 }
 
+// Exact first-K ball query over the same grid (the result of
+// pointops_ball_query_f32 without lengths: the K smallest indices j with
+// fl32((dx^2 + dy^2) + dz^2) < r2, ascending, then (-1, 0) padding; a
+// non-finite query or point never matches).  A quad of lanes per query scans
+// every cell of the box that covers the query's ball -- [q - rb, q + rb] per
+// axis, rb = sqrt(r2) (1 + 2^-10) plus a slack of 2^-20 of the coordinate
+// magnitude, wider than every point with d < r2 given float rounding, and
+// cell assignment is monotone in the coordinate -- keeping an ascending list
+// of (index, distance bits) words spread over the quad as in the kNN search.
+// A reference whose index is not below the list's K-th is skipped before
+// its distance is computed.  Non-finite references sit in the overflow cell,
+// which no box reaches; they could not match anyway.
+template <int S>
+__global__ __launch_bounds__(kGridSearchWaves * kWave) void ball3_grid_kernel(
+    const float* __restrict__ query, GridLayout L, int64_t* __restrict__ out_idx,
+    float* __restrict__ out_dist, int64_t B, int64_t M, int64_t N, int K, float r2) {
+    constexpr int KMAX = 4 * S;
+    __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
+    const int lane = lane_id();
+    const int qi = lane & 3;
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t groups = (M + kGridQueriesPerWave - 1) / kGridQueriesPerWave;
+    const int64_t gw = static_cast<int64_t>(xcd_local_block(blockIdx.x, gridDim.x)) * kGridSearchWaves + wave;
+    if (gw >= B * groups) return;  // whole wave; no barriers in this kernel
+    const int64_t b = gw / groups;
+    const int64_t pos = (gw - b * groups) * kGridQueriesPerWave + (lane >> 2);
+    const bool active = pos < M;
+    const int m = active ? L.q_order[b * M + pos] : 0;
+    const float* qp = query + 3 * (b * M + m);
+    const float q[3] = {qp[0], qp[1], qp[2]};
+    const GridParams P = L.params[b];
+    const int* off = L.ref_off + b * L.stride;
+    const float4* srt = L.sorted + b * N;
+    uint2* buf = &bufs[wave][0][0];
+    const bool live = active && finite3(q[0], q[1], q[2]) && r2 > 0.f;
+
+    uint64_t slot[S];
+#pragma unroll
+    for (int s = 0; s < S; ++s) slot[s] = (live && S * qi + s >= KMAX - K) ? ~0ull : 0ull;
+    uint64_t tau = live ? ~0ull : 0ull;
+    int cnt = 0;
+    auto admit8s = [&](const float4 (&r)[8], int n) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const uint32_t ix = static_cast<uint32_t>(f2i(r[u].w));
+            if (4 * u < n && grid_word(ix, 0u) < tau) {
+                const float d = sqdist3(r[u].x, r[u].y, r[u].z, q[0], q[1], q[2]);
+                if (d < r2) {
+                    buf[cnt * kWave + lane] = make_uint2(ix, static_cast<uint32_t>(f2i(d)));
+                    ++cnt;
+                }
+            }
+        }
+    };
+
+    const float h = 1.f / P.inv_h;
+    int c0[3], c1[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float slack = (fabsf(q[a]) + fabsf(P.lo[a]) + static_cast<float>(P.dims[a]) * h) * 0x1p-20f;
+        const float rb = sqrtf(r2) * (1.f + 0x1p-10f) + slack;
+        c0[a] = cell_axis(q[a] - rb, P.lo[a], P.inv_h, P.dims[a]);
+        c1[a] = cell_axis(q[a] + rb, P.lo[a], P.inv_h, P.dims[a]);
+    }
+    const int ny = c1[1] - c0[1] + 1, nseg = ny * (c1[2] - c0[2] + 1);
+    int g = 0, p = 0, e = 0, np = 0, ne = 0;
+    auto fetch = [&]() {
+        const int y = c0[1] + g % ny, z = c0[2] + g / ny;
+        const int row = P.dims[0] * (y + P.dims[1] * z);
+        np = off[row + c0[0]];
+        ne = off[row + c1[0] + 1];
+    };
+    bool done = !live;
+    if (!done) fetch();
+    for (;;) {
+        if (ballot(cnt > kGridCap - 8) != 0) {
+            quad_merge<S>(slot, tau, buf, lane, cnt);
+            cnt = 0;
+        }
+        while (!done && p >= e) {  // uniform within each quad
+            if (g < nseg) {
+                p = np;
+                e = ne;
+                ++g;
+                if (g < nseg) fetch();
+            } else {
+                done = true;
+            }
+        }
+        if (ballot(!done) == 0) break;
+        const bool has = p < e;
+        const int base = has ? p + qi : 0, last = has ? e - 1 : 0;
+        float4 rv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + 4 * u, last)];
+        admit8s(rv, has ? e - base : 0);
+        if (has) p += 32;
+    }
+    quad_merge<S>(slot, tau, buf, lane, cnt);
+    if (!active) return;
+    const int64_t row = (b * M + m) * K;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+        const int r = S * qi + s - (KMAX - K);
+        if (r >= 0) {
+            const bool empty = !live || slot[s] == ~0ull;
+            out_idx[row + r] = empty ? -1 : static_cast<int64_t>(slot[s] >> 32);
+            out_dist[row + r] = empty ? 0.f : i2f(static_cast<int>(static_cast<uint32_t>(slot[s])));
+        }
+    }
+}
+
+// Bounding box of each cloud's finite points, (min xyz, max xyz) per batch:
+// partial boxes of up to kGridBoundBlocks workgroups per batch, then one wave
+// per batch combines them.  Used by callers that size a search from the
+// clouds' density.
+__global__ __launch_bounds__(kGridPrepThreads) void cloud_bounds_partial_kernel(
+    const float* __restrict__ pts, float* __restrict__ partial, int64_t N) {
+    __shared__ float red[6][kGridPrepThreads / kWave];
+    const int64_t b = blockIdx.y;
+    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+    const int64_t step = static_cast<int64_t>(gridDim.x) * kGridPrepThreads;
+    const float* r = pts + 3 * b * N;
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + tid; j < N; j += step) {
+        const float x = r[3 * j], y = r[3 * j + 1], z = r[3 * j + 2];
+        if (finite3(x, y, z)) {
+            mn[0] = fminf(mn[0], x); mx[0] = fmaxf(mx[0], x);
+            mn[1] = fminf(mn[1], y); mx[1] = fmaxf(mx[1], y);
+            mn[2] = fminf(mn[2], z); mx[2] = fmaxf(mx[2], z);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        const float wmn = wave_min(mn[a]), wmx = wave_max(mx[a]);
+        if (lane == 0) {
+            red[a][wave] = wmn;
+            red[3 + a][wave] = wmx;
+        }
+    }
+    __syncthreads();
+    if (tid >= 6) return;
+    float v = red[tid][0];
+    for (int w = 1; w < kGridPrepThreads / kWave; ++w) v = tid < 3 ? fminf(v, red[tid][w]) : fmaxf(v, red[tid][w]);
+    partial[(b * gridDim.x + blockIdx.x) * 6 + tid] = v;
+}
+
+__global__ __launch_bounds__(kWave) void cloud_bounds_final_kernel(const float* __restrict__ partial,
+                                                                  float* __restrict__ out, int parts) {
+    const int64_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (int i = lane; i < parts; i += kWave) {
+        const float* t = partial + (b * parts + i) * 6;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            mn[a] = fminf(mn[a], t[a]);
+            mx[a] = fmaxf(mx[a], t[3 + a]);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        mn[a] = wave_min(mn[a]);
+        mx[a] = wave_max(mx[a]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            out[b * 6 + a] = mn[a];
+            out[b * 6 + 3 + a] = mx[a];
+        }
+    }
+}
+
 }  // namespace
 }  // namespace pointops
 
 using namespace pointops;
+
+namespace {
+
+// The five build launches shared by the kNN and ball-query searches.
+void grid_build(const float* query, const float* ref, const GridLayout& L, int64_t B, int64_t M,
+                int64_t N, int K, float hmin, hipStream_t stream) {
+    const uint32_t nb = static_cast<uint32_t>(B);
+    const uint32_t ref_blocks = static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads);
+    const uint32_t q_blocks = static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads);
+    const dim3 point_grid(ref_blocks + q_blocks, nb);
+    const dim3 scan_grid(static_cast<uint32_t>(L.tiles), nb, 2);
+    const int parts = static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
+    const dim3 prep(kGridPrepThreads);
+    hipLaunchKernelGGL(grid_bounds_kernel, dim3(static_cast<uint32_t>(parts), nb), prep, 0, stream,
+                       ref, L, N);
+    hipLaunchKernelGGL(grid_count_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks,
+                       parts, K, hmin);
+    hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
+    hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
+    hipLaunchKernelGGL(grid_scatter_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks);
+}
+
+// Search launch shape: 16 queries per wave, kGridSearchWaves waves per
+// workgroup, a multiple of 8 workgroups for the XCD-local deal.
+bool grid_search_grid(int64_t B, int64_t M, dim3& grid) {
+    const int64_t waves = B * ((M + kGridQueriesPerWave - 1) / kGridQueriesPerWave);
+    const int64_t blocks = ((waves + kGridSearchWaves - 1) / kGridSearchWaves + 7) / 8 * 8;
+    if (blocks > INT32_MAX) return false;
+    grid = dim3(static_cast<uint32_t>(blocks));
+    return true;
+}
+
+}  // namespace
 
 extern "C" {
 
@@ -772,26 +980,12 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     if (N >= (int64_t(1) << 31) - 64 || M >= (int64_t(1) << 31) - 64 || B > 65535 ||
         workspace == nullptr)
         return hipErrorInvalidValue;
+    dim3 grid;
+    if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
-    const uint32_t nb = static_cast<uint32_t>(B);
-    const uint32_t ref_blocks = static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads);
-    const uint32_t q_blocks = static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads);
-    const dim3 point_grid(ref_blocks + q_blocks, nb);
-    const dim3 scan_grid(static_cast<uint32_t>(L.tiles), nb, 2);
-    const int parts = static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
-    const dim3 prep(kGridPrepThreads);
-    hipLaunchKernelGGL(grid_bounds_kernel, dim3(static_cast<uint32_t>(parts), nb), prep, 0, stream,
-                       ref, L, N);
-    hipLaunchKernelGGL(grid_count_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks,
-                       parts, static_cast<int>(K));
-    hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
-    hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
-    hipLaunchKernelGGL(grid_scatter_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks);
-    const int64_t waves = B * ((M + kGridQueriesPerWave - 1) / kGridQueriesPerWave);
-    const int64_t blocks = ((waves + kGridSearchWaves - 1) / kGridSearchWaves + 7) / 8 * 8;
-    if (blocks > INT32_MAX) return hipErrorInvalidValue;
-    const dim3 grid(static_cast<uint32_t>(blocks)), block(kGridSearchWaves * kWave);
+    grid_build(query, ref, L, B, M, N, static_cast<int>(K), 0.f, stream);
+    const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
         hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
@@ -801,6 +995,57 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
         hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
     else
         hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+    return hipGetLastError();
+}
+
+size_t pointops_cloud_bounds_workspace_bytes(int64_t B) {
+    return B <= 0 ? 0 : static_cast<size_t>(B) * kGridBoundBlocks * 6 * sizeof(float);
+}
+
+hipError_t pointops_cloud_bounds(const float* points, float* out, void* workspace, int64_t B,
+                                 int64_t N, hipStream_t stream) {
+    if (B < 0 || N < 0 || B > 65535) return hipErrorInvalidValue;
+    if (B == 0) return hipSuccess;
+    if (workspace == nullptr || out == nullptr || points == nullptr) return hipErrorInvalidValue;
+    const int parts = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096)));
+    auto* partial = static_cast<float*>(workspace);
+    hipLaunchKernelGGL(cloud_bounds_partial_kernel, dim3(static_cast<uint32_t>(parts), static_cast<uint32_t>(B)),
+                       dim3(kGridPrepThreads), 0, stream, points, partial, N);
+    hipLaunchKernelGGL(cloud_bounds_final_kernel, dim3(static_cast<uint32_t>(B)), dim3(kWave), 0, stream,
+                       partial, out, parts);
+    return hipGetLastError();
+}
+
+size_t pointops_ball_query_grid_workspace_bytes(int64_t B, int64_t Q, int64_t P) {
+    return pointops_knn3_grid_workspace_bytes(B, Q, P);
+}
+
+hipError_t pointops_ball_query_grid_f32(const float* queries, const float* points, int64_t* idx,
+                                        float* dist2, void* workspace, int64_t B, int64_t Q,
+                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream) {
+    if (B < 0 || Q < 0 || P < 0 || K < 0 || K > 64) return hipErrorInvalidValue;
+    if (B == 0 || Q == 0 || K == 0) return hipSuccess;
+    if (P == 0 || P >= (int64_t(1) << 31) - 64 || Q >= (int64_t(1) << 31) - 64 || B > 65535 ||
+        workspace == nullptr)
+        return hipErrorInvalidValue;
+    dim3 grid;
+    if (!grid_search_grid(B, Q, grid)) return hipErrorInvalidValue;
+    GridLayout L;
+    grid_layout_bytes(B, Q, P, &L, static_cast<char*>(workspace));
+    const float hmin = (radius_sq > 0.f && radius_sq < INFINITY) ? sqrtf(radius_sq) : 0.f;
+    grid_build(queries, points, L, B, Q, P, static_cast<int>(K), hmin, stream);
+    const dim3 block(kGridSearchWaves * kWave);
+    const int k = static_cast<int>(K);
+    if (K <= 4)
+        hipLaunchKernelGGL((ball3_grid_kernel<1>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
+    else if (K <= 8)
+        hipLaunchKernelGGL((ball3_grid_kernel<2>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
+    else if (K <= 16)
+        hipLaunchKernelGGL((ball3_grid_kernel<4>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
+    else if (K <= 32)
+        hipLaunchKernelGGL((ball3_grid_kernel<8>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
+    else
+        hipLaunchKernelGGL((ball3_grid_kernel<16>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
     return hipGetLastError();
 }
 

@@ -1091,3 +1091,101 @@ def test_knn3_grid_random_sweep(cuda_device, seed, k):
     d, i = _knn3_grid(query, ref, k)
     np.testing.assert_array_equal(i, want_i)
     same_bits(d, want_d)
+
+
+# ------------------------------------------------------- grid ball query
+
+
+def _ball_grid(query: torch.Tensor, ref: torch.Tensor, radius: float, k: int):
+    """pointops_ball_query_grid_f32 through the C ABI (any cloud size)."""
+    from mps_pointops import _native
+
+    q, r = query.cuda().contiguous(), ref.cuda().contiguous()
+    B, Q, _ = q.shape
+    P = r.shape[1]
+    dist = torch.empty(B, Q, k, device="cuda")
+    idx = torch.empty(B, Q, k, dtype=torch.long, device="cuda")
+    size = _native.size_query("pointops_ball_query_grid_workspace_bytes", B, Q, P)
+    ws = torch.empty(size, dtype=torch.uint8, device="cuda")
+    _native.call("pointops_ball_query_grid_f32", q.data_ptr(), r.data_ptr(), idx.data_ptr(),
+                 dist.data_ptr(), ws.data_ptr(), B, Q, P, k, O.ball_radius_sq(radius),
+                 _native.stream(q.device))
+    return host(dist), host(idx)
+
+
+@pytest.mark.parametrize("name,radius", [("uniform", 0.4), ("slab", 0.5), ("ties", 1.0),
+                                         ("far_queries", 0.3), ("sparse_clusters", 2.0),
+                                         ("flat", 0.05), ("one_point", 0.5),
+                                         ("non_finite_refs", 0.2), ("non_finite_queries", 0.2),
+                                         ("uniform", 0.0), ("uniform", 1e30)])
+@pytest.mark.parametrize("k", [1, 16, 32, 64])
+def test_ball_query_grid_matches_oracle(cuda_device, name, radius, k):
+    """The grid ball query returns the index-order first-K answer bit for bit
+    (also radius 0: no hit, and a radius whose square overflows: every finite
+    point)."""
+    query, ref = _grid_case(name)
+    want_d, want_i = O.ball_query(query, ref, radius, k)
+    d, i = _ball_grid(query, ref, radius, k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_ball_query_grid_random_sweep(cuda_device, seed):
+    query, ref = _grid_sweep_case(seed)
+    span = float((ref.amax(1) - ref.amin(1)).max())
+    for frac, k in ((0.01, 8), (0.05, 32), (0.2, 64)):
+        want_d, want_i = O.ball_query(query, ref, span * frac, k)
+        d, i = _ball_grid(query, ref, span * frac, k)
+        np.testing.assert_array_equal(i, want_i)
+        same_bits(d, want_d)
+
+
+def test_ball_query_grid_public_path(cuda_device):
+    """ops.ball_query uses the grid search for large clouds without lengths;
+    results equal the index-order kernel's, and gradients still flow."""
+    import mps_pointops as mp
+    from mps_pointops import _native
+
+    g = torch.Generator().manual_seed(12)
+    ref = bench.make_c3(N=80_000)
+    query = ref[:, torch.randperm(80_000, generator=g)[:3000]].clone()
+    q, r = query.cuda().requires_grad_(), ref.cuda()
+    d, i = mp.ball_query(q, r, 0.5, 32)
+    bd = torch.empty_like(d)
+    bi = torch.empty_like(i)
+    _native.call("pointops_ball_query_f32", q.data_ptr(), r.data_ptr(), None, None, bi.data_ptr(),
+                 bd.data_ptr(), 1, 3000, 80_000, 32, O.ball_radius_sq(0.5), _native.stream(q.device))
+    np.testing.assert_array_equal(host(i), host(bi))
+    same_bits(host(d), host(bd))
+    d.sum().backward()
+    assert q.grad is not None and torch.isfinite(q.grad).all()
+
+
+def test_cloud_bounds_matches_numpy(cuda_device):
+    """pointops_cloud_bounds: per-cloud min/max of the finite points (exact,
+    min/max round nothing); a cloud with none gives +inf/-inf; many blocks."""
+    from mps_pointops import _native
+
+    rng = np.random.default_rng(5)
+    for B, N in ((1, 1), (3, 1000), (2, 300_000), (4, 4097)):
+        pts = (rng.standard_normal((B, N, 3)) * rng.uniform(0.1, 50, (B, 1, 3))).astype(np.float32)
+        if N > 10:
+            pts[0, 3] = (np.inf, 0.0, 0.0)
+            pts[-1, N // 2] = (np.nan, 1e30, -1e30)
+        if B > 2:
+            pts[1] = np.nan
+        x = torch.from_numpy(pts).cuda()
+        out = torch.empty((B, 6), dtype=torch.float32, device=x.device)
+        size = _native.size_query("pointops_cloud_bounds_workspace_bytes", B)
+        ws = torch.empty(size, dtype=torch.uint8, device=x.device)
+        _native.call("pointops_cloud_bounds", x.data_ptr(), out.data_ptr(), ws.data_ptr(), B, N,
+                     _native.stream(x.device))
+        got = host(out)
+        for b in range(B):
+            finite = pts[b][np.isfinite(pts[b]).all(axis=1)]
+            if len(finite) == 0:
+                want = np.array([np.inf] * 3 + [-np.inf] * 3, dtype=np.float32)
+            else:
+                want = np.concatenate([finite.min(axis=0), finite.max(axis=0)])
+            np.testing.assert_array_equal(got[b], want, err_msg=f"B={B} N={N} b={b}")
