@@ -116,6 +116,10 @@ hipError_t pointops_ball_query_f32(const float *queries, const float *points,
                                    const int64_t *query_lengths, const int64_t *point_lengths,
                                    int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
                                    int64_t K, float radius_sq, hipStream_t stream);
+hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *points,
+                                   const int64_t *query_lengths, const int64_t *point_lengths,
+                                   int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
+                                   int64_t K, float radius_sq, hipStream_t stream);
 /* The same query (identical results) over the uniform grid of
  * pointops_knn3_grid, for large clouds without lengths, 1 <= K <= 64, P >= 1:
  * each query scans the cells that cover its ball and keeps its K smallest
@@ -123,6 +127,9 @@ hipError_t pointops_ball_query_f32(const float *queries, const float *points,
  * bytes, no initialisation needed; B <= 65535.  Replaces
  * _ball_query_mps.py:139-162 for that case. */
 size_t pointops_ball_query_grid_workspace_bytes(int64_t B, int64_t Q, int64_t P);
+hipError_t pointops_ball_query_grid_f32(const float *queries, const float *points, int64_t *idx,
+                                        float *dist2, void *workspace, int64_t B, int64_t Q,
+                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream);
 /* Bounding box of each cloud's finite points: out (B, 6) = min xyz, max xyz
  * (+inf, -inf for a cloud with none).  `workspace` holds
  * pointops_cloud_bounds_workspace_bytes(B) bytes.  No reference
@@ -131,13 +138,6 @@ size_t pointops_ball_query_grid_workspace_bytes(int64_t B, int64_t Q, int64_t P)
 size_t pointops_cloud_bounds_workspace_bytes(int64_t B);
 hipError_t pointops_cloud_bounds(const float *points, float *out, void *workspace, int64_t B,
                                  int64_t N, hipStream_t stream);
-hipError_t pointops_ball_query_grid_f32(const float *queries, const float *points, int64_t *idx,
-                                        float *dist2, void *workspace, int64_t B, int64_t Q,
-                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream);
-hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *points,
-                                   const int64_t *query_lengths, const int64_t *point_lengths,
-                                   int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
-                                   int64_t K, float radius_sq, hipStream_t stream);
 
 /* Flat radius search (torch_cluster convention): first K global x indices
  * with squared distance < radius_sq, padded with -1, (Q,K); optional

@@ -303,6 +303,67 @@ def test_fps_skip_near_origin_boundary(cuda_device):
     assert picked.isdisjoint(range(1, 41)) and 41 in picked
 
 
+def _fps_shape_case(case: str) -> tuple[torch.Tensor, int, int, bool]:
+    seeds = {"uniform_exhausted": 1, "blobs_skip": 2, "plane": 3, "duplicates": 4,
+             "mixed_scale": 5, "infinite": 6}
+    g = torch.Generator().manual_seed(seeds[case])
+    if case == "uniform_exhausted":
+        return torch.rand(2, 4096, 3, generator=g), 4096, 17, False
+    if case == "blobs_skip":
+        centres = torch.randn(5, 3, generator=g) * 20
+        x = centres[torch.randint(0, 5, (2, 3000), generator=g)] + torch.randn(2, 3000, 3, generator=g)
+        x[:, ::10] *= 1e-3  # near the origin: never picked
+        return x.contiguous(), 1500, 3, True
+    if case == "plane":
+        x = torch.rand(3, 2500, 3, generator=g)
+        x[..., 2] = 0.0
+        return x, 800, 2499, False
+    if case == "duplicates":
+        base = torch.randn(200, 3, generator=g)
+        return base[torch.randint(0, 200, (2, 4096), generator=g)].contiguous(), 600, 0, False
+    if case == "mixed_scale":
+        x = torch.randn(2, 4000, 3, generator=g) * 1e-3
+        x[:, ::7] = torch.randn(2, 572, 3, generator=g) * 1e4
+        return x, 1000, 5, False
+    if case == "infinite":
+        x = torch.randn(1, 3000, 3, generator=g)
+        x[0, 10] = torch.tensor([float("inf"), 0.0, 0.0])
+        x[0, 2000] = torch.tensor([1.0, float("-inf"), 2.0])
+        return x, 500, 0, False
+    raise ValueError(case)
+
+
+@pytest.mark.parametrize("case", ["uniform_exhausted", "blobs_skip", "plane", "duplicates",
+                                  "mixed_scale", "infinite"])
+def test_fps_cloud_shapes_match_oracle(cuda_device, case):
+    """Clouds of 2049..4096 points (eight per thread of the batched kernel):
+    exhausted clouds (every remaining distance ties at zero), skipped points,
+    a degenerate axis, duplicates, widely mixed scales and infinite
+    coordinates."""
+    import mps_pointops as mp
+
+    xyz, npoint, start, skip = _fps_shape_case(case)
+    want = O.fps(xyz, npoint, start, skip)
+    got = mp.furthest_point_sample(xyz.cuda(), npoint, start, skip)
+    np.testing.assert_array_equal(host(got), want)
+
+
+def test_fps_ragged_up_to_4096_matches_oracle(cuda_device):
+    """A ragged launch whose longest cloud has 2049..4096 points also holds
+    empty, one-point and small clouds."""
+    from mps_pointops import flat
+
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(9000, 3, generator=g)
+    ptr = [0, 0, 1, 3, 70, 70, 2119, 6215, 9000]
+    lengths = np.diff(ptr)
+    got = flat.fps(x.cuda(), ptr=ptr, ratio=0.5, random_start=False)
+    counts = np.ceil(lengths.astype(np.float32) * np.float32(0.5)).astype(np.int64)
+    out_ptr = np.concatenate([[0], np.cumsum(counts)])
+    want = O.fps_flat(x, ptr, out_ptr, np.zeros(len(lengths), np.int64))
+    np.testing.assert_array_equal(host(got), want)
+
+
 def test_fps_c1_and_c2_full(cuda_device):
     import mps_pointops as mp
 
