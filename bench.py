@@ -490,7 +490,7 @@ def main() -> None:
     args = parser.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build measures one MI355X; every workload here runs on one "
-                          "GPU (batch sharding across GPUs is described in DESIGN.md)",
+                          "GPU (sharding the batch of clouds across GPUs is a design, not built)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.probe:
