@@ -87,6 +87,19 @@ size_t pointops_knn3_grid_workspace_bytes(int64_t B, int64_t M, int64_t N);
 hipError_t pointops_knn3_grid(const float *query, const float *ref, float *dist, int64_t *idx,
                               void *workspace, int64_t B, int64_t M, int64_t N, int64_t K,
                               hipStream_t stream);
+/* Nearest reference per query over the same grid (K = 1; the search of
+ * pointops_chamfer_nearest_f32 with norm 2 for clouds without lengths):
+ * dist2 (B,M) the squared distance fl32((dx^2 + dy^2) + dz^2), idx (B,M)
+ * the smallest index attaining it, identical to the linear scan.  A query
+ * whose wave would need more than 6 box faces (nearest reference far away)
+ * or sees a non-finite coordinate gets idx -1 and dist2 +inf: finish those
+ * with a linear scan (pointops_knn_flat with K = 1 per query, or
+ * pointops_chamfer_nearest_f32).  `workspace`:
+ * pointops_knn3_grid_workspace_bytes(B, M, N); N >= 1, B <= 65535.
+ * Accelerates chamfer.py:122-158 for large clouds. */
+hipError_t pointops_nearest3_grid(const float *query, const float *ref, float *dist2,
+                                  int64_t *idx, void *workspace, int64_t B, int64_t M, int64_t N,
+                                  hipStream_t stream);
 
 /* Dense exact kNN in D dimensions (sequential per-dimension accumulation).
  * Replaces ops.py:200-204 (kernels/feature_knn.metal:133-164).  Non-finite

@@ -37,6 +37,7 @@ constexpr int kGridMaxDim = 1024;
 constexpr int kGridSearchWaves = 4;
 constexpr int kGridCap = 16;  // buffered candidates per lane
 constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
+constexpr int kGridNearestGrow = 6;  // nearest mode: faces before the query is left to a scan
 constexpr int kGridQueriesPerWave = kWave / 4;  // one quad of lanes per query
 constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
@@ -576,7 +577,7 @@ __device__ __forceinline__ float box_bound(const GridParams& P, float h, const f
 template <int S>
 __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
-    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K) {
+    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K, int nearest) {
     constexpr int KMAX = 4 * S;
     __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
     const int lane = lane_id();
@@ -683,7 +684,7 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
                     done = true;
                 } else if (qc != 0) {
                     want = true;  // merge first, then check again
-                } else if (grow == kGridMaxGrow) {
+                } else if (grow == (nearest ? kGridNearestGrow : kGridMaxGrow)) {
                     escalate = true;
                     done = true;
                 } else {
@@ -722,6 +723,16 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             if (has) p += 32;
         }
     }
+    if (full && nearest) {
+        // Nearest mode leaves such waves to a linear-scan kernel: index -1.
+        if (!active) return;
+        const int64_t row = (b * M + m) * K;
+        if (qi == 3) {
+            out_dist[row] = INFINITY;
+            out_idx[row] = -1;
+        }
+        return;
+    }
     if (full) {
         // Every reference (the finite ones and the overflow cell), 32 per
         // step per quad.  A list may hold references already, so start over
@@ -747,7 +758,8 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
         const int r = S * qi + s - (KMAX - K);
         if (r >= 0) {
             const uint32_t key = static_cast<uint32_t>(slot[s] >> 32);
-            out_dist[row + r] = slot[s] == ~0ull ? INFINITY : sqrtf(i2f(static_cast<int>(key)));
+            const float d2 = i2f(static_cast<int>(key));
+            out_dist[row + r] = slot[s] == ~0ull ? INFINITY : (nearest ? d2 : sqrtf(d2));
             out_idx[row + r] = static_cast<int64_t>(static_cast<uint32_t>(slot[s]));
         }
     }
@@ -988,13 +1000,31 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
-        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else if (K <= 8)
-        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else if (K <= 16)
-        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else
-        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k);
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+    return hipGetLastError();
+}
+
+hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* dist2,
+                                  int64_t* idx, void* workspace, int64_t B, int64_t M, int64_t N,
+                                  hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
+    if (B == 0 || M == 0) return hipSuccess;
+    if (N == 0 || N >= (int64_t(1) << 31) - 64 || M >= (int64_t(1) << 31) - 64 || B > 65535 ||
+        workspace == nullptr)
+        return hipErrorInvalidValue;
+    dim3 grid;
+    if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
+    GridLayout L;
+    grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
+    grid_build(query, ref, L, B, M, N, 1, 0.f, stream);
+    hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, dim3(kGridSearchWaves * kWave), 0, stream, query,
+                       L, dist2, idx, B, M, N, 1, 1);
     return hipGetLastError();
 }
 

@@ -45,6 +45,7 @@ _SIGNATURES: dict[str, list] = {
     "pointops_three_interpolate_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_ball_query_grid_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_cloud_bounds": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "pointops_nearest3_grid": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_group_points": [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_group_points_backward": [_vp, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_group_points_rel": [_vp, _vp, _vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _i64, _vp],

@@ -92,11 +92,69 @@ def _validate_clouds(x, y, x_lengths, y_lengths) -> tuple[Tensor, Tensor]:
     return lx, ly
 
 
+_GRID_MIN_REFS = 8192
+_GRID_MIN_QUERIES = 4096
+_GRID_MIN_PAIRS = 1 << 26
+
+
+def _grid_eligible(query: Tensor, ref: Tensor, norm: int, full: bool) -> bool:
+    """The grid search serves squared-L2 3-D float32 clouds without lengths
+    that are large enough for its build to pay."""
+    batch, query_count, dimension = query.shape
+    ref_count = ref.shape[1]
+    return (full and norm == 2 and dimension == 3 and query.dtype == torch.float32
+            and ref_count >= _GRID_MIN_REFS and query_count >= _GRID_MIN_QUERIES
+            and batch <= 65535 and batch * query_count * ref_count >= _GRID_MIN_PAIRS)
+
+
+def _nearest_grid(query: Tensor, ref: Tensor) -> tuple[Tensor, Tensor]:
+    """pointops_nearest3_grid, then a linear scan for the queries it left
+    (index -1: their nearest reference is several cells away): one wave per
+    query through the flat kNN (K = 1, the same (squared distance, index)
+    order), squared distances recomputed in the kernels' order with one
+    float32 rounding per operation.  Results equal the scan's everywhere."""
+    from . import flat
+
+    batch, query_count, _ = query.shape
+    ref_count = ref.shape[1]
+    query = query.contiguous()
+    ref = ref.contiguous()
+    distances = torch.empty((batch, query_count), device=query.device, dtype=query.dtype)
+    indices = torch.empty((batch, query_count), device=query.device, dtype=torch.int64)
+    size = _native.size_query("pointops_knn3_grid_workspace_bytes", batch, query_count, ref_count)
+    workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
+    _native.call("pointops_nearest3_grid", query.data_ptr(), ref.data_ptr(), distances.data_ptr(),
+                 indices.data_ptr(), workspace.data_ptr(), batch, query_count, ref_count,
+                 _native.stream(query.device))
+    rows, cols = (indices < 0).nonzero(as_tuple=True)  # batch-major, as the flat layout needs
+    if len(rows):
+        counts = torch.bincount(rows, minlength=batch)
+        ptr_y = torch.zeros(batch + 1, dtype=torch.int64, device=query.device)
+        ptr_y[1:] = counts.cumsum(0)
+        ptr_x = torch.arange(batch + 1, dtype=torch.int64, device=query.device) * ref_count
+        packed = query[rows, cols].contiguous()
+        hit = flat.knn_indices(ref.reshape(-1, 3), packed, ptr_x, ptr_y, 1)[:, 0]
+        delta = packed - ref.reshape(-1, 3)[hit]
+        squared = delta[:, 0] * delta[:, 0]
+        squared = squared + delta[:, 1] * delta[:, 1]
+        squared = squared + delta[:, 2] * delta[:, 2]
+        distances[rows, cols] = squared
+        indices[rows, cols] = hit - rows * ref_count
+    return distances, indices
+
+
 @torch.no_grad()
 def _nearest_device(query: Tensor, ref: Tensor, query_lengths: Tensor, ref_lengths: Tensor,
-                    norm: int = 2) -> tuple[Tensor, Tensor]:
-    """Distance and first-minimum index from the native kernel (the
-    counterpart of chamfer.py:122-158)."""
+                    norm: int = 2, full: bool = False) -> tuple[Tensor, Tensor]:
+    """Distance and first-minimum index from the native kernels (the
+    counterpart of chamfer.py:122-158); ``full``: no lengths were given."""
+    if _grid_eligible(query, ref, norm, full):
+        return _nearest_grid(query, ref)
+    return _nearest_scan(query, ref, query_lengths, ref_lengths, norm)
+
+
+def _nearest_scan(query: Tensor, ref: Tensor, query_lengths: Tensor, ref_lengths: Tensor,
+                  norm: int) -> tuple[Tensor, Tensor]:
     batch, query_count, dimension = query.shape
     ref_count = ref.shape[1]
     if ref_count >= 2**31:
@@ -117,9 +175,10 @@ def _nearest_device(query: Tensor, ref: Tensor, query_lengths: Tensor, ref_lengt
 _nearest_mps = _nearest_device
 
 
-def _nearest_indices(query, ref, query_lengths, ref_lengths, norm: int = 2) -> Tensor:
+def _nearest_indices(query, ref, query_lengths, ref_lengths, norm: int = 2,
+                     full: bool = False) -> Tensor:
     """First-minimum indices under the requested distance (chamfer.py:161-212)."""
-    return _nearest_device(query, ref, query_lengths, ref_lengths, norm)[1]
+    return _nearest_device(query, ref, query_lengths, ref_lengths, norm, full)[1]
 
 
 class _NativeNearest(torch.autograd.Function):
@@ -127,8 +186,8 @@ class _NativeNearest(torch.autograd.Function):
     (norm 1): chamfer.py:215-294."""
 
     @staticmethod
-    def forward(ctx, query, ref, query_lengths, ref_lengths, norm):
-        distances, indices = _nearest_device(query, ref, query_lengths, ref_lengths, norm)
+    def forward(ctx, query, ref, query_lengths, ref_lengths, norm, full=False):
+        distances, indices = _nearest_device(query, ref, query_lengths, ref_lengths, norm, full)
         ctx.save_for_backward(query, ref, indices)
         ctx.norm = norm
         return distances
@@ -137,10 +196,10 @@ class _NativeNearest(torch.autograd.Function):
     @once_differentiable
     def backward(ctx, grad_distances):
         if grad_distances is None:
-            return None, None, None, None, None
+            return None, None, None, None, None, None
         query, ref, indices = ctx.saved_tensors
         if not indices.numel() or ref.shape[1] == 0:
-            return torch.zeros_like(query), torch.zeros_like(ref), None, None, None
+            return torch.zeros_like(query), torch.zeros_like(ref), None, None, None, None
         query = query.contiguous()
         ref = ref.contiguous()
         grad_query = torch.empty_like(query)
@@ -152,7 +211,7 @@ class _NativeNearest(torch.autograd.Function):
                      grad_distances.contiguous().to(query.dtype).data_ptr(),
                      grad_query.data_ptr(), grad_ref.data_ptr(), batch, query_count, ref.shape[1],
                      dimension, ctx.norm, _native.stream(query.device))
-        return grad_query, grad_ref, None, None, None
+        return grad_query, grad_ref, None, None, None, None
 
 
 def _reduce_points(dist: Tensor, lengths: Tensor, mode: PointReduction) -> Tensor:
@@ -209,6 +268,7 @@ def chamfer_distance(
     x, x_lengths, x_normals = _unpack_cloud(x, x_lengths, x_normals, "x")
     y, y_lengths, y_normals = _unpack_cloud(y, y_lengths, y_normals, "y")
     lx, ly = _validate_clouds(x, y, x_lengths, y_lengths)
+    full = x_lengths is None and y_lengths is None  # every point of every cloud is valid
     if x.shape[-1] != 3 and (x_normals is not None or y_normals is not None):
         raise NotImplementedError("normal loss currently requires D == 3")
     _validate_normals(x, x_normals, "x_normals")
@@ -244,10 +304,10 @@ def chamfer_distance(
                     zero_normals = zero_normals.sum()
             return zero_loss, zero_normals
 
-    dx = _NativeNearest.apply(x, y, lx, ly, norm)
+    dx = _NativeNearest.apply(x, y, lx, ly, norm, full)
     nx = None
     if return_normals:
-        ix = _nearest_indices(x, y, lx, ly, norm)
+        ix = _nearest_indices(x, y, lx, ly, norm, full)
         nx = _normal_loss(x_normals, y_normals, ix, lx, ly, abs_cosine)
     if weights is not None:
         dx = dx * weights[:, None]
@@ -259,10 +319,10 @@ def chamfer_distance(
         loss = rx
         normal_loss = rnx
     else:
-        dy = _NativeNearest.apply(y, x, ly, lx, norm)
+        dy = _NativeNearest.apply(y, x, ly, lx, norm, full)
         ny = None
         if return_normals:
-            iy = _nearest_indices(y, x, ly, lx, norm)
+            iy = _nearest_indices(y, x, ly, lx, norm, full)
             ny = _normal_loss(y_normals, x_normals, iy, ly, lx, abs_cosine)
         if weights is not None:
             dy = dy * weights[:, None]

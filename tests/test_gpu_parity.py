@@ -771,6 +771,86 @@ def test_chamfer_c5_forward_backward_reduced(cuda_device):
     np.testing.assert_allclose(host(b.grad), gb, rtol=1e-4, atol=1e-9)
 
 
+def _nearest_grid_case(case: str) -> tuple[torch.Tensor, torch.Tensor]:
+    g = torch.Generator().manual_seed({"c5_xy": 0, "c5_yx": 0, "cube": 1, "duplicates": 2,
+                                       "shell_far_queries": 3}[case])
+    if case in ("c5_xy", "c5_yx"):
+        y1, y2 = bench.make_c5()
+        return (y1, y2) if case == "c5_xy" else (y2, y1)
+    if case == "cube":
+        return torch.rand(4, 9000, 3, generator=g), torch.rand(4, 8192, 3, generator=g)
+    if case == "duplicates":
+        base = torch.randn(500, 3, generator=g)
+        pick = torch.randint(0, 500, (3, 12000), generator=g)
+        return base[pick[:, :5000]].contiguous(), base[pick[:, 3000:]].contiguous()
+    ref = torch.randn(2, 10000, 3, generator=g)
+    ref = ref / ref.norm(dim=-1, keepdim=True)  # a shell: the interior is empty
+    return torch.rand(2, 6000, 3, generator=g) * 0.2 - 0.1, ref
+
+
+@pytest.mark.parametrize("case", ["c5_xy", "c5_yx", "cube", "duplicates", "shell_far_queries"])
+def test_chamfer_nearest_grid_matches_scan(cuda_device, case):
+    """The grid search (and the scan it hands far queries to) returns the
+    linear scan's squared distances and indices bit for bit, ties to the
+    smallest index included."""
+    from mps_pointops import _native, chamfer
+
+    q, r = (t.cuda().contiguous() for t in _nearest_grid_case(case))
+    B, M, N = q.shape[0], q.shape[1], r.shape[1]
+    ql = torch.full((B,), M, dtype=torch.int64, device=q.device)
+    rl = torch.full((B,), N, dtype=torch.int64, device=q.device)
+    assert chamfer._grid_eligible(q, r, 2, True)
+    d, i = chamfer._nearest_device(q, r, ql, rl, 2, full=True)
+    sd, si = chamfer._nearest_scan(q, r, ql, rl, 2)
+    assert torch.equal(i, si)
+    assert torch.equal(d.view(torch.int32), sd.view(torch.int32))
+    if case == "shell_far_queries":  # every query is far: all of them go to the scan
+        size = _native.size_query("pointops_knn3_grid_workspace_bytes", B, M, N)
+        ws = torch.empty(size, dtype=torch.uint8, device=q.device)
+        gd = torch.empty(B, M, device=q.device)
+        gi = torch.empty(B, M, dtype=torch.int64, device=q.device)
+        _native.call("pointops_nearest3_grid", q.data_ptr(), r.data_ptr(), gd.data_ptr(),
+                     gi.data_ptr(), ws.data_ptr(), B, M, N, _native.stream(q.device))
+        assert int((gi < 0).sum()) > 0
+
+
+def test_chamfer_nearest_grid_matches_oracle(cuda_device):
+    """Config 5's clouds at B=2 through the grid path against the oracle."""
+    from mps_pointops import chamfer
+
+    y1, y2 = bench.make_c5(B=2)
+    for q, r in ((y1, y2), (y2, y1)):
+        B, M, N = q.shape[0], q.shape[1], r.shape[1]
+        ql = torch.full((B,), M, dtype=torch.int64, device="cuda")
+        rl = torch.full((B,), N, dtype=torch.int64, device="cuda")
+        qc, rc = q.cuda(), r.cuda()
+        assert chamfer._grid_eligible(qc, rc, 2, True) == (B * M * N >= chamfer._GRID_MIN_PAIRS)
+        d, i = chamfer._nearest_grid(qc, rc)
+        want_d, want_i = O.chamfer_nearest(q, r)
+        np.testing.assert_array_equal(host(i), want_i)
+        np.testing.assert_array_equal(host(d), want_d)
+
+
+def test_chamfer_c5_grid_path_equals_scan_path(cuda_device):
+    """Full config 5: chamfer_distance without lengths (grid search) and with
+    explicit full lengths (linear scan) give bit-identical losses; gradients
+    agree to float rounding (the backward accumulates the reference side with
+    atomics, so its summation order varies from run to run)."""
+    import mps_pointops as mp
+
+    y1, y2 = bench.make_c5()
+    out = []
+    for lengths in (None, torch.full((y1.shape[0],), y1.shape[1], dtype=torch.int64).cuda()):
+        a = y1.cuda().requires_grad_()
+        b = y2.cuda().requires_grad_()
+        loss, _ = mp.chamfer_distance(a, b, x_lengths=lengths, y_lengths=lengths)
+        loss.backward()
+        out.append((loss.detach(), a.grad, b.grad))
+    assert torch.equal(out[0][0].view(torch.int32), out[1][0].view(torch.int32))
+    for got, want in zip(out[0][1:], out[1][1:]):
+        torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-9)
+
+
 @pytest.mark.parametrize("k", [1, 4, 40, 256])
 def test_flat_knn_radius_match_oracle(cuda_device, k):
     from mps_pointops import flat
