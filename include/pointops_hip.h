@@ -90,12 +90,11 @@ hipError_t pointops_knn3_grid(const float *query, const float *ref, float *dist,
 /* Nearest reference per query over the same grid (K = 1; the search of
  * pointops_chamfer_nearest_f32 with norm 2 for clouds without lengths):
  * dist2 (B,M) the squared distance fl32((dx^2 + dy^2) + dz^2), idx (B,M)
- * the smallest index attaining it, identical to the linear scan.  A query
- * whose wave would need more than 6 box faces (nearest reference far away)
- * or sees a non-finite coordinate gets idx -1 and dist2 +inf: finish those
- * with a linear scan (pointops_knn_flat with K = 1 per query, or
- * pointops_chamfer_nearest_f32).  `workspace`:
- * pointops_knn3_grid_workspace_bytes(B, M, N); N >= 1, B <= 65535.
+ * the smallest index attaining it, identical to the linear scan, for
+ * finite coordinates.  Queries whose nearest reference lies more than a few
+ * cells away are finished inside the call by a linear scan over their
+ * cloud.  `workspace`: pointops_knn3_grid_workspace_bytes(B, M, N); N >= 1,
+ * B <= 65535.
  * Accelerates chamfer.py:122-158 for large clouds. */
 hipError_t pointops_nearest3_grid(const float *query, const float *ref, float *dist2,
                                   int64_t *idx, void *workspace, int64_t B, int64_t M, int64_t N,

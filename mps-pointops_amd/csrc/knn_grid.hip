@@ -37,7 +37,11 @@ constexpr int kGridMaxDim = 1024;
 constexpr int kGridSearchWaves = 4;
 constexpr int kGridCap = 16;  // buffered candidates per lane
 constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
-constexpr int kGridNearestGrow = 6;  // nearest mode: faces before the query is left to a scan
+#ifndef POINTOPS_GRID_NEAREST_GROW
+#define POINTOPS_GRID_NEAREST_GROW 6
+#endif
+// Nearest mode: box faces a lane may add before its query is left to the scan.
+constexpr int kGridNearestGrow = POINTOPS_GRID_NEAREST_GROW;
 constexpr int kGridQueriesPerWave = kWave / 4;  // one quad of lanes per query
 constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
@@ -939,6 +943,82 @@ __global__ __launch_bounds__(kWave) void cloud_bounds_final_kernel(const float* 
     }
 }
 
+// Nearest mode's second pass: one workgroup per 64 consecutive queries of
+// the grid's query order (cell-sorted, so the queries the search left are
+// clustered and most workgroups return at once); 8 waves split the
+// references, lane = query, references read with uniform loads, and the
+// best (squared distance, smallest index) per wave is combined in LDS.
+constexpr int kFillThreads = 512;
+
+__global__ __launch_bounds__(kFillThreads) void nearest_fill_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref, GridLayout L,
+    float* __restrict__ dist2, int64_t* __restrict__ idx, int64_t M, int64_t N) {
+    constexpr int NWF = kFillThreads / kWave;
+    __shared__ int keys[NWF][kWave];
+    __shared__ int ids[NWF][kWave];
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t groups = (M + kWave - 1) / kWave;
+    const int64_t b = blockIdx.x / groups;
+    const int64_t pos = (blockIdx.x - b * groups) * kWave + lane;
+    const bool active = pos < M;
+    const int64_t row = b * M + (active ? L.q_order[b * M + pos] : 0);
+    const bool need = active && idx[row] < 0;
+    if (ballot(need) == 0) return;  // the same in every wave: before any barrier
+    const float qx = query[3 * row], qy = query[3 * row + 1], qz = query[3 * row + 2];
+    const float* rp = ref + 3 * b * N;
+    const int64_t per = (N + NWF - 1) / NWF;
+    const int64_t lo = min(N, wave * per), hi = min(N, lo + per);
+    int best = 0x7FFFFFFF, bi = 0;
+    // Batches of 8 references (24 consecutive floats, wide scalar loads),
+    // the next batch loaded before the current one is scanned; ascending
+    // order keeps the first minimum.
+    const int64_t hi8 = lo + ((hi - lo) & ~int64_t(7));
+    float cur[24], nxt[24];
+    if (lo < hi8) {
+#pragma unroll
+        for (int t = 0; t < 24; ++t) cur[t] = rp[3 * lo + t];
+    }
+    for (int64_t j = lo; j < hi8; j += 8) {
+        if (j + 8 < hi8) {
+#pragma unroll
+            for (int t = 0; t < 24; ++t) nxt[t] = rp[3 * (j + 8) + t];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int key = f2i(sqdist3(cur[3 * u], cur[3 * u + 1], cur[3 * u + 2], qx, qy, qz));
+            if (key < best) {
+                best = key;
+                bi = static_cast<int>(j + u);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < 24; ++t) cur[t] = nxt[t];
+    }
+    for (int64_t j = hi8; j < hi; ++j) {
+        const int key = f2i(sqdist3(rp[3 * j], rp[3 * j + 1], rp[3 * j + 2], qx, qy, qz));
+        if (key < best) {
+            best = key;
+            bi = static_cast<int>(j);
+        }
+    }
+    keys[wave][lane] = best;
+    ids[wave][lane] = bi;
+    __syncthreads();
+    if (wave != 0 || !need) return;
+    int k = keys[0][lane], i = ids[0][lane];
+#pragma unroll
+    for (int w = 1; w < NWF; ++w) {
+        const int kk = keys[w][lane], ii = ids[w][lane];
+        if (kk < k || (kk == k && ii < i)) {
+            k = kk;
+            i = ii;
+        }
+    }
+    dist2[row] = i2f(k);
+    idx[row] = i;
+}
+
 }  // namespace
 }  // namespace pointops
 
@@ -1016,7 +1096,7 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     if (B < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
     if (B == 0 || M == 0) return hipSuccess;
     if (N == 0 || N >= (int64_t(1) << 31) - 64 || M >= (int64_t(1) << 31) - 64 || B > 65535 ||
-        workspace == nullptr)
+        workspace == nullptr || B * ((M + kWave - 1) / kWave) > INT32_MAX)
         return hipErrorInvalidValue;
     dim3 grid;
     if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
@@ -1025,6 +1105,9 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     grid_build(query, ref, L, B, M, N, 1, 0.f, stream);
     hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, dim3(kGridSearchWaves * kWave), 0, stream, query,
                        L, dist2, idx, B, M, N, 1, 1);
+    const int64_t fill_blocks = B * ((M + kWave - 1) / kWave);
+    hipLaunchKernelGGL(nearest_fill_kernel, dim3(static_cast<uint32_t>(fill_blocks)),
+                       dim3(kFillThreads), 0, stream, query, ref, L, dist2, idx, M, N);
     return hipGetLastError();
 }
 

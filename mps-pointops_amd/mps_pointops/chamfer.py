@@ -108,13 +108,9 @@ def _grid_eligible(query: Tensor, ref: Tensor, norm: int, full: bool) -> bool:
 
 
 def _nearest_grid(query: Tensor, ref: Tensor) -> tuple[Tensor, Tensor]:
-    """pointops_nearest3_grid, then a linear scan for the queries it left
-    (index -1: their nearest reference is several cells away): one wave per
-    query through the flat kNN (K = 1, the same (squared distance, index)
-    order), squared distances recomputed in the kernels' order with one
-    float32 rounding per operation.  Results equal the scan's everywhere."""
-    from . import flat
-
+    """pointops_nearest3_grid: the grid search, and a linear scan inside the
+    same call for queries whose nearest reference is several cells away.
+    Results equal the scan kernel's everywhere."""
     batch, query_count, _ = query.shape
     ref_count = ref.shape[1]
     query = query.contiguous()
@@ -126,20 +122,6 @@ def _nearest_grid(query: Tensor, ref: Tensor) -> tuple[Tensor, Tensor]:
     _native.call("pointops_nearest3_grid", query.data_ptr(), ref.data_ptr(), distances.data_ptr(),
                  indices.data_ptr(), workspace.data_ptr(), batch, query_count, ref_count,
                  _native.stream(query.device))
-    rows, cols = (indices < 0).nonzero(as_tuple=True)  # batch-major, as the flat layout needs
-    if len(rows):
-        counts = torch.bincount(rows, minlength=batch)
-        ptr_y = torch.zeros(batch + 1, dtype=torch.int64, device=query.device)
-        ptr_y[1:] = counts.cumsum(0)
-        ptr_x = torch.arange(batch + 1, dtype=torch.int64, device=query.device) * ref_count
-        packed = query[rows, cols].contiguous()
-        hit = flat.knn_indices(ref.reshape(-1, 3), packed, ptr_x, ptr_y, 1)[:, 0]
-        delta = packed - ref.reshape(-1, 3)[hit]
-        squared = delta[:, 0] * delta[:, 0]
-        squared = squared + delta[:, 1] * delta[:, 1]
-        squared = squared + delta[:, 2] * delta[:, 2]
-        distances[rows, cols] = squared
-        indices[rows, cols] = hit - rows * ref_count
     return distances, indices
 
 
