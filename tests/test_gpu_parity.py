@@ -773,7 +773,7 @@ def test_chamfer_c5_forward_backward_reduced(cuda_device):
 
 def _nearest_grid_case(case: str) -> tuple[torch.Tensor, torch.Tensor]:
     g = torch.Generator().manual_seed({"c5_xy": 0, "c5_yx": 0, "cube": 1, "duplicates": 2,
-                                       "shell_far_queries": 3}[case])
+                                       "shell_far_queries": 3, "overflow": 4}[case])
     if case in ("c5_xy", "c5_yx"):
         y1, y2 = bench.make_c5()
         return (y1, y2) if case == "c5_xy" else (y2, y1)
@@ -783,12 +783,19 @@ def _nearest_grid_case(case: str) -> tuple[torch.Tensor, torch.Tensor]:
         base = torch.randn(500, 3, generator=g)
         pick = torch.randint(0, 500, (3, 12000), generator=g)
         return base[pick[:, :5000]].contiguous(), base[pick[:, 3000:]].contiguous()
+    if case == "overflow":  # squared distances of the far half overflow to +inf
+        q = torch.rand(2, 5000, 3, generator=g)
+        r = torch.rand(2, 9000, 3, generator=g)
+        q[:, ::2] *= 3e19
+        r[:, 1::3] *= -3e19
+        return q, r
     ref = torch.randn(2, 10000, 3, generator=g)
     ref = ref / ref.norm(dim=-1, keepdim=True)  # a shell: the interior is empty
     return torch.rand(2, 6000, 3, generator=g) * 0.2 - 0.1, ref
 
 
-@pytest.mark.parametrize("case", ["c5_xy", "c5_yx", "cube", "duplicates", "shell_far_queries"])
+@pytest.mark.parametrize("case", ["c5_xy", "c5_yx", "cube", "duplicates", "shell_far_queries",
+                                  "overflow"])
 def test_chamfer_nearest_grid_matches_scan(cuda_device, case):
     """The grid search (and the scan inside it for far queries: every query
     of the shell case is far) returns the linear scan's squared distances
