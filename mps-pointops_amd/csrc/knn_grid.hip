@@ -581,7 +581,8 @@ __device__ __forceinline__ float box_bound(const GridParams& P, float h, const f
 template <int S>
 __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
-    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K, int nearest) {
+    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K, int nearest,
+    int* __restrict__ miss_count, int* __restrict__ miss_list) {
     constexpr int KMAX = 4 * S;
     __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
     const int lane = lane_id();
@@ -728,13 +729,9 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
         }
     }
     if (full && nearest) {
-        // Nearest mode leaves such waves to a linear-scan kernel: index -1.
-        if (!active) return;
-        const int64_t row = (b * M + m) * K;
-        if (qi == 3) {
-            out_dist[row] = INFINITY;
-            out_idx[row] = -1;
-        }
+        // Nearest mode appends such queries to its cloud's list for the
+        // linear-scan pass (nearest_fill_kernel), which writes their results.
+        if (active && qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
         return;
     }
     if (full) {
@@ -943,15 +940,23 @@ __global__ __launch_bounds__(kWave) void cloud_bounds_final_kernel(const float* 
     }
 }
 
-// Nearest mode's second pass: one workgroup per 64 consecutive queries of
-// the grid's query order (cell-sorted, so the queries the search left are
-// clustered and most workgroups return at once); 8 waves split the
-// references, lane = query, references read with uniform loads, and the
-// best (squared distance, smallest index) per wave is combined in LDS.
+// Nearest mode's second pass over each cloud's list of the queries the grid
+// search left (their nearest reference is several cells away): one
+// workgroup per 64 listed queries, lane = query, 8 waves splitting the
+// references (batches of 8 read with wide scalar loads, the next batch
+// requested before the current one is scanned), the best (squared distance,
+// smallest index) per wave combined in LDS.  Workgroups past the list's end
+// return at once.
 constexpr int kFillThreads = 512;
 
+__global__ void grid_zero_kernel(int* __restrict__ p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 __global__ __launch_bounds__(kFillThreads) void nearest_fill_kernel(
-    const float* __restrict__ query, const float* __restrict__ ref, GridLayout L,
+    const float* __restrict__ query, const float* __restrict__ ref,
+    const int* __restrict__ miss_count, const int* __restrict__ miss_list,
     float* __restrict__ dist2, int64_t* __restrict__ idx, int64_t M, int64_t N) {
     constexpr int NWF = kFillThreads / kWave;
     __shared__ int keys[NWF][kWave];
@@ -960,26 +965,23 @@ __global__ __launch_bounds__(kFillThreads) void nearest_fill_kernel(
     const int wave = uniform(threadIdx.x / kWave);
     const int64_t groups = (M + kWave - 1) / kWave;
     const int64_t b = blockIdx.x / groups;
-    const int64_t pos = (blockIdx.x - b * groups) * kWave + lane;
-    const bool active = pos < M;
-    const int64_t row = b * M + (active ? L.q_order[b * M + pos] : 0);
-    const bool need = active && idx[row] < 0;
-    if (ballot(need) == 0) return;  // the same in every wave: before any barrier
+    const int64_t first = (blockIdx.x - b * groups) * kWave;
+    const int64_t count = miss_count[b];
+    if (first >= count) return;  // uniform over the workgroup, before any barrier
+    const bool active = first + lane < count;
+    const int64_t row = b * M + miss_list[b * M + (active ? first + lane : first)];
     const float qx = query[3 * row], qy = query[3 * row + 1], qz = query[3 * row + 2];
     const float* rp = ref + 3 * b * N;
     const int64_t per = (N + NWF - 1) / NWF;
     const int64_t lo = min(N, wave * per), hi = min(N, lo + per);
     int best = 0x7FFFFFFF, bi = 0;
-    // Batches of 8 references (24 consecutive floats, wide scalar loads),
-    // the next batch loaded before the current one is scanned; ascending
-    // order keeps the first minimum.
     const int64_t hi8 = lo + ((hi - lo) & ~int64_t(7));
     float cur[24], nxt[24];
     if (lo < hi8) {
 #pragma unroll
         for (int t = 0; t < 24; ++t) cur[t] = rp[3 * lo + t];
     }
-    for (int64_t j = lo; j < hi8; j += 8) {
+    for (int64_t j = lo; j < hi8; j += 8) {  // ascending: the first minimum is kept
         if (j + 8 < hi8) {
 #pragma unroll
             for (int t = 0; t < 24; ++t) nxt[t] = rp[3 * (j + 8) + t];
@@ -1005,7 +1007,7 @@ __global__ __launch_bounds__(kFillThreads) void nearest_fill_kernel(
     keys[wave][lane] = best;
     ids[wave][lane] = bi;
     __syncthreads();
-    if (wave != 0 || !need) return;
+    if (wave != 0 || !active) return;
     int k = keys[0][lane], i = ids[0][lane];
 #pragma unroll
     for (int w = 1; w < NWF; ++w) {
@@ -1080,13 +1082,13 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
-        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
     else if (K <= 8)
-        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
     else if (K <= 16)
-        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
     else
-        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
     return hipGetLastError();
 }
 
@@ -1103,11 +1105,18 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     grid_build(query, ref, L, B, M, N, 1, 0.f, stream);
+    // The build's scan totals and query ranks are dead once the queries are
+    // placed: they hold the per-cloud counts and lists of far queries.
+    int* miss_count = L.tile_sum;  // B * 2 * tiles >= B ints
+    int* miss_list = L.q_rank;     // B * M ints
+    hipLaunchKernelGGL(grid_zero_kernel, dim3(static_cast<uint32_t>((B + 255) / 256)), dim3(256), 0,
+                       stream, miss_count, B);
     hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, dim3(kGridSearchWaves * kWave), 0, stream, query,
-                       L, dist2, idx, B, M, N, 1, 1);
+                       L, dist2, idx, B, M, N, 1, 1, miss_count, miss_list);
     const int64_t fill_blocks = B * ((M + kWave - 1) / kWave);
     hipLaunchKernelGGL(nearest_fill_kernel, dim3(static_cast<uint32_t>(fill_blocks)),
-                       dim3(kFillThreads), 0, stream, query, ref, L, dist2, idx, M, N);
+                       dim3(kFillThreads), 0, stream, query, ref, miss_count, miss_list, dist2, idx,
+                       M, N);
     return hipGetLastError();
 }
 
