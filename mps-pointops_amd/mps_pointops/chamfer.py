@@ -102,9 +102,12 @@ def _grid_eligible(query: Tensor, ref: Tensor, norm: int, full: bool) -> bool:
     that are large enough for its build to pay."""
     batch, query_count, dimension = query.shape
     ref_count = ref.shape[1]
+    limit = (1 << 31) - 64  # the entry point's index range and launch size
     return (full and norm == 2 and dimension == 3 and query.dtype == torch.float32
             and ref_count >= _GRID_MIN_REFS and query_count >= _GRID_MIN_QUERIES
-            and batch <= 65535 and batch * query_count * ref_count >= _GRID_MIN_PAIRS)
+            and batch <= 65535 and batch * query_count * ref_count >= _GRID_MIN_PAIRS
+            and query_count < limit and ref_count < limit
+            and batch * ((query_count + 63) // 64) < limit)
 
 
 def _nearest_grid(query: Tensor, ref: Tensor) -> tuple[Tensor, Tensor]:
