@@ -360,3 +360,25 @@ def test_pointcept_offsets_and_optional_registration():
         for name in names:
             sys.modules.pop(name, None)
         sys.modules.update(saved)
+
+
+def test_chamfer_grid_eligibility():
+    """The grid nearest search serves squared-L2 3-D float32 clouds without
+    lengths, large enough for its build to pay; everything else keeps the
+    linear scan (shape checks only, no device work)."""
+    from mps_pointops import chamfer
+
+    def clouds(b, m, n, d=3, dtype=torch.float32):
+        return torch.zeros(1, 1, d, dtype=dtype).expand(b, m, d), \
+            torch.zeros(1, 1, d, dtype=dtype).expand(b, n, d)
+
+    q, r = clouds(32, 8192, 8192)
+    assert chamfer._grid_eligible(q, r, 2, True)
+    assert not chamfer._grid_eligible(q, r, 2, False)  # lengths given
+    assert not chamfer._grid_eligible(q, r, 1, True)  # L1
+    assert not chamfer._grid_eligible(*clouds(32, 8192, 8192, dtype=torch.float64), 2, True)
+    assert not chamfer._grid_eligible(*clouds(32, 8192, 8192, d=4), 2, True)
+    assert not chamfer._grid_eligible(*clouds(32, 8192, 4096), 2, True)  # too few references
+    assert not chamfer._grid_eligible(*clouds(32, 2048, 8192), 2, True)  # too few queries
+    assert not chamfer._grid_eligible(*clouds(1, 4096, 8192), 2, True)  # too few pairs
+    assert not chamfer._grid_eligible(*clouds(70000, 4096, 8192), 2, True)  # batch limit
