@@ -118,6 +118,11 @@ MI355X_HBM_BYTES_PER_S = 8.0e12
 # issue ceiling is 256 CUs x 64 lanes x 2.4 GHz = 39.3 T op/s; the JSON line
 # reports against the published figure.
 MI355X_FP32_PEAK = 157.3e12
+# Issue ceiling of unfused, unpacked FP32 VALU code: one op per lane per clock,
+# 64 lanes per CU (4 SIMDs x 16), 256 CUs at 2.4 GHz.
+MI355X_CUS = 256
+MI355X_VALU_ISSUE_PER_CU = 64 * 2.4e9
+MI355X_VALU_ISSUE = MI355X_CUS * MI355X_VALU_ISSUE_PER_CU
 FPS_OPS_PER_POINT_STEP = 9  # 3 sub, 3 mul, 2 add (unfused), 1 min
 PAIR_OPS = 8                # 3-D squared distance: 3 sub, 3 mul, 2 add
 
@@ -177,34 +182,45 @@ def cpu_info() -> dict:
     return {"model": model, "os_cpu_count": os.cpu_count()}
 
 
-def cpu_baseline(xyz_cpu: torch.Tensor, clouds: int) -> dict:
+def cpu_baseline(xyz_cpu: torch.Tensor, clouds: int, warmup: int = 3, repeats: int = 20) -> dict:
     """The reference's CPU algorithms (PyTorch-CPU port) on the first
-    `clouds` clouds of the config-2 input, scaled to points/s."""
+    `clouds` clouds of the config-2 input, scaled to points/s: `warmup`
+    untimed passes, then the median of `repeats` timed passes (each op's
+    median reported beside the total)."""
+    import statistics
+
     sys.path.insert(0, str(ROOT))
     from oracle import torch_port
 
     torch.set_num_threads(os.cpu_count() or 1)
     x = xyz_cpu[:clouds].contiguous()
-    t0 = time.perf_counter()
-    idx = torch_port.furthest_point_sample(x, C2_NPOINT)
-    t1 = time.perf_counter()
-    centres = x.gather(1, idx[..., None].expand(-1, -1, 3))
-    t_ball = 0.0
-    for radius, k in C2_RADII:
+
+    def one_pass() -> tuple[float, float, float]:
+        t0 = time.perf_counter()
+        idx = torch_port.furthest_point_sample(x, C2_NPOINT)
+        t_fps = time.perf_counter() - t0
+        centres = x.gather(1, idx[..., None].expand(-1, -1, 3))
         s = time.perf_counter()
-        torch_port.ball_query(centres, x, radius, k)
-        t_ball += time.perf_counter() - s
-    s = time.perf_counter()
-    torch_port.knn(centres, x, C2_KNN_K)
-    t_knn = time.perf_counter() - s
-    total = (t1 - t0) + t_ball + t_knn
+        for radius, k in C2_RADII:
+            torch_port.ball_query(centres, x, radius, k)
+        t_ball = time.perf_counter() - s
+        s = time.perf_counter()
+        torch_port.knn(centres, x, C2_KNN_K)
+        return t_fps, t_ball, time.perf_counter() - s
+
+    for _ in range(warmup):
+        one_pass()
+    passes = [one_pass() for _ in range(max(1, repeats))]
+    total = statistics.median(sum(p) for p in passes)
+    t_fps, t_ball, t_knn = (statistics.median(p[i] for p in passes) for i in range(3))
     return {
         "value": clouds * x.shape[1] / total,
         "unit": "points/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"{clouds} of 32 clouds of config 2 (N=4096): FPS 1024 + 3 ball queries + kNN16, "
-                  f"PyTorch-CPU port of reference.py; fps {t1 - t0:.3f}s ball {t_ball:.3f}s "
+                  f"PyTorch-CPU port of reference.py, median of {len(passes)} passes after "
+                  f"{warmup} warmups; medians fps {t_fps:.3f}s ball {t_ball:.3f}s "
                   f"knn {t_knn:.3f}s",
         "cpu": cpu_info(),
     }
@@ -332,6 +348,8 @@ def run(args) -> dict:
 
     kernel = fps_kernel_name(N)
     achieved = fps_ops / t_fps
+    # One workgroup per cloud: B of the 256 CUs run the FPS kernel.
+    occupied = min(B, MI355X_CUS) * MI355X_VALU_ISSUE_PER_CU
     traffic = profiled_traffic(kernel, "c2")
     result = {
         "metric": "points/sec for FPS+ball_query+kNN at B=32,N=4096; % of HBM/FP32 roofline",
@@ -356,17 +374,22 @@ def run(args) -> dict:
         "propagation_not_in_value": propagation,
         "roofline": {
             "kernel": kernel,
-            "bound": "mfma",
+            "bound": "valu",
             "compute": "fp32 VALU, unfused (no MFMA, no FMA, no packed fp32)",
             "achieved": achieved / 1e12,
             "peak": MI355X_FP32_PEAK / 1e12,
             "unit": "TFLOP/s",
             "frac": achieved / MI355X_FP32_PEAK,
             "traffic": traffic,
+            "valu_issue_peak": MI355X_VALU_ISSUE / 1e12,
+            "frac_valu_issue": achieved / MI355X_VALU_ISSUE,
+            "occupied_cus": min(B, MI355X_CUS),
+            "frac_occupied_cu_issue": achieved / occupied,
         },
     }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(xyz_cpu, args.cpu_clouds)
+        result["cpu_baseline"] = cpu_baseline(xyz_cpu, args.cpu_clouds, args.cpu_warmup,
+                                              args.cpu_repeats)
     return result
 
 
@@ -482,6 +505,8 @@ def main() -> None:
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--cpu-clouds", type=int, default=32)
+    parser.add_argument("--cpu-warmup", type=int, default=3)
+    parser.add_argument("--cpu-repeats", type=int, default=20)
     parser.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                         help="workload; the headline metric (and the default) is c2")
     parser.add_argument("--probe", action="store_true",

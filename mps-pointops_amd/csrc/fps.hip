@@ -7,28 +7,27 @@
 // set (their running distance is -inf); if no point can be picked the step
 // takes index 0.
 //
+//
 // Kernels:
-//   fps_regs_kernel<P,T>    one workgroup per cloud, the cloud's points and
-//                           running distances in VGPRs (P consecutive points
-//                           per thread, so lane order is index order and the
-//                           argmax needs no index reduction); each wave
-//                           publishes (distance, index, xyz) of its best
-//                           point, so one barrier and one LDS read per step
-//                           (double-buffered slots) broadcast the centroid.
-//   fps_global_kernel<T>    one workgroup per cloud for clouds larger than
-//                           LDS: points re-read from L2, running distances in
-//                           a caller-provided scratch array.
-//   fps_lazy_kernel<P,T>    one cloud over up to 128 CUs (cooperative launch):
-//                           each workgroup keeps its chunk in VGPRs; an
-//                           exchange publishes every wave's best candidate
-//                           and a bound, after which every workgroup takes
-//                           exact steps over the candidates alone until the
-//                           bound could be reached (the product kernel).
-//   fps_large_kernel<P,T>   the same launch with a full exchange per step:
-//                           each workgroup publishes a tagged (distance,
-//                           index, xyz) record per step in 8 copies; every
-//                           workgroup polls all records of one copy.
+//   fps_lazy_regs_kernel<P,T>  one workgroup per cloud, the cloud's points
+//                              and running distances in VGPRs (P consecutive
+//                              points per thread, so lane order is index
+//                              order); exact steps over 64 published
+//                              candidates between exchanges (clouds of up to
+//                              8192 points, batched or ragged).
+//   fps_global_kernel<T>       one workgroup per cloud for larger clouds of a
+//                              batch: points re-read from L2, running
+//                              distances in a caller-provided scratch array.
+//   fps_lazy_kernel<P,T>       one cloud over up to 256 CUs (cooperative
+//                              launch): each workgroup keeps its chunk in
+//                              VGPRs; an exchange publishes every wave's best
+//                              candidate and a bound, after which every
+//                              workgroup takes exact steps over the
+//                              candidates alone until the bound could be
+//                              reached.
 #include <hip/hip_cooperative_groups.h>
+
+#include <cstdlib>
 
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
@@ -103,116 +102,6 @@ struct alignas(16) WaveBest {
     float x, y, z;
     int pad[3];
 };
-
-// Thread t holds points t*P .. t*P+P-1, so point order = (wave, lane, slot)
-// order: the first maximum found by slot, then lane, then wave, is the one
-// with the smallest index.  Running distances are never NaN, so their bit
-// patterns order like the floats as signed ints (-inf below +0).  Each wave
-// publishes its candidate with the coordinates, so one barrier and one LDS
-// round trip per step give every wave the next centroid.
-template <int P, int T>
-__global__ __launch_bounds__(T) void fps_regs_kernel(const float* __restrict__ xyz,
-                                                     const int64_t* __restrict__ ptr,
-                                                     const int64_t* __restrict__ out_ptr,
-                                                     const int64_t* __restrict__ starts,
-                                                     int64_t* __restrict__ out, int64_t N,
-                                                     int64_t npoint, int64_t start, int skip) {
-    constexpr int NW = T / kWave;
-    static_assert(NW <= 8, "the block argmax reduces 8 lanes");
-    __shared__ WaveBest slots[2][8];
-
-    const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
-    if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
-    const float* p = xyz + 3 * seg.in_lo;
-    int64_t* o = out + seg.out_lo;
-    const int n = static_cast<int>(seg.n);
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
-
-    // One spare element each: with 9+ elements a uniform dynamic index
-    // (px[os] below) compiles to one indexed move instead of a select chain.
-    float px[P + 1], py[P + 1], pz[P + 1];
-    float md[P];  // running distances
-#pragma unroll
-    for (int k = 0; k <= P; ++k) {
-        px[k] = py[k] = pz[k] = 0.f;
-    }
-    int far = static_cast<int>(seg.start);
-    float cx = 0.f, cy = 0.f, cz = 0.f;  // coordinates of point `far`
-    if (n > 0) {
-        // Loads are clamped into the cloud (not skipped) so that all P of
-        // them are in flight at once; padding slots are masked below.
-#pragma unroll
-        for (int k = 0; k < P; ++k) {
-            const int jj = min(tid * P + k, n - 1);
-            px[k] = p[3 * jj];
-            py[k] = p[3 * jj + 1];
-            pz[k] = p[3 * jj + 2];
-        }
-        const int f = min(max(far, 0), n - 1);
-        cx = p[3 * f];
-        cy = p[3 * f + 1];
-        cz = p[3 * f + 2];
-    }
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-        const int j = tid * P + k;
-        const bool valid = j < n;
-        px[k] = valid ? px[k] : 0.f;
-        py[k] = valid ? py[k] : 0.f;
-        pz[k] = valid ? pz[k] : 0.f;
-        md[k] = !valid ? -INFINITY
-                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
-    }
-
-    // Lanes of the block argmax: lane l reads wave (l % 8)'s candidate;
-    // waves past NW read a copy of wave 0's, which never wins a tie.
-    const int peer = (lane % 8) < NW ? lane % 8 : 0;
-    for (int64_t step = 0; step < seg.cnt; ++step) {
-        if (tid == 0) o[step] = seg.base + far;
-        if (step + 1 == seg.cnt) break;
-        int v[P];
-#pragma unroll
-        for (int k = 0; k < P; ++k) {
-            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
-            v[k] = f2i(md[k]);
-        }
-        int lm = v[0];
-#pragma unroll
-        for (int k = 1; k < P; ++k) lm = max(lm, v[k]);
-        int ls = P - 1;  // first slot of this lane holding lm
-#pragma unroll
-        for (int k = P - 2; k >= 0; --k) ls = v[k] == lm ? k : ls;
-        // First lane holding the wave's largest value: the smallest index.
-        const int wv = wave_max_i32_l63(lm);
-        const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
-        const int os = readlane(ls, wl);
-        WaveBest* buf = slots[step & 1];
-        const float wx = i2f(readlane(f2i(px[os]), wl));
-        const float wy = i2f(readlane(f2i(py[os]), wl));
-        const float wz = i2f(readlane(f2i(pz[os]), wl));
-        if (lane == 0) {
-            WaveBest c;
-            c.key = wv;
-            c.index = (wave * kWave + wl) * P + os;
-            c.x = wx;
-            c.y = wy;
-            c.z = wz;
-            c.pad[0] = c.pad[1] = c.pad[2] = 0;
-            buf[wave] = c;
-        }
-        __syncthreads();
-        const WaveBest e = buf[peer];
-        const int bv = group8_max_i32(e.key);
-        const int bw = static_cast<int>(__builtin_ctzll(ballot(e.key == bv)));
-        far = readlane(e.index, bw);
-        cx = i2f(readlane(f2i(e.x), bw));
-        cy = i2f(readlane(f2i(e.y), bw));
-        cz = i2f(readlane(f2i(e.z), bw));
-    }
-}
-
 // fps_lazy_regs_kernel<P,T>: the batched kernel with the exchange of
 // fps_lazy_kernel inside one workgroup.  At an exchange every wave extracts
 // its KC = 64 / NW best points (largest running distance, then smallest
@@ -398,280 +287,40 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
         far = (win == INT_MAX) ? 0 : win;
     }
 }
-
 // ------------------------------------------------------------ large cloud
 //
-// fps_large_kernel<P,T>: one cloud over G <= kLargeMaxGrid co-resident
-// workgroups (at most one per CU), cooperative launch.  Workgroup g owns points
-// [g*chunk, g*chunk+chunk); thread t holds P consecutive ones in VGPRs, so the
-// local argmax is the register tree + DPP max of fps_regs_kernel, and the wave
-// holding the winner reads its coordinates from its own registers (uniform
-// register index).  Per step the local winner is published as a record of
-// four 64-bit words written with agent-scope atomic stores, each carrying the
-// step tag so that a reader can tell a complete record of this step from a
-// stale one two steps back (records are double-buffered by step parity and
-// stored as structure of arrays):
-//   w0 = vkey << 32 | tag << 21 | (~idx & 0x1FFFFF)
-//   w1 = x_bits << 32 | tag,  w2 = y_bits << 32 | tag,  w3 = z_bits << 32 | tag
-// vkey = 0 when the workgroup has no candidate, else float bits + 1 (running
-// distances are >= +0 for candidates, so the bits order like the values and
-// the largest (vkey, ~idx) is the largest value with the smallest index).
-// Every record is written to 8 copies (lane r of the winning wave writes copy
-// r) and workgroup g reads copy g % 8, which spreads the polls of all
-// workgroups over 8 sets of cache lines (one shared copy measured 4.8 us per
-// step, 8 copies 3.6 us).  Thread t of every workgroup polls the key word of
-// record t until it carries the step's tag, then reads the coordinate words;
-// the wave reduces the keys with two 32-bit DPP maxima, and a barrier
-// combines the waves.  (With an exchange per step, 128 workgroups for a
-// 1M-point cloud polled less and measured faster than 256; the lazy kernel
-// below exchanges rarely and uses one workgroup per CU.)  Polls are bounded: after kSpinLimit attempts (or when another
-// workgroup has given up) the kernel raises a status word and every workgroup
-// returns, so no launch can hang.
+// Constants of the persistent large-cloud kernel below: one cloud over G <=
+// kLargeMaxGrid co-resident workgroups (at most one per CU), cooperative
+// launch; workgroup g owns points [g*chunk, g*chunk+chunk), thread t holds P
+// consecutive ones in VGPRs.  Indices travel in 21 bits of the records.
+// Polls are bounded: after kSpinLimit attempts (or when another workgroup
+// has given up) the kernel raises the status word, workgroup 0 writes -1 to
+// every output slot it has not written, and every workgroup returns, so no
+// launch can hang and no slot is left unwritten.
 constexpr int kLargeIdxBits = 21;
 constexpr uint32_t kLargeIdxMask = (1u << kLargeIdxBits) - 1u;
 constexpr int64_t kLargeMaxN = int64_t(1) << kLargeIdxBits;
 constexpr uint32_t kSpinLimit = 1u << 22;
-#ifndef POINTOPS_FPS_LARGE_THREADS
-#define POINTOPS_FPS_LARGE_THREADS 256
-#endif
-#ifndef POINTOPS_FPS_LARGE_GRID
-#define POINTOPS_FPS_LARGE_GRID 256  // one workgroup per CU (the lazy exchange is rare)
-#endif
-constexpr int kLargeThreads = POINTOPS_FPS_LARGE_THREADS;
+constexpr int kLargeThreads = 256;
 constexpr int kLargeMaxGrid = kLargeThreads;  // one polled record per thread (SoA stride)
 // Every record is written to kLargeReplicas copies, and workgroup g polls copy
 // g % kLargeReplicas, so each copy's cache lines are read by 1/kLargeReplicas
-// of the pollers instead of all of them.
-#ifndef POINTOPS_FPS_LARGE_REPLICAS
-#define POINTOPS_FPS_LARGE_REPLICAS 8
-#endif
-constexpr int kLargeReplicas = POINTOPS_FPS_LARGE_REPLICAS;
-constexpr int64_t kLargeCopyWords = 4 * kLargeMaxGrid;  // one copy: 4 words per record
-constexpr int kLargePreferredGrid = POINTOPS_FPS_LARGE_GRID;
-static_assert(kLargePreferredGrid <= kLargeMaxGrid, "one polled record per thread");
+// of the pollers instead of all of them (one shared copy measured 4.8 us per
+// exchange-free step on 1M points, 8 copies 3.6 us).
+constexpr int kLargeReplicas = 8;
 
-__device__ __forceinline__ uint32_t step_tag(int64_t step) {
-    return (static_cast<uint32_t>(step >> 1) & 0x3FFu) | 0x400u;  // never 0
-}
-
-struct RecordPoll {
-    uint64_t w0, w1, w2, w3;
-};
-
-// One agent-scope read of the four words of a record (structure of arrays).
-__device__ __forceinline__ RecordPoll poll_record(const uint64_t* q) {
-    RecordPoll r;
-    r.w0 = __hip_atomic_load(q + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.w1 = __hip_atomic_load(q + 1 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.w2 = __hip_atomic_load(q + 2 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    r.w3 = __hip_atomic_load(q + 3 * kLargeMaxGrid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return r;
-}
-
-__device__ __forceinline__ bool record_ready(const RecordPoll& r, uint32_t tag) {
-    return ((r.w0 >> kLargeIdxBits) & 0x7FFu) == tag && static_cast<uint32_t>(r.w1) == tag &&
-           static_cast<uint32_t>(r.w2) == tag && static_cast<uint32_t>(r.w3) == tag;
-}
-
-__device__ __forceinline__ void take_record(const RecordPoll& r, uint32_t& khi, uint32_t& klo,
-                                            int& rx, int& ry, int& rz) {
-    khi = static_cast<uint32_t>(r.w0 >> 32);
-    klo = static_cast<uint32_t>(r.w0) & kLargeIdxMask;
-    rx = static_cast<int>(r.w1 >> 32);
-    ry = static_cast<int>(r.w2 >> 32);
-    rz = static_cast<int>(r.w3 >> 32);
-}
-
-// True when this poller must stop: too many polls, or another workgroup has
-// already given up (checked every 64 polls).  Raises the shared status word.
-__device__ __forceinline__ bool poll_give_up(uint32_t* status, uint32_t spins) {
-    if (spins >= kSpinLimit ||
+// True when this poller must stop: `limit` polls done, or another workgroup
+// has already given up (checked every 64 polls).  Raises the shared status
+// word.  Checked before each read, so limit 0 gives up at the first poll
+// (the host-forced failure path of the tests; every wave still exits).
+__device__ __forceinline__ bool poll_give_up(uint32_t* status, uint32_t spins, uint32_t limit) {
+    if (spins >= limit ||
         ((spins & 63u) == 63u &&
          __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT))) {
         __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         return true;
     }
     return false;
-}
-
-template <int P, int T>
-__global__ __launch_bounds__(T) void fps_large_kernel(
-    const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
-    uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk) {
-    constexpr int NW = T / kWave;
-    constexpr int kNegInf = static_cast<int>(0xFF800000u);
-    __shared__ int2 slots[2][NW];
-    __shared__ uint64_t red_key[2][NW];
-    __shared__ float4 red_xyz[2][NW];
-    __shared__ int abort_flag;
-
-    const int G = gridDim.x;
-    const int g = blockIdx.x;
-    const int tid = threadIdx.x;
-    const int wave = tid / kWave;
-    const int lane = tid % kWave;
-    const int lo = g * chunk;
-    const int n = max(0, min(chunk, N - lo));
-    const float* p = xyz + 3 * static_cast<int64_t>(lo);
-
-    float px[P], py[P], pz[P], md[P];
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-        px[k] = py[k] = pz[k] = 0.f;
-    }
-    if (n > 0) {
-        // Loads are clamped into the cloud (not skipped) so that all P of
-        // them are in flight at once; padding slots are masked below.
-#pragma unroll
-        for (int k = 0; k < P; ++k) {
-            const int jj = min(tid * P + k, n - 1);
-            px[k] = p[3 * jj];
-            py[k] = p[3 * jj + 1];
-            pz[k] = p[3 * jj + 2];
-        }
-    }
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-        const int j = tid * P + k;
-        const bool valid = j < n;
-        px[k] = valid ? px[k] : 0.f;
-        py[k] = valid ? py[k] : 0.f;
-        pz[k] = valid ? pz[k] : 0.f;
-        md[k] = !valid ? -INFINITY
-                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
-    }
-    if (tid == 0) abort_flag = 0;
-    __syncthreads();
-
-    int far = start;
-    float cx = xyz[3 * static_cast<int64_t>(far)];
-    float cy = xyz[3 * static_cast<int64_t>(far) + 1];
-    float cz = xyz[3 * static_cast<int64_t>(far) + 2];
-    for (int64_t step = 0; step < npoint; ++step) {
-        if (g == 0 && tid == 0) out[step] = far;
-        if (step + 1 == npoint) break;
-        const int par = static_cast<int>(step & 1);
-
-        // Local argmax of this workgroup's chunk: first maximum in index order.
-        int v[P];
-#pragma unroll
-        for (int k = 0; k < P; ++k) {
-            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
-            v[k] = f2i(md[k]);
-        }
-        int lm = v[0];
-#pragma unroll
-        for (int k = 1; k < P; ++k) lm = max(lm, v[k]);
-        int ls = P - 1;  // first slot of this lane holding lm
-#pragma unroll
-        for (int k = P - 2; k >= 0; --k) ls = v[k] == lm ? k : ls;
-        const int wv = wave_max_i32_l63(lm);
-        const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
-        const int wi = (wave * kWave + wl) * P + readlane(ls, wl);
-        if (lane == 0) slots[par][wave] = make_int2(wv, wi);
-        __syncthreads();
-
-        // The wave holding the workgroup's winner publishes its record: the
-        // winner's coordinates are read from that lane's registers.
-        const uint32_t tag = step_tag(step);
-        uint64_t* base = records + static_cast<int64_t>(par) * kLargeReplicas * kLargeCopyWords;
-        int bv = slots[par][0].x, bi = slots[par][0].y;
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            if (slots[par][w].x > bv) {
-                bv = slots[par][w].x;
-                bi = slots[par][w].y;
-            }
-        }
-        bv = uniform(bv);
-        bi = uniform(bi);
-        if (wave == bi / (kWave * P)) {
-            // Uniform register index (GPR indexing mode), then the lane.
-            const int ol = uniform((bi / P) % kWave), os = uniform(bi % P);
-            float ox = i2f(readlane(f2i(px[os]), ol));
-            float oy = i2f(readlane(f2i(py[os]), ol));
-            float oz = i2f(readlane(f2i(pz[os]), ol));
-            if (lane < kLargeReplicas) {  // lane r writes copy r
-                uint32_t vkey = 0;
-                if (bv != kNegInf) vkey = static_cast<uint32_t>(bv) + 1u;
-                else ox = oy = oz = 0.f;
-                const uint32_t gidx = static_cast<uint32_t>(lo + bi);
-                uint64_t* rec = base + lane * kLargeCopyWords + g;
-                __hip_atomic_store(rec + 1 * kLargeMaxGrid,
-                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(ox))) << 32) | tag,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(rec + 2 * kLargeMaxGrid,
-                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(oy))) << 32) | tag,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(rec + 3 * kLargeMaxGrid,
-                                   (static_cast<uint64_t>(static_cast<uint32_t>(f2i(oz))) << 32) | tag,
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                __hip_atomic_store(rec + 0,
-                                   (static_cast<uint64_t>(vkey) << 32) |
-                                       (static_cast<uint64_t>(tag) << kLargeIdxBits) |
-                                       (~gidx & kLargeIdxMask),
-                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            }
-        }
-
-        // Thread t polls record t until all four words carry this step's tag.
-        uint32_t khi = 0, klo = 0;
-        int rx = 0, ry = 0, rz = 0;
-        if (tid < G) {
-            const uint64_t* q = base + (g % kLargeReplicas) * kLargeCopyWords + tid;
-            for (uint32_t spins = 0;; ++spins) {
-                // The key word is stored last: poll it alone, then read the
-                // coordinate words once it carries this step's tag.
-                const uint64_t w0 = __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                if (((w0 >> kLargeIdxBits) & 0x7FFu) == tag) {
-                    const RecordPoll r = poll_record(q);
-                    if (record_ready(r, tag)) {
-                        take_record(r, khi, klo, rx, ry, rz);
-                        break;
-                    }
-                }
-                if (poll_give_up(status, spins)) {
-                    abort_flag = 1;
-                    break;
-                }
-            }
-        }
-        // Wave maximum of (khi, klo): khi <= 0x7F800001 and klo < 2^21, so both
-        // compare correctly as signed ints.
-        const int hmax = wave_max_i32_l63(static_cast<int>(khi));
-        const int lmax = wave_max_i32_l63(static_cast<int>(khi) == hmax ? static_cast<int>(klo) : -1);
-        const int rl = static_cast<int>(__builtin_ctzll(
-            ballot(static_cast<int>(khi) == hmax && static_cast<int>(klo) == lmax)));
-        if (lane == 0) {
-            red_key[par][wave] = (static_cast<uint64_t>(static_cast<uint32_t>(hmax)) << 32) |
-                                 static_cast<uint32_t>(lmax);
-            red_xyz[par][wave] = make_float4(i2f(readlane(rx, rl)), i2f(readlane(ry, rl)),
-                                             i2f(readlane(rz, rl)), 0.f);
-        }
-        __syncthreads();
-        if (abort_flag) return;  // uniform: written before the barrier
-        int bw = 0;
-        uint64_t best = red_key[par][0];
-#pragma unroll
-        for (int w = 1; w < NW; ++w) {
-            if (red_key[par][w] > best) {
-                best = red_key[par][w];
-                bw = w;
-            }
-        }
-        if ((best >> 32) == 0) {  // nothing can be picked: index 0, like the reference
-            far = 0;
-            cx = xyz[0];
-            cy = xyz[1];
-            cz = xyz[2];
-        } else {
-            far = static_cast<int>(~static_cast<uint32_t>(best) & kLargeIdxMask);
-            const float4 c = red_xyz[par][bw];
-            cx = c.x;
-            cy = c.y;
-            cz = c.z;
-        }
-    }
 }
 
 // fps_lazy_kernel<P,T>: the large-cloud FPS with an exchange every few steps
@@ -689,15 +338,16 @@ __global__ __launch_bounds__(T) void fps_large_kernel(
 // exchange are applied to every workgroup's own points at the next exchange
 // (a running minimum does not depend on the order).  Records carry a tag per
 // 64-bit word and are double-buffered by exchange parity, in kLargeReplicas
-// copies as in fps_large_kernel; polls are bounded.
-#ifndef POINTOPS_FPS_LAZY_CAND
-#define POINTOPS_FPS_LAZY_CAND 1
-#endif
-#ifndef POINTOPS_FPS_LAZY_PENDING
-#define POINTOPS_FPS_LAZY_PENDING 64
-#endif
-constexpr int kLazyCand = POINTOPS_FPS_LAZY_CAND;           // candidates per wave
-constexpr int kLazyMaxPending = POINTOPS_FPS_LAZY_PENDING;  // steps between exchanges at most
+// copies; polls are bounded.  Record of wave w (structure of arrays, stride
+// kLazyMaxWaves words):
+//   word 4c   = key << 32 | tag << 21 | idx   (candidate c: running distance
+//                                              bits, 21-bit global index)
+//   word 4c+1 = x_bits << 32 | tag,  4c+2 = y_bits << 32 | tag,
+//   word 4c+3 = z_bits << 32 | tag,  last = bound_bits << 32 | tag
+// The tag (exchange number mod 1024, bit 10 set) lets a reader tell a record
+// of this exchange from one two exchanges back.
+constexpr int kLazyCand = 1;          // candidates per wave
+constexpr int kLazyMaxPending = 64;   // steps between exchanges at most
 constexpr int kLazyRecWords = 4 * kLazyCand + 1;
 constexpr int kLazyMaxWaves = kLargeMaxGrid * (kLargeThreads / kWave);
 constexpr int64_t kLazyCopyWords = static_cast<int64_t>(kLazyRecWords) * kLazyMaxWaves;
@@ -705,7 +355,8 @@ constexpr int64_t kLazyCopyWords = static_cast<int64_t>(kLazyRecWords) * kLazyMa
 template <int P, int T>
 __global__ __launch_bounds__(T) void fps_lazy_kernel(
     const float* __restrict__ xyz, int64_t* __restrict__ out, uint64_t* __restrict__ records,
-    uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk) {
+    uint32_t* __restrict__ status, int N, int64_t npoint, int start, int skip, int chunk,
+    uint32_t spin_limit) {
     constexpr int NW = T / kWave;
     static_assert(NW <= 8 && P <= 32, "shape");
     constexpr int RPT = kLazyMaxWaves / T;  // records read per thread at most
@@ -833,6 +484,10 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
             if (rw >= waves) continue;
             const uint64_t* q = copy + rw;
             for (uint32_t spins = 0;; ++spins) {
+                if (poll_give_up(status, spins, spin_limit)) {
+                    abort_flag = 1;
+                    break;
+                }
                 const uint64_t wb = __hip_atomic_load(q + static_cast<int64_t>(kLazyRecWords - 1) * kLazyMaxWaves,
                                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 if (static_cast<uint32_t>(wb) == tag) {
@@ -860,16 +515,18 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
                         break;
                     }
                 }
-                if (poll_give_up(status, spins)) {
-                    abort_flag = 1;
-                    break;
-                }
             }
         }
         bmax = wave_max_i32_l63(bmax);
         if (lane == 0) wave_bound[wave] = bmax;
         __syncthreads();
-        if (abort_flag) return;  // uniform: written before the barrier
+        if (abort_flag) {  // uniform: written before the barrier
+            // Slots from `step` on were never written: mark them -1 so a
+            // caller that misses the status word still sees the failure.
+            if (g == 0)
+                for (int64_t s = step + tid; s < npoint; s += T) out[s] = -1;
+            return;
+        }
         int bound = wave_bound[0];
 #pragma unroll
         for (int w = 1; w < NW; ++w) bound = max(bound, wave_bound[w]);
@@ -936,17 +593,9 @@ template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream) {
-#ifndef POINTOPS_FPS_LAZY_REGS
-#define POINTOPS_FPS_LAZY_REGS 1
-#endif
-    if (POINTOPS_FPS_LAZY_REGS)
-        hipLaunchKernelGGL((fps_lazy_regs_kernel<P, kRegsThreads>),
-                           dim3(static_cast<uint32_t>(blocks)), dim3(kRegsThreads), 0, stream, xyz,
-                           ptr, out_ptr, starts, out, N, npoint, start, skip);
-    else
-        hipLaunchKernelGGL((fps_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
-                           dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                           start, skip);
+    hipLaunchKernelGGL((fps_lazy_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
+                       dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                       start, skip);
     return hipGetLastError();
 }
 
@@ -971,23 +620,28 @@ hipError_t launch_fps(const float* xyz, const int64_t* ptr, const int64_t* out_p
     return hipGetLastError();
 }
 
-#ifndef POINTOPS_FPS_LAZY
-#define POINTOPS_FPS_LAZY 1
-#endif
-
 // The persistent large-cloud kernel for P points per thread.
 template <int P>
 const void* large_kernel() {
-    if (POINTOPS_FPS_LAZY) return reinterpret_cast<const void*>(&fps_lazy_kernel<P, kLargeThreads>);
-    return reinterpret_cast<const void*>(&fps_large_kernel<P, kLargeThreads>);
+    return reinterpret_cast<const void*>(&fps_lazy_kernel<P, kLargeThreads>);
+}
+
+// Polls of one record before the large-cloud kernel gives up: kSpinLimit,
+// or POINTOPS_FPS_SPIN_LIMIT when set (a diagnostic: 0 makes every call
+// give up at its first exchange, which is how the failure path is tested).
+uint32_t spin_limit() {
+    const char* env = std::getenv("POINTOPS_FPS_SPIN_LIMIT");
+    if (env == nullptr || *env == '\0') return kSpinLimit;
+    return static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
 }
 
 template <int P>
 hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint32_t* status,
                         int N, int64_t npoint, int start, int skip, int chunk, int grid,
                         hipStream_t stream) {
+    uint32_t limit = spin_limit();
     void* args[] = {(void*)&xyz, (void*)&out, (void*)&records, (void*)&status, (void*)&N,
-                    (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk};
+                    (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk, (void*)&limit};
     return hipLaunchCooperativeKernel(large_kernel<P>(), dim3(grid), dim3(kLargeThreads), args, 0,
                                       stream);
 }
@@ -1048,7 +702,7 @@ size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
     // status word (padded to 256 B) + 2 parities x copies x records
-    const int64_t words = 2 * kLargeReplicas * (POINTOPS_FPS_LAZY ? kLazyCopyWords : kLargeCopyWords);
+    const int64_t words = 2 * kLargeReplicas * kLazyCopyWords;
     return 256 + static_cast<size_t>(words) * sizeof(uint64_t);
 }
 
@@ -1070,9 +724,6 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
     const int s32 = static_cast<int>(start_idx);
     const int skip = skip_near_origin ? 1 : 0;
     const int choices[] = {1, 2, 4, 8, 16, 32};
-    // Prefer at most kLargePreferredGrid workgroups; clouds too large for that
-    // use up to one workgroup per CU (and per polling thread).
-    for (int limit : {kLargePreferredGrid, kLargeMaxGrid})
     for (int P : choices) {
         int cap = 0;
         switch (P) {
@@ -1083,7 +734,7 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
             case 16: cap = large_capacity<16>(device); break;
             default: cap = large_capacity<32>(device); break;
         }
-        cap = min(cap, limit);
+        cap = min(cap, kLargeMaxGrid);
         const int64_t per_block = static_cast<int64_t>(P) * kLargeThreads;
         const int64_t need = (N + per_block - 1) / per_block;
         if (cap <= 0 || need > cap) continue;

@@ -33,6 +33,23 @@ _KNN_GRID_MIN_N = 32_768
 _KNN_GRID_MIN_PAIRS = 1 << 26
 
 
+def _check_large_status(workspace: Tensor) -> None:
+    """Raise if the persistent kernel gave up waiting for a workgroup's record
+    (its first 4 workspace bytes are then non-zero and the unwritten output
+    slots hold -1).  Reading the word synchronises with the stream once per
+    large-cloud call; the reference's host loop has no such sync, but a
+    partial result must not pass silently.  Skipped during graph capture,
+    where the -1 slots remain the signal."""
+    if torch.cuda.is_current_stream_capturing():
+        return
+    if int(workspace[:4].view(torch.int32).item()) != 0:
+        raise RuntimeError(
+            "furthest_point_sample: the large-cloud kernel stopped waiting for a workgroup "
+            "(its cooperative launch did not run all workgroups together); the output is "
+            "incomplete"
+        )
+
+
 def furthest_point_sample(
     xyz: Tensor,
     npoint: int,
@@ -88,6 +105,7 @@ def furthest_point_sample(
         workspace = torch.zeros(size, dtype=torch.uint8, device=xyz.device)
         _native.call("pointops_fps_large", xyz.data_ptr(), out.data_ptr(), workspace.data_ptr(),
                      N, npoint, start_idx, int(skip_near_origin), stream)
+        _check_large_status(workspace)
         return out
     size = _native.size_query("pointops_fps_dense_scratch_bytes", B, N)
     scratch = torch.empty(size, dtype=torch.uint8, device=xyz.device) if size else None

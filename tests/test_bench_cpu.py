@@ -25,7 +25,8 @@ def test_cpu_baseline_fields():
     """One cloud of config 2 through the CPU port: points/s, the cores used,
     the kind of baseline and what was sampled."""
     xyz = bench.make_c2(B=1)
-    out = bench.cpu_baseline(xyz, 1)
+    out = bench.cpu_baseline(xyz, 1, warmup=1, repeats=3)
     assert out["value"] > 0 and out["unit"] == "points/s"
     assert out["kind"] == "port" and out["cores"] >= 1
     assert out["sample"].startswith("1 of 32 clouds of config 2")
+    assert "median of 3 passes after 1 warmups" in out["sample"]

@@ -243,6 +243,48 @@ def test_fps_large_matches_oracle(cuda_device, n):
         np.testing.assert_array_equal(host(got), want)
 
 
+def _fps_large_abi(xyz: torch.Tensor, npoint: int, start: int):
+    """pointops_fps_large through the C ABI: (indices, status word)."""
+    from mps_pointops import _native
+
+    x = xyz.cuda().contiguous()
+    N = x.shape[1]
+    out = torch.full((npoint,), -777, dtype=torch.long, device="cuda")
+    size = _native.size_query("pointops_fps_large_workspace_bytes", N, npoint)
+    ws = torch.zeros(size, dtype=torch.uint8, device="cuda")
+    _native.call("pointops_fps_large", x.data_ptr(), out.data_ptr(), ws.data_ptr(), N, npoint,
+                 start, 0, _native.stream(x.device))
+    torch.cuda.synchronize()
+    return host(out), int(ws[:4].view(torch.int32).item())
+
+
+def test_fps_large_status_word_clear_after_success(cuda_device):
+    xyz = rand_cloud(1, 200_000, 5)
+    got, status = _fps_large_abi(xyz, 500, 3)
+    assert status == 0
+    np.testing.assert_array_equal(got, O.fps(xyz, 500, 3)[0])
+
+
+def test_fps_large_forced_give_up_is_reported(cuda_device, monkeypatch):
+    """A poll limit of 0 (set from the host) makes every workgroup give up at
+    its first exchange: the status word is raised, the first sample (written
+    before any exchange) stays, every other slot is -1, and the public call
+    raises.  Every wave exits normally."""
+    import mps_pointops as mp
+
+    xyz = rand_cloud(1, 100_000, 6)
+    monkeypatch.setenv("POINTOPS_FPS_SPIN_LIMIT", "0")
+    got, status = _fps_large_abi(xyz, 300, 11)
+    assert status == 1
+    assert got[0] == 11 and (got[1:] == -1).all()
+    with pytest.raises(RuntimeError, match="incomplete"):
+        mp.furthest_point_sample(xyz.cuda(), 300, 11, strategy="multigroup")
+    monkeypatch.delenv("POINTOPS_FPS_SPIN_LIMIT")
+    got, status = _fps_large_abi(xyz, 300, 11)
+    assert status == 0
+    np.testing.assert_array_equal(got, O.fps(xyz, 300, 11)[0])
+
+
 @pytest.mark.parametrize("n,distinct", [(4096, 300), (1000, 40), (8192, 3000)])
 def test_fps_dense_repeated_points(cuda_device, n, distinct):
     """Clouds built from few distinct points (equal distances everywhere, and
