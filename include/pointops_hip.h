@@ -56,6 +56,20 @@ hipError_t pointops_fps_large(const float *xyz, int64_t *out, void *workspace, i
                               int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
                               hipStream_t stream);
 
+/* pointops_fps_large without a workspace argument: allocates nothing.  No
+ * counterpart in the reference; it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  The workspace is a 640 KiB array in the library's
+ * device memory, one per GPU, held until the process ends; each call clears
+ * it with a fill kernel on `stream` before the launch.  Limits as
+ * pointops_fps_large: 1 <= N <= 2^21 points, else hipErrorInvalidValue
+ * before anything is enqueued.  Calls that overlap on one GPU (several
+ * streams or host threads) share the array and race: serialise them.  A give-up
+ * of the kernel shows as -1 in every output slot it did not write. */
+hipError_t pointops_fps_large_noalloc(const float *xyz, int64_t *out, int64_t N, int64_t npoint,
+                                      int64_t start_idx, int32_t skip_near_origin,
+                                      hipStream_t stream);
+
 /* Ragged FPS (torch_cluster layout).  Replaces _flat_fps_mps.py:86-95
  * (kernels/fps_flat.metal:7-96).  Cloud b is x[ptr[b]:ptr[b+1]]; its samples
  * go to out[out_ptr[b]:out_ptr[b+1]] as global indices starting from the

@@ -28,6 +28,7 @@
 #include <hip/hip_cooperative_groups.h>
 
 #include <cstdlib>
+#include <mutex>
 
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
@@ -646,6 +647,43 @@ hipError_t launch_large(const float* xyz, int64_t* out, uint64_t* records, uint3
                                       stream);
 }
 
+// Status word (padded to 256 B) + 2 parities x copies x records.
+constexpr size_t kLargeWorkspaceBytes =
+    256 + static_cast<size_t>(2 * kLargeReplicas * kLazyCopyWords) * sizeof(uint64_t);
+
+// Workspace of pointops_fps_large_noalloc (640 KiB per GPU, held until the
+// process ends).  Host code never passes this name to a kernel: it is only a
+// host-side handle, whose device address (one per GPU) comes from
+// hipGetSymbolAddress in scratch_address().
+static __device__ __align__(256) unsigned char scratch[kLargeWorkspaceBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex scratch_mutex;
+void* scratch_ptr[kMaxDevices];  // device address of `scratch` on each GPU, once looked up
+
+// Device address of `scratch` on `device` (the current device), looked up on
+// the first call for that device.
+hipError_t scratch_address(int device, void** out) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(scratch_mutex);
+    if (scratch_ptr[device] == nullptr) {
+        void* p = nullptr;
+        const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (err != hipSuccess) return err;
+        if (p == nullptr) return hipErrorInvalidSymbol;
+        scratch_ptr[device] = p;
+    }
+    *out = scratch_ptr[device];
+    return hipSuccess;
+}
+
+// Zero-fill of n 64-bit words (a kernel, so the clear is an ordinary launch
+// on the caller's stream rather than a memset node).
+__global__ __launch_bounds__(256) void zero_words_kernel(uint64_t* __restrict__ p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
 template <int P>
 int large_capacity(int device) {
     int per_cu = 0;
@@ -701,28 +739,37 @@ hipError_t pointops_fps_flat(const float* x, const int64_t* ptr, const int64_t* 
 size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
-    // status word (padded to 256 B) + 2 parities x copies x records
-    const int64_t words = 2 * kLargeReplicas * kLazyCopyWords;
-    return 256 + static_cast<size_t>(words) * sizeof(uint64_t);
+    return kLargeWorkspaceBytes;
 }
 
-hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,
-                              int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
-                              hipStream_t stream) {
+}  // extern "C"
+
+namespace pointops {
+namespace {
+
+// Checks shared by both large-cloud entry points; hipSuccess with *run = false
+// when there is nothing to do.
+hipError_t check_large(const float* xyz, const int64_t* out, int64_t N, int64_t npoint,
+                       int64_t start_idx, bool* run) {
+    *run = false;
     if (N < 0 || npoint < 0) return hipErrorInvalidValue;
     if (npoint == 0) return hipSuccess;
     if (N == 0 || N > kLargeMaxN || start_idx < 0 || start_idx >= N) return hipErrorInvalidValue;
-    if (xyz == nullptr || out == nullptr || workspace == nullptr) return hipErrorInvalidValue;
-    int device = 0;
-    hipError_t err = hipGetDevice(&device);
-    if (err != hipSuccess) return err;
-    // Smallest P (points per thread) whose grid fits one workgroup per CU
-    // and one polled record per thread.
+    if (xyz == nullptr || out == nullptr) return hipErrorInvalidValue;
+    *run = true;
+    return hipSuccess;
+}
+
+// Launches the persistent kernel with the smallest P (points per thread)
+// whose grid fits one workgroup per CU and one polled record per thread.
+// `workspace` holds kLargeWorkspaceBytes bytes, zero-filled.
+hipError_t launch_large_any(const float* xyz, int64_t* out, void* workspace, int64_t N,
+                            int64_t npoint, int64_t start_idx, int skip, int device,
+                            hipStream_t stream) {
     auto* status = static_cast<uint32_t*>(workspace);
     auto* records = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + 256);
     const int n32 = static_cast<int>(N);
     const int s32 = static_cast<int>(start_idx);
-    const int skip = skip_near_origin ? 1 : 0;
     const int choices[] = {1, 2, 4, 8, 16, 32};
     for (int P : choices) {
         int cap = 0;
@@ -750,6 +797,47 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
         }
     }
     return hipErrorInvalidValue;
+}
+
+}  // namespace
+}  // namespace pointops
+
+extern "C" {
+
+hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, int64_t N,
+                              int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
+                              hipStream_t stream) {
+    bool run = false;
+    hipError_t err = check_large(xyz, out, N, npoint, start_idx, &run);
+    if (err != hipSuccess || !run) return err;
+    if (workspace == nullptr) return hipErrorInvalidValue;
+    int device = 0;
+    err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    return launch_large_any(xyz, out, workspace, N, npoint, start_idx, skip_near_origin ? 1 : 0,
+                            device, stream);
+}
+
+hipError_t pointops_fps_large_noalloc(const float* xyz, int64_t* out, int64_t N, int64_t npoint,
+                                      int64_t start_idx, int32_t skip_near_origin,
+                                      hipStream_t stream) {
+    bool run = false;
+    hipError_t err = check_large(xyz, out, N, npoint, start_idx, &run);
+    if (err != hipSuccess || !run) return err;
+    int device = 0;
+    err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    void* ws = nullptr;
+    err = scratch_address(device, &ws);
+    if (err != hipSuccess) return err;
+    // The previous call's records and status stay in the array: clear them.
+    constexpr int64_t words = static_cast<int64_t>(kLargeWorkspaceBytes / sizeof(uint64_t));
+    hipLaunchKernelGGL(zero_words_kernel, dim3(static_cast<uint32_t>((words + 255) / 256)),
+                       dim3(256), 0, stream, static_cast<uint64_t*>(ws), words);
+    err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return launch_large_any(xyz, out, ws, N, npoint, start_idx, skip_near_origin ? 1 : 0, device,
+                            stream);
 }
 
 }  // extern "C"

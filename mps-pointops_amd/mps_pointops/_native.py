@@ -31,6 +31,7 @@ _size = ctypes.c_size_t
 _SIGNATURES: dict[str, list] = {
     "pointops_fps_dense": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "pointops_fps_large": [_vp, _vp, _vp, _i64, _i64, _i64, _i32, _vp],
+    "pointops_fps_large_noalloc": [_vp, _vp, _i64, _i64, _i64, _i32, _vp],
     "pointops_fps_flat": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_knn3": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_knn3_grid": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
