@@ -1,5 +1,6 @@
-"""Optional stand-ins for ``pointnet2_ops``, ``knn_cuda`` and ``torch_cluster``
-(the neighbourhood-search part of /root/reference/mps_pointops/compat.py).
+"""Stand-ins for ``pointnet2_ops``, ``knn_cuda`` and ``torch_cluster`` on the
+native ROCm kernels (the neighbourhood-search surface of
+/root/reference/mps_pointops/compat.py).
 
 Call ``install()`` before importing code that uses them::
 
@@ -10,15 +11,16 @@ Call ``install()`` before importing code that uses them::
     from knn_cuda import KNN
     from torch_cluster import fps, knn, radius
 
-A name that is already importable (for example the real CUDA package) is left
-alone unless ``force=True``.  Covered: ``furthest_point_sample``,
-``gather_operation``, ``grouping_operation`` and ``ball_query`` from
-``pointnet2_utils``, plus its ``QueryAndGroup`` and ``GroupAll`` modules on
-the fused grouping kernel (not in the reference's stand-in); ``KNN`` from ``knn_cuda``; ``fps``, ``knn``, ``radius``,
-``knn_graph`` and ``radius_graph`` from ``torch_cluster``.  The reference's
-graph/cluster extras (graclus, grid, random_walk, nearest) are outside this
-package's scope; ``install(pointcept=True)`` adds the Pointcept v1.2.1 PTv1
-``pointops`` module (``mps_pointops.pointcept``).
+A top-level name that is already importable (for example the real CUDA
+package) is left alone unless ``force=True``.  Served: ``pointnet2_utils``'s
+``furthest_point_sample``, ``gather_operation``, ``grouping_operation`` and
+``ball_query`` (plus ``QueryAndGroup`` / ``GroupAll`` on the fused grouping
+kernel, which the reference's stand-in lacks); ``knn_cuda.KNN``;
+``torch_cluster``'s ``fps``, ``knn``, ``radius``, ``knn_graph`` and
+``radius_graph``.  The reference's graph/cluster extras (graclus, grid,
+random_walk, nearest) are outside this package.  ``install(pointcept=True)``
+adds the Pointcept v1.2.1 PTv1 ``pointops`` module
+(``mps_pointops.pointcept``).
 """
 
 from __future__ import annotations
@@ -36,15 +38,15 @@ from . import pointcept as pointcept_ops
 
 
 def furthest_point_sample(xyz: Tensor, npoint: int) -> Tensor:
-    """Like ``pointnet2_ops.pointnet2_utils.furthest_point_sample``: (B, N, 3)
-    float32 -> (B, npoint) int32, start at 0, points with x^2+y^2+z^2 <= 1e-3
-    never picked (compat.py:53-59)."""
+    """pointnet2_ops' FPS: (B, N, 3) float32 -> (B, npoint) int32, starting
+    at index 0, never picking points with x^2+y^2+z^2 <= 1e-3
+    (compat.py:53-59)."""
     return ops.furthest_point_sample(xyz, npoint, skip_near_origin=True).int()
 
 
 def gather_operation(features: Tensor, idx: Tensor) -> Tensor:
     """(B, C, N), (B, npoint) -> (B, C, npoint) (compat.py:62-65): the
-    native gather on the GPU, with its scatter-add gradient."""
+    native gather, with its deterministic scatter-add gradient."""
     return group.group_points(features, idx)
 
 
@@ -59,91 +61,85 @@ def grouping_operation(features: Tensor, idx: Tensor) -> Tensor:
 
 
 def ball_query(radius: float, nsample: int, xyz: Tensor, new_xyz: Tensor) -> Tensor:
-    """(B, N, 3), (B, npoint, 3) -> (B, npoint, nsample) int32 (compat.py:76-85).
-
-    The first ``nsample`` points in input order with squared distance
-    ``< radius**2``; empty slots repeat the first neighbour and a query with no
-    neighbour gets all zeros, as in pointnet2_ops.
-    """
+    """pointnet2_ops' ball query (compat.py:76-85): (B, N, 3), (B, npoint, 3)
+    -> (B, npoint, nsample) int32 holding the first ``nsample`` points in
+    input order with squared distance ``< radius**2``; unused slots repeat
+    the query's first neighbour, and a query without neighbours is all 0."""
     _, idx = ops.ball_query(new_xyz, xyz, radius, nsample)
-    first = idx[..., :1].clamp(min=0)
-    return torch.where(idx >= 0, idx, first).int()
+    if idx.shape[-1] == 0:
+        return idx.int()
+    first = idx.narrow(-1, 0, 1).clamp_min(0)
+    return idx.where(idx >= 0, first).int()
 
 
 class KNN(torch.nn.Module):
-    """Like ``knn_cuda.KNN`` (compat.py:91-112).
-
-    With ``transpose_mode=True`` ``ref`` is (B, N, D), ``query`` (B, M, D) and
-    the outputs (B, M, k); otherwise (B, D, N), (B, D, M) and (B, k, M).
-    ``dist`` is Euclidean.  No gradients flow.
-    """
+    """``knn_cuda.KNN(k, transpose_mode)`` (compat.py:91-112): Euclidean
+    distances and indices of the ``k`` nearest references, no gradient.
+    ``transpose_mode=True`` takes (B, N, D) / (B, M, D) and returns (B, M, k);
+    otherwise the layouts are (B, D, N) / (B, D, M) -> (B, k, M)."""
 
     def __init__(self, k: int, transpose_mode: bool = False):
         super().__init__()
         self.k = k
         self.transpose_mode = transpose_mode
 
+    def _rows(self, t: Tensor) -> Tensor:
+        """The point-major (B, count, D) view of an input or (B, count, k)
+        result in this module's layout."""
+        return t if self.transpose_mode else t.transpose(1, 2)
+
+    @torch.no_grad()
     def forward(self, ref: Tensor, query: Tensor) -> tuple[Tensor, Tensor]:
-        if not self.transpose_mode:
-            ref, query = ref.transpose(1, 2), query.transpose(1, 2)
-        with torch.no_grad():
-            dist, idx = ops.knn(query.float(), ref.float(), self.k)
-        if not self.transpose_mode:
-            dist, idx = dist.transpose(1, 2), idx.transpose(1, 2)
-        return dist, idx
+        dist, idx = ops.knn(self._rows(query).float(), self._rows(ref).float(), self.k)
+        return self._rows(dist), self._rows(idx)
 
 
-def _module(name: str, **attrs) -> types.ModuleType:
+def _stand_in(name: str, package: bool = False, **attrs) -> types.ModuleType:
+    """A module object for sys.modules with a spec, so importlib treats it
+    like an imported module (a package when ``package``)."""
     module = types.ModuleType(name)
+    module.__spec__ = ModuleSpec(name, loader=None, is_package=package)
+    if package:
+        module.__path__ = []
     module.__dict__.update(attrs)
-    module.__spec__ = ModuleSpec(name, loader=None, is_package="__path__" in attrs)
     return module
 
 
-def install(force: bool = False, *, pointcept: bool = False) -> list[str]:
-    """Register the stand-ins in ``sys.modules`` (compat.py:125-172); with
-    ``pointcept=True`` also the Pointcept v1.2.1 PTv1 ``pointops`` surface."""
-    pointnet2_utils = _module(
-        "pointnet2_ops.pointnet2_utils",
-        furthest_point_sample=furthest_point_sample,
-        gather_operation=gather_operation,
-        grouping_operation=grouping_operation,
-        ball_query=ball_query,
-        QueryAndGroup=group.QueryAndGroup,
-        GroupAll=group.GroupAll,
-    )
-    packages = {
-        "pointnet2_ops": {
-            "pointnet2_ops": _module("pointnet2_ops", pointnet2_utils=pointnet2_utils, __path__=[]),
-            "pointnet2_ops.pointnet2_utils": pointnet2_utils,
-        },
-        "knn_cuda": {"knn_cuda": _module("knn_cuda", KNN=KNN)},
-        "torch_cluster": {
-            "torch_cluster": _module(
-                "torch_cluster",
-                fps=flat.fps,
-                knn=flat.knn,
-                radius=flat.radius,
-                knn_graph=flat.knn_graph,
-                radius_graph=flat.radius_graph,
-            )
-        },
+def _stand_ins(pointcept: bool) -> dict[str, list[types.ModuleType]]:
+    """Top-level name -> the modules registered for it."""
+    utils = _stand_in("pointnet2_ops.pointnet2_utils",
+                      furthest_point_sample=furthest_point_sample,
+                      gather_operation=gather_operation,
+                      grouping_operation=grouping_operation,
+                      ball_query=ball_query,
+                      QueryAndGroup=group.QueryAndGroup,
+                      GroupAll=group.GroupAll)
+    table = {
+        "pointnet2_ops": [_stand_in("pointnet2_ops", package=True, pointnet2_utils=utils), utils],
+        "knn_cuda": [_stand_in("knn_cuda", KNN=KNN)],
+        "torch_cluster": [_stand_in("torch_cluster", fps=flat.fps, knn=flat.knn,
+                                    radius=flat.radius, knn_graph=flat.knn_graph,
+                                    radius_graph=flat.radius_graph)],
     }
     if pointcept:
-        packages["pointops"] = {
-            "pointops": _module(
-                "pointops",
-                farthest_point_sampling=pointcept_ops.farthest_point_sampling,
-                knn_query=pointcept_ops.knn_query,
-                grouping=pointcept_ops.grouping,
-                knn_query_and_group=pointcept_ops.knn_query_and_group,
-                interpolation=pointcept_ops.interpolation,
-            ),
-        }
-    installed = []
-    for top, modules in packages.items():
-        if not force and (top in sys.modules or importlib.util.find_spec(top) is not None):
+        table["pointops"] = [_stand_in("pointops", **{
+            name: getattr(pointcept_ops, name) for name in pointcept_ops.__all__})]
+    return table
+
+
+def _importable(name: str) -> bool:
+    return name in sys.modules or importlib.util.find_spec(name) is not None
+
+
+def install(force: bool = False, *, pointcept: bool = False) -> list[str]:
+    """Register the stand-ins in ``sys.modules`` (compat.py:125-172) and
+    return the module names registered; ``pointcept=True`` adds the
+    Pointcept v1.2.1 PTv1 ``pointops`` surface."""
+    registered: list[str] = []
+    for top, modules in _stand_ins(pointcept).items():
+        if not force and _importable(top):
             continue
-        sys.modules.update(modules)
-        installed.extend(modules)
-    return installed
+        for module in modules:
+            sys.modules[module.__name__] = module
+            registered.append(module.__name__)
+    return registered

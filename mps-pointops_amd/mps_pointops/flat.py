@@ -1,16 +1,24 @@
-"""Flat point-cloud operators with the ``torch_cluster`` index convention, on
-ROCm (signatures and validation of /root/reference/mps_pointops/flat.py and
-its native helpers _flat_fps_mps.py / _flat_search_mps.py).
+"""Flat point-cloud operators in the ``torch_cluster`` convention, on ROCm.
 
-``x`` holds reference points, ``y`` query points, batch vectors are sorted,
-and results use global indices into the flat tensors.  FPS and radius use 3-D
-coordinates; kNN accepts feature vectors of any positive dimension.
+Signatures, defaults, exception types and messages are those of
+/root/reference/mps_pointops/flat.py (with _flat_fps_mps.py and
+_flat_search_mps.py); the code is this package's own.  ``x`` holds the
+reference points and ``y`` the queries as flat ``(N, D)`` rows, clouds are
+contiguous runs described by a sorted batch vector (or, for ``fps``, an
+offset array ``ptr``), and every result uses global row indices.  FPS and
+radius take 3-D coordinates; kNN takes any positive dimension.
+
+All clouds of a call go to one ragged launch (``pointops_fps_flat``,
+``pointops_knn_flat``, ``pointops_radius_flat_*``).  A batch vector is
+validated with one device-to-host read (first id, sortedness and last id
+together); its offsets are a bincount prefix sum on the device.
 """
 
 from __future__ import annotations
 
 import math
 import struct
+from dataclasses import dataclass
 from typing import Sequence
 
 import torch
@@ -19,128 +27,161 @@ from torch import Tensor
 from . import _native
 from ._ball_query import _checked_radius_and_k
 
-_KNN_MAX_K = 256
-_UINT_MAX = (1 << 32) - 1
+_KNN_MAX_K = 256          # widest neighbour list of the native kNN (ops.py:30)
+_MAX_CLOUD = (1 << 32) - 1  # longest cloud a ragged FPS launch indexes
+_FLOWS = ("source_to_target", "target_to_source")
 
 
-def _points(value: Tensor, name: str) -> None:
+# ----------------------------------------------------------- validation
+
+
+def _rows(value, name: str, *, coordinates: bool) -> None:
+    """A floating-point (N, 3) coordinate table or (N, D >= 1) feature table."""
     if not isinstance(value, Tensor):
         raise TypeError(f"{name} must be a torch.Tensor")
-    if value.ndim != 2 or value.shape[1] != 3:
+    if coordinates and (value.ndim != 2 or value.shape[1] != 3):
         raise ValueError(f"{name} must have shape (N, 3), got {tuple(value.shape)}")
-    if not value.is_floating_point():
-        raise TypeError(f"{name} must have a floating-point dtype")
-
-
-def _features(value: Tensor, name: str) -> None:
-    if not isinstance(value, Tensor):
-        raise TypeError(f"{name} must be a torch.Tensor")
-    if value.ndim != 2 or value.shape[1] < 1:
+    if not coordinates and (value.ndim != 2 or value.shape[1] < 1):
         raise ValueError(f"{name} must have shape (N, D) with D >= 1, got {tuple(value.shape)}")
     if not value.is_floating_point():
         raise TypeError(f"{name} must have a floating-point dtype")
 
 
-def _batch_size(value: int | None) -> int | None:
-    if value is None:
-        return None
+def _count_arg(value, name: str) -> int:
+    """A non-negative Python int (bool excluded)."""
     if isinstance(value, bool) or not isinstance(value, int) or value < 0:
-        raise ValueError("batch_size must be a non-negative integer")
+        raise ValueError(f"{name} must be a non-negative integer")
     return value
 
 
-def _check_batch(batch: Tensor | None, count: int, device: torch.device, name: str) -> int:
-    """flat.py:49-64 (host syncs for sortedness and the largest id)."""
+def _optional_batch_size(value) -> int | None:
+    return None if value is None else _count_arg(value, "batch_size")
+
+
+def _clouds_in(batch, rows: int, device: torch.device, name: str) -> int:
+    """Number of clouds a sorted batch vector names (its last id + 1; 0 for
+    no vector or no rows).  One device-to-host read covers the checks."""
     if batch is None:
         return 0
     if not isinstance(batch, Tensor):
         raise TypeError(f"{name} must be a torch.Tensor or None")
-    if batch.ndim != 1 or batch.numel() != count:
-        raise ValueError(f"{name} must have shape ({count},)")
+    if batch.ndim != 1 or batch.numel() != rows:
+        raise ValueError(f"{name} must have shape ({rows},)")
     if batch.device != device:
         raise ValueError(f"{name} must be on {device}")
     if batch.dtype not in (torch.int32, torch.int64):
         raise TypeError(f"{name} must have an integer dtype (int32 or int64)")
-    if not count:
+    if rows == 0:
         return 0
-    if bool((batch[0] < 0).item()) or bool((batch[1:] < batch[:-1]).any().item()):
+    ids = batch.long()
+    first, descending, last = torch.stack(
+        (ids[0], (ids[1:] < ids[:-1]).any().long(), ids[-1])).tolist()
+    if first < 0 or descending:
         raise ValueError(f"{name} must be sorted with non-negative batch IDs")
-    return int(batch[-1].item()) + 1
+    return last + 1
 
 
-def _ptr_from_batch(batch: Tensor | None, count: int, device: torch.device, size: int) -> Tensor:
+def _offsets(batch: Tensor | None, rows: int, device: torch.device, clouds: int) -> Tensor:
+    """(clouds + 1,) int64 row offsets of a sorted batch vector; without a
+    vector all rows form one cloud (even when there are none)."""
     if batch is None:
-        return torch.tensor([0, count], dtype=torch.long, device=device)
-    if size == 0:
-        return torch.zeros(1, dtype=torch.long, device=device)
-    boundaries = torch.arange(size + 1, dtype=torch.long, device=device)
-    return torch.searchsorted(batch.contiguous().long(), boundaries).long()
+        return torch.tensor([0, rows], dtype=torch.long, device=device)
+    offsets = torch.zeros(clouds + 1, dtype=torch.long, device=device)
+    if clouds:
+        offsets[1:] = torch.bincount(batch.long(), minlength=clouds).cumsum(0)
+    return offsets
 
 
-def _pair_ptrs(x, y, batch_x, batch_y, batch_size):
-    explicit_size = _batch_size(batch_size)
-    size_x = _check_batch(batch_x, len(x), x.device, "batch_x")
-    size_y = _check_batch(batch_y, len(y), y.device, "batch_y")
-    size = max(1, size_x, size_y, explicit_size or 0)
-    if size > 1 and (batch_x is None or batch_y is None):
-        raise ValueError("batch_x and batch_y are both required for multiple batches")
-    if explicit_size is not None and explicit_size < max(size_x, size_y):
-        raise ValueError("batch_size is smaller than the largest batch ID")
-    return (
-        _ptr_from_batch(batch_x, len(x), x.device, size),
-        _ptr_from_batch(batch_y, len(y), y.device, size),
-    )
+@dataclass(frozen=True)
+class _SearchLayout:
+    """Offsets of the reference and query clouds of one search call."""
+
+    x_offsets: Tensor
+    y_offsets: Tensor
+
+    @property
+    def clouds(self) -> int:
+        return len(self.x_offsets) - 1
+
+    @classmethod
+    def of(cls, x: Tensor, y: Tensor, batch_x, batch_y, batch_size) -> "_SearchLayout":
+        requested = _optional_batch_size(batch_size)
+        in_x = _clouds_in(batch_x, len(x), x.device, "batch_x")
+        in_y = _clouds_in(batch_y, len(y), y.device, "batch_y")
+        clouds = max(1, in_x, in_y, requested or 0)
+        if clouds > 1 and (batch_x is None or batch_y is None):
+            raise ValueError("batch_x and batch_y are both required for multiple batches")
+        if requested is not None and requested < max(in_x, in_y):
+            raise ValueError("batch_size is smaller than the largest batch ID")
+        return cls(_offsets(batch_x, len(x), x.device, clouds),
+                   _offsets(batch_y, len(y), y.device, clouds))
 
 
-def _fps_ptr(x, batch, batch_size, ptr) -> Tensor:
-    """flat.py:100-122."""
-    if ptr is not None:
-        if isinstance(ptr, Tensor):
-            if ptr.device != x.device or ptr.dtype not in (torch.int32, torch.int64):
-                raise ValueError("ptr must be an integer tensor on the same device as x")
-            result = ptr.long()
-        elif isinstance(ptr, (list, tuple)):
-            result = torch.tensor(ptr, dtype=torch.long, device=x.device)
-        else:
-            raise TypeError("ptr must be a tensor, a sequence of integers, or None")
-        if result.ndim != 1 or len(result) == 0:
-            raise ValueError("ptr must be a non-empty one-dimensional offset array")
-        if int(result[0].item()) != 0 or int(result[-1].item()) != len(x):
-            raise ValueError("ptr must start at 0 and end at len(x)")
-        if bool((result[1:] < result[:-1]).any().item()):
-            raise ValueError("ptr must be non-decreasing")
-        return result.contiguous()
-    explicit_size = _batch_size(batch_size)
-    inferred_size = _check_batch(batch, len(x), x.device, "batch")
-    if explicit_size is not None and explicit_size < inferred_size:
-        raise ValueError("batch_size is smaller than the largest batch ID")
-    size = (max(1, inferred_size, explicit_size or 0) if batch is None
-            else max(inferred_size, explicit_size or 0))
-    return _ptr_from_batch(batch, len(x), x.device, size)
+def _fps_offsets(x: Tensor, batch, batch_size, ptr) -> Tensor:
+    """Cloud offsets for fps: an explicit ``ptr`` wins over ``batch``."""
+    if ptr is None:
+        requested = _optional_batch_size(batch_size)
+        named = _clouds_in(batch, len(x), x.device, "batch")
+        if requested is not None and requested < named:
+            raise ValueError("batch_size is smaller than the largest batch ID")
+        clouds = max(named, requested or 0)
+        if batch is None:
+            clouds = max(1, clouds)
+        return _offsets(batch, len(x), x.device, clouds)
+    if isinstance(ptr, Tensor):
+        if ptr.device != x.device or ptr.dtype not in (torch.int32, torch.int64):
+            raise ValueError("ptr must be an integer tensor on the same device as x")
+        offsets = ptr.long()
+    elif isinstance(ptr, (list, tuple)):
+        offsets = torch.tensor(ptr, dtype=torch.long, device=x.device)
+    else:
+        raise TypeError("ptr must be a tensor, a sequence of integers, or None")
+    if offsets.ndim != 1 or len(offsets) == 0:
+        raise ValueError("ptr must be a non-empty one-dimensional offset array")
+    head, tail, descending = torch.stack(
+        (offsets[0], offsets[-1], (offsets[1:] < offsets[:-1]).any().long())).tolist()
+    if head != 0 or tail != len(x):
+        raise ValueError("ptr must start at 0 and end at len(x)")
+    if descending:
+        raise ValueError("ptr must be non-decreasing")
+    return offsets.contiguous()
 
 
-def _ratio(value, dtype: torch.dtype) -> Tensor:
-    """The ratio as the CPU scalar tensor torch_cluster would use (flat.py:125-147)."""
+def _ratio_tensor(value, dtype: torch.dtype) -> Tensor:
+    """The sampling ratio as the CPU tensor torch_cluster computes with: a
+    Python number becomes a 0-d tensor of the points' dtype, a tensor ratio
+    keeps its own dtype and shape (0-d and [1] promote differently)."""
     if value is None:
         value = 0.5
     if isinstance(value, Tensor):
         if value.numel() != 1 or value.ndim > 1:
             raise ValueError("ratio tensor must be scalar or a length-one vector")
-        result = value.detach().to("cpu")
+        ratio = value.detach().to("cpu")
     elif isinstance(value, bool) or not isinstance(value, (int, float)):
         raise TypeError("ratio must be a number or scalar tensor")
     else:
-        result = torch.tensor(float(value), dtype=dtype)
-    if not math.isfinite(float(result)) or float(result) < 0:
+        ratio = torch.tensor(float(value), dtype=dtype)
+    number = float(ratio)
+    if not (math.isfinite(number) and number >= 0):
         raise ValueError("ratio must be finite and non-negative")
-    return result
+    return ratio
 
 
-def _sample_counts(lengths: list[int], ratio: Tensor) -> list[int]:
-    """torch_cluster's GPU count rule: ceil(deg.to(ratio.dtype) * ratio)
-    (flat.py:150-158 with mps=True)."""
-    sizes = torch.tensor(lengths, dtype=ratio.dtype)
-    return torch.ceil(sizes * ratio).to(torch.long).tolist()
+def _samples_per_cloud(lengths: list[int], ratio: Tensor) -> list[int]:
+    """torch_cluster's GPU rule: ceil(length.to(ratio.dtype) * ratio)."""
+    return torch.ceil(torch.tensor(lengths, dtype=ratio.dtype) * ratio).long().tolist()
+
+
+def _radius_sq_torch_cluster(r: float) -> float:
+    """The torch_cluster threshold: r * r in double, then rounded to float32
+    (inf when that overflows)."""
+    try:
+        return struct.unpack("f", struct.pack("f", r * r))[0]
+    except OverflowError:
+        return math.inf
+
+
+# ---------------------------------------------------------------- fps
 
 
 def fps(
@@ -151,51 +192,52 @@ def fps(
     batch_size: int | None = None,
     ptr: Tensor | Sequence[int] | None = None,
 ) -> Tensor:
-    """Sample global point indices with the torch_cluster count rule
-    (flat.py:161-217).  ``ratio=None`` means 0.5; ``ptr`` takes precedence over
-    ``batch``; ``random_start=False`` starts from the first point of each
-    non-empty cloud.  Returns int64 indices on ``x.device``.
-    """
-    _points(x, "x")
+    """Global indices of farthest point samples, ``ceil(len * ratio)`` per
+    cloud (the torch_cluster count rule), flat.py:161-217.  ``ratio=None``
+    means 0.5; ``ptr`` takes precedence over ``batch``; without
+    ``random_start`` each cloud starts at its first point.  int64 on
+    ``x.device``."""
+    _rows(x, "x", coordinates=True)
     _native.require_device(x.device)
     if x.dtype != torch.float32:
         raise TypeError("x must be float32 on ROCm")
-    sample_ratio = _ratio(ratio, x.dtype)
-    offsets = _fps_ptr(x, batch, batch_size, ptr)
-    offset_values = offsets.cpu().tolist()
-    lengths = [hi - lo for lo, hi in zip(offset_values, offset_values[1:])]
-    counts = _sample_counts(lengths, sample_ratio)
-    output_offsets = [0]
+    ratio_t = _ratio_tensor(ratio, x.dtype)
+    offsets = _fps_offsets(x, batch, batch_size, ptr)
+    bounds = offsets.tolist()
+    lengths = [b - a for a, b in zip(bounds, bounds[1:])]
+    counts = _samples_per_cloud(lengths, ratio_t)
+    out_bounds = [0]
     for count in counts:
-        output_offsets.append(output_offsets[-1] + count)
-    if output_offsets[-1] == 0:
+        out_bounds.append(out_bounds[-1] + count)
+    total = out_bounds[-1]
+    if total == 0:
         return torch.empty(0, dtype=torch.long, device=x.device)
     if random_start:
-        length_tensor = torch.tensor(lengths, dtype=torch.long, device=x.device)
-        starts = (torch.rand(len(lengths), device=x.device) * length_tensor).long()
-        starts = torch.minimum(starts, (length_tensor - 1).clamp_min(0))
+        sizes = torch.tensor(lengths, dtype=torch.long, device=x.device)
+        draw = (torch.rand(len(lengths), device=x.device) * sizes).long()
+        starts = torch.minimum(draw, (sizes - 1).clamp_min(0))
     else:
         starts = torch.zeros(len(lengths), dtype=torch.long, device=x.device)
-    if any(c > 0 and n == 0 for c, n in zip(counts, lengths)):
+    longest = max(lengths)
+    if longest > _MAX_CLOUD or any(c > 0 and n == 0 for c, n in zip(counts, lengths)):
         raise ValueError("invalid ptr, out_ptr, or starts for the input point clouds")
-    max_len = max(lengths) if lengths else 0
-    if max_len > _UINT_MAX:
-        raise ValueError("invalid ptr, out_ptr, or starts for the input point clouds")
-    out = torch.empty(output_offsets[-1], dtype=torch.long, device=x.device)
-    x = x.contiguous()
-    out_ptr = torch.tensor(output_offsets, dtype=torch.long, device=x.device)
-    size = _native.size_query("pointops_fps_flat_scratch_bytes", len(x), max_len)
-    scratch = torch.empty(size, dtype=torch.uint8, device=x.device) if size else None
-    _native.call("pointops_fps_flat", x.data_ptr(), offsets.data_ptr(), out_ptr.data_ptr(),
+    points = x.contiguous()
+    out = torch.empty(total, dtype=torch.long, device=x.device)
+    out_ptr = torch.tensor(out_bounds, dtype=torch.long, device=x.device)
+    scratch_bytes = _native.size_query("pointops_fps_flat_scratch_bytes", len(points), longest)
+    scratch = torch.empty(scratch_bytes, dtype=torch.uint8, device=x.device) if scratch_bytes else None
+    _native.call("pointops_fps_flat", points.data_ptr(), offsets.data_ptr(), out_ptr.data_ptr(),
                  starts.contiguous().data_ptr(), out.data_ptr(), _native.ptr(scratch),
-                 len(lengths), len(x), max_len, _native.stream(x.device))
+                 len(lengths), len(points), longest, _native.stream(x.device))
     return out
 
 
-def _search_inputs(x: Tensor, y: Tensor, *, feature_space: bool = False) -> None:
-    validate = _features if feature_space else _points
-    validate(x, "x")
-    validate(y, "y")
+# ------------------------------------------------------ kNN and radius
+
+
+def _search_pair(x, y, *, coordinates: bool) -> None:
+    _rows(x, "x", coordinates=coordinates)
+    _rows(y, "y", coordinates=coordinates)
     if x.shape[1] != y.shape[1]:
         raise ValueError(f"x and y feature dimensions differ: {x.shape[1]} and {y.shape[1]}")
     if x.device != y.device:
@@ -204,60 +246,44 @@ def _search_inputs(x: Tensor, y: Tensor, *, feature_space: bool = False) -> None
         raise TypeError(f"x and y must have the same dtype, got {x.dtype} and {y.dtype}")
 
 
-def _nonnegative_int(value: int, name: str) -> int:
-    if isinstance(value, bool) or not isinstance(value, int) or value < 0:
-        raise ValueError(f"{name} must be a non-negative integer")
-    return value
-
-
-def _edges(indices: Tensor) -> Tensor:
-    """Drop -1 padding: [2, E] (query, reference) edges (flat.py:247-253)."""
-    if indices.numel() == 0:
-        return torch.empty((2, 0), dtype=torch.long, device=indices.device)
-    valid = indices >= 0
-    queries = torch.arange(indices.shape[0], device=indices.device, dtype=torch.long)
-    queries = queries[:, None].expand_as(indices)[valid]
-    return torch.stack((queries, indices[valid]), dim=0)
-
-
-def _torch_cluster_radius_sq(r: float) -> float:
-    """fl32(r * r) with r * r in double (_flat_search_mps.py:66-76)."""
-    try:
-        return struct.unpack("f", struct.pack("f", r * r))[0]
-    except OverflowError:
-        return math.inf
+def _edge_index(table: Tensor) -> Tensor:
+    """[2, E] (query row, reference row) pairs of a -1 padded (Q, K) table,
+    row-major."""
+    queries, slots = torch.nonzero(table >= 0, as_tuple=True)
+    return torch.stack((queries, table[queries, slots]))
 
 
 def knn_indices(x: Tensor, y: Tensor, ptr_x: Tensor, ptr_y: Tensor, k: int) -> Tensor:
-    """(Q, k) global x indices by (squared distance, index), -1 padded."""
-    out = torch.empty((len(y), k), dtype=torch.int64, device=x.device)
-    if len(y) == 0 or k == 0:
-        return out
-    _native.call("pointops_knn_flat", y.data_ptr(), x.data_ptr(), ptr_y.contiguous().data_ptr(),
-                 ptr_x.contiguous().data_ptr(), out.data_ptr(), len(y), len(ptr_x) - 1,
-                 x.shape[1], k, _native.stream(x.device))
-    return out
+    """(Q, k) global x rows nearest to each y row, ordered by (squared
+    distance, index), -1 where a cloud has fewer than k rows."""
+    table = torch.empty((len(y), k), dtype=torch.int64, device=x.device)
+    if len(y) and k:
+        _native.call("pointops_knn_flat", y.data_ptr(), x.data_ptr(), ptr_y.contiguous().data_ptr(),
+                     ptr_x.contiguous().data_ptr(), table.data_ptr(), len(y), len(ptr_x) - 1,
+                     x.shape[1], k, _native.stream(x.device))
+    return table
 
 
 def radius_indices(x: Tensor, y: Tensor, ptr_x: Tensor, ptr_y: Tensor, r: float,
                    max_num_neighbors: int, ignore_same_index: bool = False) -> Tensor:
-    """First valid global x indices per query, -1 padded
-    (_flat_search_mps.py:111-147)."""
+    """(Q, max_num_neighbors) first x rows in index order with squared
+    distance below fl32(r * r in double), -1 padded; with
+    ``ignore_same_index`` a row equal to the query's own row number is
+    skipped before the cap (_flat_search_mps.py:111-147)."""
     if x.dtype not in (torch.float32, torch.float16) or y.dtype != x.dtype:
         raise TypeError("flat radius requires matching float32 or float16 x and y")
     radius_f32, _ = _checked_radius_and_k(r, max_num_neighbors)
-    radius_sq = _torch_cluster_radius_sq(float(r))
-    out = torch.empty((len(y), max_num_neighbors), dtype=torch.int64, device=x.device)
+    table = torch.empty((len(y), max_num_neighbors), dtype=torch.int64, device=x.device)
     if len(y) == 0 or max_num_neighbors == 0:
-        return out
+        return table
     if radius_f32 == 0.0:
-        out.fill_(-1)
-        return out
-    name = "pointops_radius_flat_f32" if x.dtype == torch.float32 else "pointops_radius_flat_f16"
-    _native.call(name, y.data_ptr(), x.data_ptr(), ptr_y.contiguous().data_ptr(),
-                 ptr_x.contiguous().data_ptr(), out.data_ptr(), len(y), len(ptr_x) - 1,
-                 max_num_neighbors, radius_sq, int(ignore_same_index), _native.stream(x.device))
-    return out
+        return table.fill_(-1)
+    entry = "pointops_radius_flat_f32" if x.dtype == torch.float32 else "pointops_radius_flat_f16"
+    _native.call(entry, y.data_ptr(), x.data_ptr(), ptr_y.contiguous().data_ptr(),
+                 ptr_x.contiguous().data_ptr(), table.data_ptr(), len(y), len(ptr_x) - 1,
+                 max_num_neighbors, _radius_sq_torch_cluster(float(r)), int(ignore_same_index),
+                 _native.stream(x.device))
+    return table
 
 
 def knn(
@@ -270,25 +296,26 @@ def knn(
     num_workers: int = 1,
     batch_size: int | None = None,
 ) -> Tensor:
-    """Global ``[query, reference]`` edges for the nearest points
-    (flat.py:291-329).  The effective ``min(k, len(x))`` must be at most 256;
-    ``cosine=True`` is not implemented; ``num_workers`` has no effect.
-    """
-    _search_inputs(x, y, feature_space=True)
-    k = _nonnegative_int(k, "k")
+    """``[2, E]`` (query, reference) edges to the ``k`` nearest references of
+    each query within its cloud (flat.py:291-329).  ``min(k, len(x))`` must
+    be at most 256; ``cosine=True`` is not implemented; ``num_workers`` has
+    no effect."""
+    _search_pair(x, y, coordinates=False)
+    k = _count_arg(k, "k")
     if cosine:
         raise NotImplementedError("cosine kNN is not supported")
-    _nonnegative_int(num_workers, "num_workers")
+    _count_arg(num_workers, "num_workers")
     _native.require_device(x.device)
     if x.dtype != torch.float32:
         raise TypeError("x and y must be float32 for kNN on ROCm")
     if k == 0 or len(x) == 0 or len(y) == 0:
         return torch.empty((2, 0), dtype=torch.long, device=x.device)
-    ptr_x, ptr_y = _pair_ptrs(x, y, batch_x, batch_y, batch_size)
+    layout = _SearchLayout.of(x, y, batch_x, batch_y, batch_size)
     width = min(k, len(x))
     if width > _KNN_MAX_K:
         raise ValueError(f"effective k must be at most {_KNN_MAX_K} on ROCm, got {width}")
-    return _edges(knn_indices(x.contiguous(), y.contiguous(), ptr_x, ptr_y, width))
+    table = knn_indices(x.contiguous(), y.contiguous(), layout.x_offsets, layout.y_offsets, width)
+    return _edge_index(table)
 
 
 def radius(
@@ -302,39 +329,44 @@ def radius(
     batch_size: int | None = None,
     ignore_same_index: bool = False,
 ) -> Tensor:
-    """Global ``[query, reference]`` edges with squared distance ``< r^2``
-    (flat.py:332-373): neighbours in reference input order, at most
-    ``max_num_neighbors`` per query.  ``ignore_same_index=True`` is not
-    implemented (as in the reference's public API).
-    """
-    _search_inputs(x, y)
-    limit = _nonnegative_int(max_num_neighbors, "max_num_neighbors")
-    _nonnegative_int(num_workers, "num_workers")
+    """``[2, E]`` (query, reference) edges to the first references of each
+    query's cloud, in index order, with squared distance below ``r**2``
+    (flat.py:332-373); at most ``max_num_neighbors`` per query.
+    ``ignore_same_index=True`` is not implemented, as in the reference."""
+    _search_pair(x, y, coordinates=True)
+    limit = _count_arg(max_num_neighbors, "max_num_neighbors")
+    _count_arg(num_workers, "num_workers")
     if ignore_same_index:
         raise NotImplementedError("ignore_same_index=True is not supported")
-    if isinstance(r, bool) or not isinstance(r, (int, float)):
-        raise ValueError("r must be a finite non-negative number")
-    r = float(r)
-    if not math.isfinite(r) or r < 0:
+    if isinstance(r, bool) or not isinstance(r, (int, float)) or not math.isfinite(float(r)) \
+            or float(r) < 0:
         raise ValueError("r must be a finite non-negative number")
     _native.require_device(x.device)
     if x.dtype not in (torch.float16, torch.float32):
         raise TypeError("x and y must be float16 or float32 for radius on ROCm")
     if limit == 0 or len(x) == 0 or len(y) == 0:
         return torch.empty((2, 0), dtype=torch.long, device=x.device)
-    ptr_x, ptr_y = _pair_ptrs(x, y, batch_x, batch_y, batch_size)
-    width = min(limit, len(x))
-    return _edges(radius_indices(x.contiguous(), y.contiguous(), ptr_x, ptr_y, r, width))
+    layout = _SearchLayout.of(x, y, batch_x, batch_y, batch_size)
+    table = radius_indices(x.contiguous(), y.contiguous(), layout.x_offsets, layout.y_offsets,
+                           float(r), min(limit, len(x)))
+    return _edge_index(table)
 
 
-def _graph_edges(edges: Tensor, loop: bool, flow: str) -> Tensor:
-    if flow not in ("source_to_target", "target_to_source"):
+# --------------------------------------------------------------- graphs
+
+
+def _check_flow(flow: str) -> None:
+    if flow not in _FLOWS:
         raise ValueError("flow must be 'source_to_target' or 'target_to_source'")
-    if flow == "source_to_target":
-        edges = edges.flip(0)
+
+
+def _as_graph(edges: Tensor, loop: bool, flow: str) -> Tensor:
+    """torch_cluster 1.6.3 orientation of self-search edges: (source,
+    target) rows, reference first for ``source_to_target``; without ``loop``
+    the edges from a point to itself are dropped."""
     if not loop:
         edges = edges[:, edges[0] != edges[1]]
-    return edges
+    return edges.flip(0) if flow == "source_to_target" else edges
 
 
 def knn_graph(
@@ -347,13 +379,13 @@ def knn_graph(
     num_workers: int = 1,
     batch_size: int | None = None,
 ) -> Tensor:
-    """kNN graph with torch_cluster 1.6.3 edge orientation (flat.py:386-404)."""
-    k = _nonnegative_int(k, "k")
-    if flow not in ("source_to_target", "target_to_source"):
-        raise ValueError("flow must be 'source_to_target' or 'target_to_source'")
-    edges = knn(x, x, k if loop else k + 1, batch, batch,
-                cosine=cosine, num_workers=num_workers, batch_size=batch_size)
-    return _graph_edges(edges, loop, flow)
+    """kNN graph of ``x`` (flat.py:386-404): ``k + 1`` neighbours are searched
+    when self loops are removed."""
+    k = _count_arg(k, "k")
+    _check_flow(flow)
+    edges = knn(x, x, k if loop else k + 1, batch, batch, cosine=cosine,
+                num_workers=num_workers, batch_size=batch_size)
+    return _as_graph(edges, loop, flow)
 
 
 def radius_graph(
@@ -366,13 +398,13 @@ def radius_graph(
     num_workers: int = 1,
     batch_size: int | None = None,
 ) -> Tensor:
-    """Radius graph with torch_cluster 1.6.3 edge orientation (flat.py:407-425)."""
-    limit = _nonnegative_int(max_num_neighbors, "max_num_neighbors")
-    if flow not in ("source_to_target", "target_to_source"):
-        raise ValueError("flow must be 'source_to_target' or 'target_to_source'")
+    """Radius graph of ``x`` (flat.py:407-425): ``max_num_neighbors + 1``
+    candidates when self loops are removed."""
+    limit = _count_arg(max_num_neighbors, "max_num_neighbors")
+    _check_flow(flow)
     edges = radius(x, x, r, batch, batch, limit if loop else limit + 1,
                    num_workers=num_workers, batch_size=batch_size)
-    return _graph_edges(edges, loop, flow)
+    return _as_graph(edges, loop, flow)
 
 
 __all__ = ["fps", "knn", "radius", "knn_graph", "radius_graph"]

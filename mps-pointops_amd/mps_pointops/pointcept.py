@@ -26,51 +26,62 @@ _PAD_DISTANCE = 100_000.0     # sqrt(1e10), the upstream unfilled distance
 _MAX_NSAMPLE = 256            # the native kNN's K limit (ops.py:30)
 
 
-def _points(value: Tensor, name: str) -> None:
+def _points(value, name: str) -> None:
     if not isinstance(value, Tensor) or value.ndim != 2 or value.shape[1] != 3:
         raise ValueError(f"{name} must be a tensor of shape (N, 3)")
     if value.dtype != torch.float32:
         raise ValueError(f"{name} must be float32")
 
 
-def _offsets(value: Tensor, count: int | None, device: torch.device, name: str) -> list[int]:
-    """Inclusive cumulative counts -> [0, *ends] (pointcept.py:47-58)."""
-    if not isinstance(value, Tensor) or value.ndim != 1 or value.dtype not in (torch.int32, torch.int64):
+def _bounds(offset, rows: int | None, device: torch.device, name: str) -> list[int]:
+    """Pointcept's inclusive per-batch ends (e.g. ``[4, 9]``) as the row
+    bounds ``[0, 4, 9]``, read to the host once; ``rows`` (when given) must
+    be the last end (pointcept.py:47-58)."""
+    if (not isinstance(offset, Tensor) or offset.ndim != 1
+            or offset.dtype not in (torch.int32, torch.int64)):
         raise ValueError(f"{name} must be a one-dimensional int32/int64 tensor")
-    if value.device != device:
+    if offset.device != device:
         raise ValueError(f"{name} must be on {device}")
-    ends = value.tolist()
-    if count is not None and ((ends and ends[-1] != count) or (not ends and count != 0)):
-        raise ValueError(f"{name} must end at its point count ({count})")
-    if any(end < start for start, end in zip((0, *ends[:-1]), ends)):
+    bounds = [0, *offset.tolist()]
+    if rows is not None and bounds[-1] != rows:
+        raise ValueError(f"{name} must end at its point count ({rows})")
+    if any(hi < lo for lo, hi in zip(bounds, bounds[1:])):
         raise ValueError(f"{name} must be nondecreasing and nonnegative")
-    return [0, *ends]
+    return bounds
 
 
-def _pairs(xyz: Tensor, offset: Tensor, new_xyz: Tensor | None,
-           new_offset: Tensor | None) -> tuple[Tensor, list[int], list[int]]:
-    """pointcept.py:61-77."""
+def _pairs(xyz, offset, new_xyz, new_offset) -> tuple[Tensor, list[int], list[int]]:
+    """Reference and query rows with their bounds; without new_xyz /
+    new_offset the points query themselves (pointcept.py:61-77)."""
     _points(xyz, "xyz")
-    if new_xyz is None and new_offset is None:
-        new_xyz, new_offset = xyz, offset
-    elif new_xyz is None or new_offset is None:
+    if (new_xyz is None) != (new_offset is None):
         raise ValueError("new_xyz and new_offset must be provided together")
+    if new_xyz is None:
+        new_xyz, new_offset = xyz, offset
     _points(new_xyz, "new_xyz")
     if xyz.device != new_xyz.device:
         raise ValueError("xyz and new_xyz must be on the same device")
-    ref_ends = _offsets(offset, len(xyz), xyz.device, "offset")
-    query_ends = _offsets(new_offset, len(new_xyz), xyz.device, "new_offset")
-    if len(ref_ends) != len(query_ends):
+    ref_bounds = _bounds(offset, len(xyz), xyz.device, "offset")
+    query_bounds = _bounds(new_offset, len(new_xyz), xyz.device, "new_offset")
+    if len(ref_bounds) != len(query_bounds):
         raise ValueError("offset and new_offset must have the same batch count")
-    return new_xyz, ref_ends, query_ends
+    return new_xyz, ref_bounds, query_bounds
+
+
+def _gather_rows(table: Tensor, idx: Tensor) -> Tensor:
+    """(M, K, C) rows of an (N, C) table at (M, K) indices, zeros where the
+    index is -1 (their gradient is masked out as well)."""
+    rows = table.index_select(0, idx.reshape(-1).long().clamp_min(0))
+    rows = rows.view(*idx.shape, table.shape[1])
+    return rows.where((idx >= 0)[..., None], 0.0)
 
 
 def farthest_point_sampling(xyz: Tensor, offset: Tensor, new_offset: Tensor) -> Tensor:
     """Global int32 FPS indices, starting at each batch's first point
     (pointcept.py:80-104): one ragged launch for every batch."""
     _points(xyz, "xyz")
-    source = _offsets(offset, len(xyz), xyz.device, "offset")
-    target = _offsets(new_offset, None, xyz.device, "new_offset")
+    source = _bounds(offset, len(xyz), xyz.device, "offset")
+    target = _bounds(new_offset, None, xyz.device, "new_offset")
     if len(source) != len(target):
         raise ValueError("offset and new_offset must have the same batch count")
     lengths = [hi - lo for lo, hi in zip(source, source[1:])]
@@ -131,30 +142,25 @@ def knn_query(nsample: int, xyz: Tensor, offset: Tensor, new_xyz: Tensor | None 
 def grouping(idx: Tensor, feat: Tensor, xyz: Tensor, new_xyz: Tensor | None = None,
              with_xyz: bool = False) -> Tensor:
     """(N, C) features gathered to (M, K, C), zeros for -1; with ``with_xyz``
-    the relative positions first, (M, K, 3+C) (pointcept.py:175-210)."""
+    the neighbours' positions relative to their query come first, (M, K,
+    3+C) (pointcept.py:175-210).  Gradients reach ``feat`` and, through the
+    relative positions, ``xyz`` and ``new_xyz``; padded slots carry none."""
     _points(xyz, "xyz")
-    if not isinstance(feat, Tensor) or feat.ndim != 2 or len(feat) != len(xyz):
-        raise ValueError("feat must have shape (N, C) matching xyz")
-    if feat.dtype != torch.float32 or feat.device != xyz.device:
-        raise ValueError("feat must be float32 on the xyz device")
+    _check_features(feat, xyz)
     if not isinstance(idx, Tensor) or idx.ndim != 2 or idx.dtype not in (torch.int32, torch.int64):
         raise ValueError("idx must be a two-dimensional int32/int64 tensor")
     if idx.device != xyz.device:
         raise ValueError("idx must be on the xyz device")
-    if bool((idx < -1).any()) or bool((idx >= len(xyz)).any()):
+    if bool(((idx < -1) | (idx >= len(xyz))).any().item()):
         raise ValueError("idx contains an out-of-range point index")
-    valid = idx >= 0
-    safe = torch.where(valid, idx.long(), len(xyz))
-    grouped = torch.cat((feat, feat.new_zeros((1, feat.shape[1]))), dim=0)[safe]
+    grouped = _gather_rows(feat, idx)
     if not with_xyz:
         return grouped
-    if new_xyz is None:
-        new_xyz = xyz
-    _points(new_xyz, "new_xyz")
-    if new_xyz.device != xyz.device or len(new_xyz) != len(idx):
+    centres = xyz if new_xyz is None else new_xyz
+    _points(centres, "new_xyz")
+    if centres.device != xyz.device or len(centres) != len(idx):
         raise ValueError("new_xyz must have one row per idx row on the xyz device")
-    relative = torch.cat((xyz, xyz.new_zeros((1, 3))), dim=0)[safe] - new_xyz.unsqueeze(1)
-    relative = torch.where(valid.unsqueeze(-1), relative, 0)
+    relative = (_gather_rows(xyz, idx) - centres[:, None, :]).where((idx >= 0)[..., None], 0.0)
     return torch.cat((relative, grouped), dim=-1)
 
 
@@ -173,19 +179,22 @@ def knn_query_and_group(feat: Tensor, xyz: Tensor, offset: Tensor | None = None,
 def interpolation(xyz: Tensor, new_xyz: Tensor, feat: Tensor, offset: Tensor,
                   new_offset: Tensor, k: int = 3) -> Tensor:
     """Inverse-distance interpolation of (N, C) features to the new points
-    over their k nearest (pointcept.py:228-253): -1 neighbours weigh 0, an
-    empty reference batch gives 0, weights are constants for autograd."""
+    over their ``k`` nearest (pointcept.py:228-253): weights 1 / (d + 1e-8)
+    normalised per query (the sum floored at 1e-20), 0 for -1 neighbours,
+    so a query of an empty reference batch gets 0; the weights are
+    constants for autograd."""
+    _check_features(feat, xyz)
+    idx, dist = knn_query(k, xyz, offset, new_xyz, new_offset)
+    inverse = (1.0 / (dist + 1e-8)).where(idx >= 0, 0.0)
+    weight = inverse / inverse.sum(dim=1, keepdim=True).clamp_min(1e-20)
+    return (_gather_rows(feat, idx) * weight[..., None]).sum(dim=1)
+
+
+def _check_features(feat, xyz: Tensor) -> None:
     if not isinstance(feat, Tensor) or feat.ndim != 2 or len(feat) != len(xyz):
         raise ValueError("feat must have shape (N, C) matching xyz")
     if feat.dtype != torch.float32 or feat.device != xyz.device:
         raise ValueError("feat must be float32 on the xyz device")
-    idx, dist = knn_query(k, xyz, offset, new_xyz, new_offset)
-    valid = idx >= 0
-    reciprocal = torch.where(valid, 1.0 / (dist + 1e-8), 0.0)
-    weight = reciprocal / reciprocal.sum(dim=1, keepdim=True).clamp_min(1e-20)
-    padded = torch.cat((feat, feat.new_zeros((1, feat.shape[1]))), dim=0)
-    safe = torch.where(valid, idx.long(), len(feat))
-    return (padded[safe] * weight.unsqueeze(-1)).sum(dim=1)
 
 
 __all__ = ["farthest_point_sampling", "knn_query", "grouping", "knn_query_and_group",

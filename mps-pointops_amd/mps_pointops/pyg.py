@@ -39,7 +39,7 @@ def _ptrs(x: Tensor, y: Tensor, ptr_x: Tensor | None, ptr_y: Tensor | None, *,
           feature_space: bool = False) -> tuple[Tensor, Tensor]:
     """pyg.py:59-72: an unbatched x is the whole reference set for every
     query (ptr_y is then ignored); ptr_x needs ptr_y."""
-    flat._search_inputs(x, y, feature_space=feature_space)
+    flat._search_pair(x, y, coordinates=not feature_space)
     if ptr_x is None:
         return (torch.tensor([0, len(x)], dtype=torch.long, device=x.device),
                 torch.tensor([0, len(y)], dtype=torch.long, device=y.device))
@@ -56,8 +56,8 @@ def _knn_rocm(x: Tensor, y: Tensor, ptr_x: Tensor | None = None, ptr_y: Tensor |
               k: int = 1, cosine: bool = False, num_workers: int = 1) -> Tensor:
     """pyg-lib's query-major ``[query, reference]`` edges (pyg.py:75-101)."""
     ptr_x, ptr_y = _ptrs(x, y, ptr_x, ptr_y, feature_space=True)
-    k = flat._nonnegative_int(k, "k")
-    flat._nonnegative_int(num_workers, "num_workers")
+    k = flat._count_arg(k, "k")
+    flat._count_arg(num_workers, "num_workers")
     if cosine:
         raise NotImplementedError("cosine kNN is not supported for ROCm point clouds")
     if x.dtype != torch.float32:
@@ -67,7 +67,7 @@ def _knn_rocm(x: Tensor, y: Tensor, ptr_x: Tensor | None = None, ptr_y: Tensor |
     width = min(k, len(x))
     if width > flat._KNN_MAX_K:
         raise ValueError(f"effective k must be at most {flat._KNN_MAX_K} on ROCm, got {width}")
-    return flat._edges(flat.knn_indices(x.contiguous(), y.contiguous(), ptr_x, ptr_y, width))
+    return flat._edge_index(flat.knn_indices(x.contiguous(), y.contiguous(), ptr_x, ptr_y, width))
 
 
 def _radius_rocm(x: Tensor, y: Tensor, ptr_x: Tensor | None = None, ptr_y: Tensor | None = None,
@@ -76,8 +76,8 @@ def _radius_rocm(x: Tensor, y: Tensor, ptr_x: Tensor | None = None, ptr_y: Tenso
     """The first neighbours in x order, optionally without equal indices
     (pyg.py:104-130)."""
     ptr_x, ptr_y = _ptrs(x, y, ptr_x, ptr_y)
-    limit = flat._nonnegative_int(max_num_neighbors, "max_num_neighbors")
-    flat._nonnegative_int(num_workers, "num_workers")
+    limit = flat._count_arg(max_num_neighbors, "max_num_neighbors")
+    flat._count_arg(num_workers, "num_workers")
     if x.dtype not in (torch.float16, torch.float32):
         raise TypeError("x and y must be float16 or float32 for radius on ROCm")
     if limit == 0 or len(x) == 0 or len(y) == 0:
@@ -85,7 +85,7 @@ def _radius_rocm(x: Tensor, y: Tensor, ptr_x: Tensor | None = None, ptr_y: Tenso
     width = min(limit, len(x))
     indices = flat.radius_indices(x.contiguous(), y.contiguous(), ptr_x, ptr_y, r, width,
                                   ignore_same_index=ignore_same_index)
-    return flat._edges(indices)
+    return flat._edge_index(indices)
 
 
 def _fps_rocm(src: Tensor, ptr: Tensor, ratio: float = 0.5, random_start: bool = True) -> Tensor:

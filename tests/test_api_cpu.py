@@ -167,12 +167,12 @@ def test_checked_radius_and_k_rules():
         _checked_radius_and_k(1.0, 1 << 63)
     # torch_cluster's threshold differs by one ulp at r=0.21 and r=0.1
     # (tests/test_flat.py:207-224).
-    from mps_pointops.flat import _torch_cluster_radius_sq
+    from mps_pointops.flat import _radius_sq_torch_cluster
 
     r21 = np.float32(0.21)
-    assert np.float32(r21 * r21) < np.float32(_torch_cluster_radius_sq(0.21))
+    assert np.float32(r21 * r21) < np.float32(_radius_sq_torch_cluster(0.21))
     r01 = np.float32(0.1)
-    assert np.float32(r01 * r01) > np.float32(_torch_cluster_radius_sq(0.1))
+    assert np.float32(r01 * r01) > np.float32(_radius_sq_torch_cluster(0.1))
 
 
 def test_pointnet2_validation():
@@ -214,16 +214,16 @@ def test_chamfer_argument_validation():
 
 def test_flat_sample_counts_follow_torch_cluster_gpu_rule():
     """tests/test_flat.py:155-204: ceil(deg * ratio) in the ratio's dtype."""
-    from mps_pointops.flat import _ratio, _sample_counts
+    from mps_pointops.flat import _ratio_tensor, _samples_per_cloud
 
     for n, ratio, expected in ((25, 0.6, 16), (45, 0.6, 28), (50, 0.3, 16), (90, 0.3, 28),
                                (10, 0.5, 5), (7, 0.5, 4), (9, 1.0, 9)):
-        assert _sample_counts([n], _ratio(ratio, torch.float32)) == [expected]
+        assert _samples_per_cloud([n], _ratio_tensor(ratio, torch.float32)) == [expected]
     # A float64 tensor ratio keeps its dtype on the GPU rule: 15 for 0-D and [1].
-    assert _sample_counts([25], _ratio(torch.tensor(0.6, dtype=torch.float64), torch.float32)) == [15]
-    assert _sample_counts([25], _ratio(torch.tensor([0.6], dtype=torch.float64), torch.float32)) == [15]
+    assert _samples_per_cloud([25], _ratio_tensor(torch.tensor(0.6, dtype=torch.float64), torch.float32)) == [15]
+    assert _samples_per_cloud([25], _ratio_tensor(torch.tensor([0.6], dtype=torch.float64), torch.float32)) == [15]
     with pytest.raises(ValueError, match="ratio"):
-        _ratio(-0.1, torch.float32)
+        _ratio_tensor(-0.1, torch.float32)
 
 
 def test_flat_validation():
@@ -382,3 +382,97 @@ def test_chamfer_grid_eligibility():
     assert not chamfer._grid_eligible(*clouds(32, 2048, 8192), 2, True)  # too few queries
     assert not chamfer._grid_eligible(*clouds(1, 4096, 8192), 2, True)  # too few pairs
     assert not chamfer._grid_eligible(*clouds(70000, 4096, 8192), 2, True)  # batch limit
+
+
+def test_flat_layout_offsets_match_searchsorted():
+    """Batch vectors -> cloud offsets (one bincount prefix sum) against
+    numpy's searchsorted, including empty clouds and a larger batch_size."""
+    from mps_pointops import flat
+
+    rng = np.random.default_rng(4)
+    for trial in range(20):
+        nx, ny = int(rng.integers(1, 300)), int(rng.integers(1, 200))
+        bx = np.sort(rng.integers(0, 6, nx))
+        by = np.sort(rng.integers(0, 6, ny))
+        extra = int(rng.integers(0, 3)) if trial % 2 else None
+        size = max(int(bx[-1]), int(by[-1])) + 1 + (extra or 0)
+        x, y = torch.rand(nx, 3), torch.rand(ny, 3)
+        layout = flat._SearchLayout.of(x, y, torch.from_numpy(bx), torch.from_numpy(by).int(),
+                                       None if extra is None else size)
+        assert layout.x_offsets.tolist() == np.searchsorted(bx, np.arange(size + 1)).tolist()
+        assert layout.y_offsets.tolist() == np.searchsorted(by, np.arange(size + 1)).tolist()
+    one = flat._SearchLayout.of(torch.rand(7, 3), torch.rand(2, 3), None, None, None)
+    assert one.x_offsets.tolist() == [0, 7] and one.y_offsets.tolist() == [0, 2]
+
+
+def test_flat_layout_errors_follow_reference_messages():
+    """flat.py:49-98: the reference's checks and messages, in its order."""
+    from mps_pointops import flat
+
+    x = torch.rand(4, 3)
+    with pytest.raises(ValueError, match="batch_size must be a non-negative integer"):
+        flat._SearchLayout.of(x, x, None, None, -1)
+    with pytest.raises(TypeError, match="batch_x must be a torch.Tensor or None"):
+        flat._SearchLayout.of(x, x, [0, 0, 0, 0], None, None)
+    with pytest.raises(ValueError, match=r"batch_x must have shape \(4,\)"):
+        flat._SearchLayout.of(x, x, torch.zeros(3, dtype=torch.long), None, None)
+    with pytest.raises(TypeError, match="integer dtype"):
+        flat._SearchLayout.of(x, x, torch.zeros(4), None, None)
+    with pytest.raises(ValueError, match="sorted with non-negative batch IDs"):
+        flat._SearchLayout.of(x, x, torch.tensor([0, 1, 0, 1]), torch.zeros(4, dtype=torch.long),
+                              None)
+    with pytest.raises(ValueError, match="sorted with non-negative batch IDs"):
+        flat._SearchLayout.of(x, x, torch.tensor([-1, 0, 0, 0]), None, None)
+    with pytest.raises(ValueError, match="both required for multiple batches"):
+        flat._SearchLayout.of(x, x, torch.tensor([0, 0, 1, 1]), None, None)
+    with pytest.raises(ValueError, match="batch_size is smaller than the largest batch ID"):
+        b = torch.tensor([0, 0, 2, 2])
+        flat._SearchLayout.of(x, x, b, b, 2)
+
+
+def test_flat_fps_offsets_ptr_and_batch():
+    from mps_pointops import flat
+
+    x = torch.rand(10, 3)
+    assert flat._fps_offsets(x, None, None, [0, 4, 10]).tolist() == [0, 4, 10]
+    assert flat._fps_offsets(x, None, None, torch.tensor([0, 10], dtype=torch.int32)).tolist() \
+        == [0, 10]
+    assert flat._fps_offsets(x, None, None, None).tolist() == [0, 10]
+    b = torch.tensor([0, 0, 0, 1, 1, 3, 3, 3, 3, 3])
+    assert flat._fps_offsets(x, b, None, None).tolist() == [0, 3, 5, 5, 10]
+    assert flat._fps_offsets(x, b, 6, None).tolist() == [0, 3, 5, 5, 10, 10, 10]
+    assert flat._fps_offsets(torch.rand(0, 3), torch.zeros(0, dtype=torch.long), None,
+                             None).tolist() == [0]
+    with pytest.raises(TypeError, match="ptr must be a tensor, a sequence of integers, or None"):
+        flat._fps_offsets(x, None, None, 3)
+    with pytest.raises(ValueError, match="non-empty one-dimensional offset array"):
+        flat._fps_offsets(x, None, None, [])
+    with pytest.raises(ValueError, match="start at 0 and end at len"):
+        flat._fps_offsets(x, None, None, [0, 9])
+    with pytest.raises(ValueError, match="non-decreasing"):
+        flat._fps_offsets(x, None, None, [0, 6, 4, 10])
+    with pytest.raises(ValueError, match="integer tensor on the same device"):
+        flat._fps_offsets(x, None, None, torch.tensor([0.0, 10.0]))
+    with pytest.raises(ValueError, match="batch_size is smaller"):
+        flat._fps_offsets(x, b, 2, None)
+
+
+def test_compat_install_registers_and_respects_existing(monkeypatch):
+    import sys as _sys
+    import types
+
+    from mps_pointops import compat
+
+    for name in ("pointnet2_ops", "pointnet2_ops.pointnet2_utils", "knn_cuda", "torch_cluster",
+                 "pointops"):
+        monkeypatch.delitem(_sys.modules, name, raising=False)
+    monkeypatch.setitem(_sys.modules, "knn_cuda", types.ModuleType("knn_cuda"))
+    names = compat.install()
+    assert names == ["pointnet2_ops", "pointnet2_ops.pointnet2_utils", "torch_cluster"]
+    from pointnet2_ops import pointnet2_utils
+    assert pointnet2_utils.ball_query is compat.ball_query
+    assert _sys.modules["pointnet2_ops"].__path__ == []
+    from torch_cluster import knn_graph
+    assert knn_graph.__module__ == "mps_pointops.flat"
+    assert compat.install(force=True, pointcept=True)[-1] == "pointops"
+    from pointops import interpolation  # noqa: F401
