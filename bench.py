@@ -145,11 +145,11 @@ class KernelTimer:
 
 
 def fps_kernel_name(n: int) -> str:
-    """Template instance fps_lazy_regs_kernel<P,512> that a cloud of n points uses."""
+    """Template instance fps_tiled_kernel<P,512> that a cloud of n points uses."""
     p = 1
     while p * 512 < n:
         p *= 2
-    return f"fps_lazy_regs_kernel<{p},512>"
+    return f"fps_tiled_kernel<{p},512>"
 
 
 def profiled_traffic(kernel: str, workload: str):

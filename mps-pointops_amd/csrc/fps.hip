@@ -9,22 +9,21 @@
 //
 //
 // Kernels:
-//   fps_lazy_regs_kernel<P,T>  one workgroup per cloud, the cloud's points
-//                              and running distances in VGPRs (P consecutive
-//                              points per thread, so lane order is index
-//                              order); exact steps over 64 published
-//                              candidates between exchanges (clouds of up to
-//                              8192 points, batched or ragged).
-//   fps_global_kernel<T>       one workgroup per cloud for larger clouds of a
-//                              batch: points re-read from L2, running
-//                              distances in a caller-provided scratch array.
-//   fps_lazy_kernel<P,T>       one cloud over up to 256 CUs (cooperative
-//                              launch): each workgroup keeps its chunk in
-//                              VGPRs; an exchange publishes every wave's best
-//                              candidate and a bound, after which every
-//                              workgroup takes exact steps over the
-//                              candidates alone until the bound could be
-//                              reached.
+//   fps_tiled_kernel<P,T>   one workgroup per cloud of up to 8192 points
+//                           (batched or ragged), its points and running
+//                           distances in VGPRs, sorted into spatially compact
+//                           64-point tiles so that a step updates only the
+//                           tiles it can change; exact steps over 64
+//                           published candidates between exchanges.
+//   fps_global_kernel<T>    one workgroup per cloud for larger clouds of a
+//                           batch: points re-read from L2, running distances
+//                           in a caller-provided scratch array.
+//   fps_lazy_kernel<P,T>    one cloud over up to 256 CUs (cooperative
+//                           launch): each workgroup keeps its chunk in VGPRs;
+//                           an exchange publishes every wave's best candidate
+//                           and a bound, after which every workgroup takes
+//                           exact steps over the candidates alone until the
+//                           bound could be reached.
 #include <hip/hip_cooperative_groups.h>
 
 #include <cstdlib>
@@ -103,27 +102,55 @@ struct alignas(16) WaveBest {
     float x, y, z;
     int pad[3];
 };
-// fps_lazy_regs_kernel<P,T>: the batched kernel with the exchange of
-// fps_lazy_kernel inside one workgroup.  At an exchange every wave extracts
-// its KC = 64 / NW best points (largest running distance, then smallest
-// index) and the (KC+1)-th largest running distance, its bound, into LDS;
-// after one barrier every wave holds all 64 candidates, one per lane, and
-// takes steps on its own -- no barrier -- choosing the candidate with the
-// largest distance (smallest index on ties), updating its own points and the
-// candidates with it, while the choice is provably the exact argmax: always
-// for the first step after an exchange, and afterwards while the chosen
-// distance is strictly above every wave's bound.  All waves see the same
-// candidates, so they take the same steps.
+// fps_tiled_kernel<P,T>: the lazy single-workgroup FPS on a spatially sorted
+// cloud, so that most per-step updates can be skipped.
+//
+// Setup: the cloud is counting-sorted in LDS by a 12-bit Morton key of its
+// 16 x 16 x 16 cell (over the cloud's bounding box); sorted position q goes
+// to wave q / (64 P), slot (q / 64) % P, lane q % 64, so every (wave, slot) --
+// a tile -- holds 64 nearby points.  Each point keeps its original index,
+// which breaks every tie (largest running distance, then smallest index),
+// so results do not depend on the sort.  Lane s of every wave holds the
+// bounding box of the wave's tile s.
+//
+// Steps are taken lazily: at an exchange every wave publishes its KC best
+// points (largest running distance, then smallest index) and the (KC+1)-th
+// largest running distance, its bound; every wave then holds the 64
+// candidates, one per lane, and takes steps on its own (no barrier) while the
+// chosen key is provably the argmax of the cloud -- always for the first
+// step after an exchange (each wave published its maximum), afterwards while
+// it is strictly above every bound (an unpublished running distance is at
+// most its wave's bound, and distances only decrease).  Candidates are
+// updated with the points' own arithmetic.  A step with centroid c and chosen key M (the
+// largest running distance of the cloud) updates tile s only if
+// lb(c, box_s) < M, where lb applies the update's own rounded operations
+// to the per-axis gaps between c and the box: rounding is monotone, so lb
+// is at most the rounded squared distance of every point in the box, and
+// every running distance is at most M; a skipped tile therefore has no
+// running distance that the update would lower.
 template <int P, int T>
-__global__ __launch_bounds__(T) void fps_lazy_regs_kernel(const float* __restrict__ xyz,
-                                                          const int64_t* __restrict__ ptr,
-                                                          const int64_t* __restrict__ out_ptr,
-                                                          const int64_t* __restrict__ starts,
-                                                          int64_t* __restrict__ out, int64_t N,
-                                                          int64_t npoint, int64_t start, int skip) {
+__global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ xyz,
+                                                      const int64_t* __restrict__ ptr,
+                                                      const int64_t* __restrict__ out_ptr,
+                                                      const int64_t* __restrict__ starts,
+                                                      int64_t* __restrict__ out, int64_t N,
+                                                      int64_t npoint, int64_t start, int skip) {
     constexpr int NW = T / kWave;
     constexpr int KC = kWave / NW;  // candidates per wave
-    static_assert(KC * NW == kWave && KC + 1 <= kWave, "one candidate per lane");
+    constexpr int CAP = P * T;      // points per cloud at most
+    constexpr int kCells = 4096;
+    static_assert(KC * NW == kWave && KC + 1 <= kWave && P <= 16 && CAP <= 8192, "shape");
+    static_assert(kCells % T == 0, "cells per thread");
+    // The sort's arrays, then (from the load of the tiles on) the points'
+    // coordinates by sorted position, for the exchange's candidates.
+    constexpr int kSortInts = kCells + CAP;
+    constexpr int kBufVec = (kSortInts * 4 > CAP * 16 ? kSortInts * 4 : CAP * 16) / 16;
+    __shared__ float4 buf[kBufVec];
+    int* const cell_count = reinterpret_cast<int*>(buf);  // per-cell counts, then offsets
+    int* const sorted_index = cell_count + kCells;         // sorted position -> local index
+    float4* const spts = buf;                              // sorted position -> xyz
+    __shared__ float red[6][NW];        // bounding-box partials
+    __shared__ int wave_sum[NW];
     __shared__ WaveBest cands[kWave];
     __shared__ int bounds[NW];
 
@@ -135,108 +162,299 @@ __global__ __launch_bounds__(T) void fps_lazy_regs_kernel(const float* __restric
     const int tid = threadIdx.x;
     const int wave = tid / kWave;
     const int lane = tid % kWave;
-
-    constexpr int PA = P <= 8 ? P + 1 : P;  // see fps_lazy_kernel
-    float px[PA], py[PA], pz[PA];
-    float md[P];
-#pragma unroll
-    for (int k = 0; k < PA; ++k) px[k] = py[k] = pz[k] = 0.f;
     const int far0 = static_cast<int>(seg.start);
-    float cx = 0.f, cy = 0.f, cz = 0.f;
-    if (n > 0) {
+    if (tid == 0) o[0] = seg.base + far0;
+    if (seg.cnt == 1 || n <= 0) return;
+
+    // ---- setup: bounding box, cells, counting sort
+    for (int c = tid; c < kCells; c += T) cell_count[c] = 0;
+    float lx[P], ly[P], lz[P];  // points t*P .. t*P+P-1 in index order
 #pragma unroll
-        for (int k = 0; k < P; ++k) {
-            const int jj = min(tid * P + k, n - 1);
-            px[k] = p[3 * jj];
-            py[k] = p[3 * jj + 1];
-            pz[k] = p[3 * jj + 2];
+    for (int k = 0; k < P; ++k) {
+        const int j = min(tid * P + k, n - 1);
+        lx[k] = p[3 * j];
+        ly[k] = p[3 * j + 1];
+        lz[k] = p[3 * j + 2];
+    }
+    {
+        float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int k = 0; k < P; ++k) {  // clamped duplicates do not change the box
+            mn[0] = fminf(mn[0], lx[k]); mx[0] = fmaxf(mx[0], lx[k]);
+            mn[1] = fminf(mn[1], ly[k]); mx[1] = fmaxf(mx[1], ly[k]);
+            mn[2] = fminf(mn[2], lz[k]); mx[2] = fmaxf(mx[2], lz[k]);
         }
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            mn[a] = wave_min(mn[a]);
+            mx[a] = wave_max(mx[a]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                red[a][wave] = mn[a];
+                red[3 + a][wave] = mx[a];
+            }
+        }
+    }
+    __syncthreads();  // box partials and cleared counters
+    float lo[3], scale[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        float mn = red[a][0], mx = red[3 + a][0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            mn = fminf(mn, red[a][w]);
+            mx = fmaxf(mx, red[3 + a][w]);
+        }
+        lo[a] = mn;
+        const float ext = mx - mn;
+        scale[a] = (ext > 0.f && ext < INFINITY) ? 16.f / ext : 0.f;
+    }
+    int cell[P], rank[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const float c3[3] = {lx[k], ly[k], lz[k]};
+        uint32_t key = 0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            // fmaxf/fminf also map NaN to cell 0 and infinities to the edges.
+            const float f = fminf(fmaxf((c3[a] - lo[a]) * scale[a], 0.f), 15.f);
+            const uint32_t q = static_cast<uint32_t>(f);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) key |= ((q >> b) & 1u) << (3 * b + a);
+        }
+        cell[k] = static_cast<int>(key);
+        rank[k] = (tid * P + k < n) ? atomicAdd(&cell_count[key], 1) : 0;
+    }
+    __syncthreads();  // counts complete
+    {
+        constexpr int CPT = kCells / T;  // cells per thread, scanned in place
+        int run = 0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int v = cell_count[tid * CPT + c];
+            cell_count[tid * CPT + c] = run;
+            run += v;
+        }
+        int incl = run;  // inclusive scan of the per-thread totals over the wave
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += up;
+        }
+        if (lane == kWave - 1) wave_sum[wave] = incl;
+        __syncthreads();  // wave totals
+        int before = incl - run;
+        for (int w = 0; w < wave; ++w) before += wave_sum[w];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) cell_count[tid * CPT + c] += before;
+    }
+    __syncthreads();  // offsets complete
+#pragma unroll
+    for (int k = 0; k < P; ++k)
+        if (tid * P + k < n) sorted_index[cell_count[cell[k]] + rank[k]] = tid * P + k;
+    __syncthreads();  // permutation complete
+
+    // ---- this thread's tile points, their indices and running distances
+    constexpr int PA = P <= 8 ? P + 1 : P;  // see fps_lazy_kernel
+    float px[PA], py[PA], pz[PA], md[P];
+    int pcode[PA];  // local index << 13 | sorted position
+#pragma unroll
+    for (int k = 0; k < PA; ++k) {
+        px[k] = py[k] = pz[k] = 0.f;
+        pcode[k] = 0x7FFFFFFF;
+    }
+    float cx, cy, cz;
+    {
         const int f = min(max(far0, 0), n - 1);
         cx = p[3 * f];
         cy = p[3 * f + 1];
         cz = p[3 * f + 2];
     }
+    float blo[3] = {INFINITY, INFINITY, INFINITY}, bhi[3] = {-INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int k = 0; k < P; ++k) {
-        const int j = tid * P + k;
-        const bool valid = j < n;
-        px[k] = valid ? px[k] : 0.f;
-        py[k] = valid ? py[k] : 0.f;
-        pz[k] = valid ? pz[k] : 0.f;
+        const int q = (wave * P + k) * kWave + lane;
+        const bool valid = q < n;
+        const int j = valid ? sorted_index[q] : 0;
+        px[k] = valid ? p[3 * j] : 0.f;
+        py[k] = valid ? p[3 * j + 1] : 0.f;
+        pz[k] = valid ? p[3 * j + 2] : 0.f;
+        pcode[k] = valid ? (j << 13) | q : 0x7FFFFFFF;
         md[k] = !valid ? -INFINITY
                        : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
         md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
+        // Box of tile k (padding excluded), kept in lane k.
+        const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
+        const float tly = wave_min(valid ? py[k] : INFINITY), thy = wave_max(valid ? py[k] : -INFINITY);
+        const float tlz = wave_min(valid ? pz[k] : INFINITY), thz = wave_max(valid ? pz[k] : -INFINITY);
+        if (lane == k) {
+            blo[0] = tlx; bhi[0] = thx;
+            blo[1] = tly; bhi[1] = thy;
+            blo[2] = tlz; bhi[2] = thz;
+        }
     }
-    if (tid == 0) o[0] = seg.base + far0;
+
+    __syncthreads();  // every sorted index has been read
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int q = (wave * P + k) * kWave + lane;
+        if (q < n) spts[q] = make_float4(px[k], py[k], pz[k], 0.f);
+    }
+    __syncthreads();  // coordinates by sorted position
+
+    // ---- lazy steps
+    // Tile updates run one step late (their scalar branches then test a
+    // mask that is already in SGPRs): the centroid and mask of the step
+    // before.  Steps read only the candidates, and every update is applied
+    // before the next exchange reads the points.
+    uint32_t pend = 0;
+    float pfx = 0.f, pfy = 0.f, pfz = 0.f;
+    auto apply_pending = [&]() {
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+            if ((pend >> k) & 1u)
+                md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], pfx, pfy, pfz));
+        pend = 0;
+    };
     int64_t step = 1;
     while (step < seg.cnt) {
-        // Exchange: this wave's KC best points and its bound.  av[] holds
-        // the running distances not yet taken (taken ones read INT_MIN).
-        int av[PA];
+        // Exchange: this wave's KC best points (largest running distance,
+        // then smallest index) and its bound, the (KC+1)-th.  Keys pack
+        // (running distance bits ^ sign, ~code) into 64 bits, so one
+        // unsigned compare orders them; each lane keeps its two largest keys
+        // below `lim` (the last key it published) and rescans its slots only
+        // when it publishes a second time in one exchange.  Candidate r
+        // collects in lane r; its coordinates are read from LDS afterwards.
+        uint64_t lim = ~uint64_t(0), h1 = 0, h2 = 0;  // 0: no key; 1: not yet known
+        auto rescan = [&]() {
+            h1 = 0;
+            h2 = 0;
 #pragma unroll
-        for (int k = 0; k < PA; ++k) av[k] = k < P ? f2i(md[k]) : static_cast<int>(0x80000000u);
+            for (int k = 0; k < P; ++k) {
+                const uint64_t key =
+                    (static_cast<uint64_t>(static_cast<uint32_t>(f2i(md[k])) ^ 0x80000000u) << 32) |
+                    static_cast<uint32_t>(~pcode[k]);
+                const bool below = key < lim;
+                const bool first = below && key > h1;
+                const bool second = below && !first && key > h2;
+                h2 = first ? h1 : (second ? key : h2);
+                h1 = first ? key : h1;
+            }
+        };
+        rescan();
+        int ck = 0, cc = 0x7FFFFFFF;
         int bound = 0;
 #pragma unroll
         for (int r = 0; r <= KC; ++r) {
-            int lm = av[0];
-#pragma unroll
-            for (int k = 1; k < P; ++k) lm = max(lm, av[k]);
-            int ls = P - 1;
-#pragma unroll
-            for (int k = P - 2; k >= 0; --k) ls = av[k] == lm ? k : ls;
-            const int wv = wave_max_i32_l63(lm);
-            const int wl = static_cast<int>(__builtin_ctzll(ballot(lm == wv)));
-            const int os = readlane(ls, wl);
+            const uint32_t hh = static_cast<uint32_t>(h1 >> 32);
+            const uint32_t wv = wave_max_u32_l63(hh);
+            const uint64_t at = ballot(hh == wv);
+            int wl = static_cast<int>(__builtin_ctzll(at));
+            if (__popcll(at) > 1) {  // equal distances: the largest ~code (smallest index)
+                const uint32_t wlo = wave_max_u32_l63(hh == wv ? static_cast<uint32_t>(h1) : 0u);
+                wl = static_cast<int>(__builtin_ctzll(ballot(hh == wv && static_cast<uint32_t>(h1) == wlo)));
+            }
             if (r == KC) {
-                bound = wv;
+                bound = static_cast<int>(wv ^ 0x80000000u);
                 break;
             }
-            const float bx = i2f(readlane(f2i(px[os]), wl));
-            const float by = i2f(readlane(f2i(py[os]), wl));
-            const float bz = i2f(readlane(f2i(pz[os]), wl));
-            if (lane == 0) {
-                WaveBest e;
-                e.key = wv;
-                e.index = (wave * kWave + wl) * P + os;
-                e.x = bx;
-                e.y = by;
-                e.z = bz;
-                e.pad[0] = e.pad[1] = e.pad[2] = 0;
-                cands[wave * KC + r] = e;
+            const int code = static_cast<int>(~static_cast<uint32_t>(readlane(static_cast<int>(h1), wl)));
+            ck = lane == r ? static_cast<int>(wv ^ 0x80000000u) : ck;
+            cc = lane == r ? code : cc;
+            // The winner's next key is its second (known) or needs a rescan
+            // below the key just published.
+            const bool popped = lane == wl;
+            const bool again = readlane(static_cast<int>(h2), wl) == 1 && readlane(static_cast<int>(h2 >> 32), wl) == 0;
+            lim = popped ? h1 : lim;
+            if (again) {
+                const uint64_t keep1 = h1, keep2 = h2;
+                rescan();
+                h1 = popped ? h1 : keep1;
+                h2 = popped ? h2 : keep2;
+            } else {
+                h1 = popped ? h2 : h1;
+                h2 = popped ? uint64_t(1) : h2;
             }
-            av[os] = lane == wl ? static_cast<int>(0x80000000u) : av[os];
+        }
+        if (lane < KC) {
+            // Padding codes 0x7FFFFFFF: a published padding key never wins a
+            // step, so any in-range position serves.
+            const float4 c = spts[min(cc & 0x1FFF, CAP - 1)];
+            WaveBest e;
+            e.key = ck;
+            e.index = cc >> 13;
+            e.x = c.x;
+            e.y = c.y;
+            e.z = c.z;
+            e.pad[0] = e.pad[1] = e.pad[2] = 0;
+            cands[wave * KC + lane] = e;
         }
         if (lane == 0) bounds[wave] = bound;
         __syncthreads();
         const WaveBest mine = cands[lane];
-        int maxb = bounds[0];
+        int maxb_v = bounds[0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) maxb = max(maxb, bounds[w]);
+        for (int w = 1; w < NW; ++w) maxb_v = max(maxb_v, bounds[w]);
         __syncthreads();  // every wave has read the candidates before any rewrites them
         int cmd = mine.key;
         const int cidx = mine.index;
         const float ccx = mine.x, ccy = mine.y, ccz = mine.z;
-        for (bool first = true; step < seg.cnt; first = false) {
-            const int wv = wave_max_i32_l63(cmd);
-            if (!first && !(wv > maxb)) break;  // an unpublished point may tie or beat it
-            // Ties (rare) go to the smallest index, whatever lane holds it.
+        // A later step of the run needs a key above every bound and above 0.
+        // A taken candidate's key becomes its distance to itself, 0 -- or
+        // stays +inf/-inf when a coordinate is not finite (the distance is
+        // NaN) -- so with finite candidates none is taken twice in one run;
+        // a non-finite candidate limits runs to one step.
+        const bool odd = !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
+        const int maxb = ballot(odd) ? INT_MAX : max(uniform(maxb_v), 0);
+        // Steps of this run: at most `left`, counted in 32 bits.
+        const int left = static_cast<int>(min<int64_t>(seg.cnt - step, int64_t(1) << 30));
+        int taken = 0;
+        // Step of this run at which each candidate was taken (-1: not
+        // taken; at most once, see maxb); wave 0 stores the run's samples
+        // after it.
+        int when = -1;
+        // One step with chosen key wv: the candidate holding it (smallest
+        // index on a tie), its step recorded, the candidates updated, and
+        // the tiles it may change queued for the next step.
+        auto take = [&](int wv) {
             const uint64_t at_max = ballot(cmd == wv);
             int wl = static_cast<int>(__builtin_ctzll(at_max));
-            if (__popcll(at_max) > 1) {
+            if (__popcll(at_max) > 1) {  // ties (rare): the smallest index
                 const int wneg = wave_max_i32_l63(cmd == wv ? -cidx : static_cast<int>(0x80000000u));
                 wl = static_cast<int>(__builtin_ctzll(ballot(cmd == wv && -cidx == wneg)));
             }
-            const int fidx = readlane(cidx, wl);
             const float fx = i2f(readlane(f2i(ccx), wl));
             const float fy = i2f(readlane(f2i(ccy), wl));
             const float fz = i2f(readlane(f2i(ccz), wl));
-            if (tid == 0) o[step] = seg.base + fidx;
-            ++step;
-#pragma unroll
-            for (int k = 0; k < P; ++k)
-                md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], fx, fy, fz));
             cmd = f2i(running_min(i2f(cmd), sqdist3(ccx, ccy, ccz, fx, fy, fz)));
+            when = lane == wl ? taken : when;
+            // Tiles whose box may hold a point nearer to the centroid than
+            // the chosen (largest) running distance.
+            const float M = i2f(wv);
+            const float gx = fmaxf(fmaxf(blo[0] - fx, fx - bhi[0]), 0.f);
+            const float gy = fmaxf(fmaxf(blo[1] - fy, fy - bhi[1]), 0.f);
+            const float gz = fmaxf(fmaxf(blo[2] - fz, fz - bhi[2]), 0.f);
+            float lb = gx * gx;
+            lb = lb + gy * gy;
+            lb = lb + gz * gz;
+            pend = static_cast<uint32_t>(ballot(lb < M));
+            pfx = fx;
+            pfy = fy;
+            pfz = fz;
+            ++taken;
+        };
+        take(wave_max_i32_l63(cmd));  // the first step after an exchange is exact
+        while (taken < left) {
+            const int wv = wave_max_i32_l63(cmd);
+            if (pend) apply_pending();
+            if (!(wv > maxb)) break;  // an unpublished point may tie or beat it
+            take(wv);
         }
+        if (pend) apply_pending();
+        if (wave == 0 && when >= 0) o[step + when] = seg.base + cidx;
+        step += taken;
     }
 }
 
@@ -594,7 +812,7 @@ template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream) {
-    hipLaunchKernelGGL((fps_lazy_regs_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
+    hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
                        dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
                        start, skip);
     return hipGetLastError();

@@ -122,6 +122,25 @@ __device__ __forceinline__ int wave_max_i32_l63(int v) {
     return readlane(v, 63);
 }
 
+// DPP move whose unwritten lanes read 0, the identity of unsigned max.
+template <int CTRL, int ROW_MASK = 0xF>
+__device__ __forceinline__ uint32_t dpp_or_zero(uint32_t v) {
+    return static_cast<uint32_t>(
+        __builtin_amdgcn_update_dpp(0, static_cast<int>(v), CTRL, ROW_MASK, 0xF, false));
+}
+
+// Maximum over the wave of an unsigned int, as a wave-uniform value (the
+// row_bcast scheme of wave_max_i32_l63).
+__device__ __forceinline__ uint32_t wave_max_u32_l63(uint32_t v) {
+    v = max(v, dpp_or_zero<kDppQuadXor1>(v));
+    v = max(v, dpp_or_zero<kDppQuadXor2>(v));
+    v = max(v, dpp_or_zero<kDppRowHalfMirror>(v));
+    v = max(v, dpp_or_zero<kDppRowMirror>(v));
+    v = max(v, dpp_or_zero<0x142, 0xA>(v));  // row_bcast:15 into rows 1 and 3
+    v = max(v, dpp_or_zero<0x143, 0xC>(v));  // row_bcast:31 into rows 2 and 3
+    return static_cast<uint32_t>(readlane(static_cast<int>(v), 63));
+}
+
 // Maximum over each aligned group of 8 lanes, read from lane 0.
 __device__ __forceinline__ int group8_max_i32(int v) {
     v = max(v, dpp_or_lowest<kDppQuadXor1>(v));
