@@ -114,6 +114,19 @@ hipError_t pointops_nearest3_grid(const float *query, const float *ref, float *d
                                   int64_t *idx, void *workspace, int64_t B, int64_t M, int64_t N,
                                   hipStream_t stream);
 
+/* The same search (identical results) for clouds of 1 <= N <= 8192
+ * references, M <= 16384 queries and 1 <= K <= 32, faster: one workgroup per
+ * cloud counting-sorts the references by Morton cell into `workspace`
+ * (pointops_knn3_windowed_workspace_bytes(B, M, N) bytes, no initialisation
+ * needed), and each query starts from a limit taken from the references
+ * around its own cell in that order, so that only references at least that
+ * near are buffered and merged.  Replaces ops.py:195-199
+ * (kernels/knn.metal:32-140), like pointops_knn3. */
+size_t pointops_knn3_windowed_workspace_bytes(int64_t B, int64_t M, int64_t N);
+hipError_t pointops_knn3_windowed(const float *query, const float *ref, float *dist, int64_t *idx,
+                                  void *workspace, int64_t B, int64_t M, int64_t N, int64_t K,
+                                  hipStream_t stream);
+
 /* Dense exact kNN in D dimensions (sequential per-dimension accumulation).
  * Replaces ops.py:200-204 (kernels/feature_knn.metal:133-164).  Non-finite
  * queries and non-finite distances never match; unfilled slots are (inf, -1). */

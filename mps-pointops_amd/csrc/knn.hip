@@ -1,7 +1,9 @@
 // Exact k-nearest-neighbour search for gfx950.
 //
 // Two designs.  Dense 3-D queries with K <= 32 use knn3_lane_kernel (one lane
-// per query, described with the kernel below).  Everything else (K up to 256,
+// per query, described with the kernel below; for clouds of up to 8192
+// references it can start from a per-query limit taken from the query's
+// Morton neighbours, see knn_window_prep_kernel).  Everything else (K up to 256,
 // D != 3, flat/ragged batches) uses the wave-per-query kernels:
 //
 // One wave per query.  Lane l scans reference j = 64*c + l of chunk c; the
@@ -343,12 +345,181 @@ __device__ __forceinline__ void lane_publish_and_merge(
     }
 }
 
+// ------------------------------------------------------------------------
+// Starting limit from Morton neighbours (clouds of up to 8192 references).
+//
+// knn_window_prep_kernel (one workgroup per cloud) counting-sorts the
+// references by a 16 x 16 x 16 Morton cell of the finite references'
+// bounding box and writes their coordinates in that order, and gives every
+// query a "home": the middle of its cell's range in the sorted order (or where
+// the cell would start).  knn3_lane_kernel then takes, per query, the window
+// of r*K sorted references around its home (r = min(8, N/K)) in K strided
+// groups {w0 + g + j*K : j < r} and the largest of the K group minima: every
+// group holds a reference at or below it, so at least K references are, and
+// the query's K-th neighbour is no further.  Only references with keys at or
+// below it are admitted from the start, which spares most of the list merging
+// that a full list would otherwise cost before it tightens.
+constexpr int kWindowPrepThreads = 1024;
+constexpr int kWindowMaxRefs = 8192;
+constexpr int kWindowMaxQueries = 16384;
+constexpr int kWindowCells = 4096;  // 16^3 Morton cells
+constexpr int kWindowGroups = 8;    // window references per group (r <= 8)
+
+struct WindowLayout {
+    float4* sorted;  // [B][N]: coordinates in Morton order (w unused)
+    int* home;       // [B][M]: per query row, a position in the sorted order
+};
+
+__host__ __device__ inline size_t window_layout_bytes(int64_t B, int64_t M, int64_t N,
+                                                      WindowLayout* out, char* base) {
+    const size_t sorted_bytes = (static_cast<size_t>(B * N) * sizeof(float4) + 255) & ~size_t(255);
+    if (out != nullptr) {
+        out->sorted = reinterpret_cast<float4*>(base);
+        out->home = reinterpret_cast<int*>(base + sorted_bytes);
+    }
+    return sorted_bytes + static_cast<size_t>(B * M) * sizeof(int);
+}
+
+__device__ __forceinline__ uint32_t window_cell(float x, float y, float z, const float (&lo)[3],
+                                                const float (&scale)[3]) {
+    const float c3[3] = {x, y, z};
+    uint32_t key = 0;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        // fmaxf/fminf map NaN to cell 0 and infinities to the edge cells.
+        const float f = fminf(fmaxf((c3[a] - lo[a]) * scale[a], 0.f), 15.f);
+        const uint32_t q = static_cast<uint32_t>(f);
+#pragma unroll
+        for (int bit = 0; bit < 4; ++bit) key |= ((q >> bit) & 1u) << (3 * bit + a);
+    }
+    return key;
+}
+
+__global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
+    const float* __restrict__ query, const float* __restrict__ ref, WindowLayout L, int M, int N) {
+    constexpr int RPT = kWindowMaxRefs / kWindowPrepThreads;
+    constexpr int QPT = kWindowMaxQueries / kWindowPrepThreads;
+    constexpr int CPT = kWindowCells / kWindowPrepThreads;  // cells per thread in the scan
+    constexpr int NWV = kWindowPrepThreads / kWave;
+    __shared__ int cell_off[kWindowCells + 1];
+    __shared__ float red[6][NWV];
+    __shared__ int wave_sum[NWV];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave, wave = tid / kWave;
+    const int64_t b = blockIdx.x;
+    const float* rp = ref + 3 * b * N;
+    const float* qp = query + 3 * b * M;
+
+    for (int c = tid; c <= kWindowCells; c += kWindowPrepThreads) cell_off[c] = 0;
+    // References and queries are requested together, without branches (an
+    // index past the end reads the last point again), so that every load is
+    // in flight before the first wait.
+    float px[RPT], py[RPT], pz[RPT], qx[QPT], qy[QPT], qz[QPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = min(tid + k * kWindowPrepThreads, N - 1);
+        px[k] = rp[3 * j];
+        py[k] = rp[3 * j + 1];
+        pz[k] = rp[3 * j + 2];
+    }
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int m = min(tid + k * kWindowPrepThreads, M - 1);
+        qx[k] = qp[3 * m];
+        qy[k] = qp[3 * m + 1];
+        qz[k] = qp[3 * m + 2];
+    }
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = tid + k * kWindowPrepThreads;
+        if (j < N && isfinite(px[k]) && isfinite(py[k]) && isfinite(pz[k])) {
+            mn[0] = fminf(mn[0], px[k]); mx[0] = fmaxf(mx[0], px[k]);
+            mn[1] = fminf(mn[1], py[k]); mx[1] = fmaxf(mx[1], py[k]);
+            mn[2] = fminf(mn[2], pz[k]); mx[2] = fmaxf(mx[2], pz[k]);
+        }
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        mn[a] = wave_min(mn[a]);
+        mx[a] = wave_max(mx[a]);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            red[a][wave] = mn[a];
+            red[3 + a][wave] = mx[a];
+        }
+    }
+    __syncthreads();  // box partials and cleared counters
+    float lo[3], scale[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        float l = red[a][0], h = red[3 + a][0];
+        for (int w = 1; w < NWV; ++w) {
+            l = fminf(l, red[a][w]);
+            h = fmaxf(h, red[3 + a][w]);
+        }
+        const float ext = h - l;  // no finite reference: -inf - inf, not >= 0
+        lo[a] = ext >= 0.f ? l : 0.f;
+        scale[a] = (ext > 0.f && ext < INFINITY) ? 16.f / ext : 0.f;
+    }
+    int cell[RPT], rank[RPT];
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = tid + k * kWindowPrepThreads;
+        cell[k] = static_cast<int>(window_cell(px[k], py[k], pz[k], lo, scale));
+        rank[k] = j < N ? atomicAdd(&cell_off[cell[k]], 1) : 0;
+    }
+    __syncthreads();  // counts complete
+    {
+        int run = 0;
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) {
+            const int v = cell_off[tid * CPT + c];
+            cell_off[tid * CPT + c] = run;
+            run += v;
+        }
+        int incl = run;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += up;
+        }
+        if (lane == kWave - 1) wave_sum[wave] = incl;
+        __syncthreads();  // wave totals
+        int before = incl - run;
+        for (int w = 0; w < wave; ++w) before += wave_sum[w];
+#pragma unroll
+        for (int c = 0; c < CPT; ++c) cell_off[tid * CPT + c] += before;
+        if (tid == kWindowPrepThreads - 1) cell_off[kWindowCells] = before + run;
+    }
+    __syncthreads();  // offsets complete
+    float4* sorted = L.sorted + b * N;
+#pragma unroll
+    for (int k = 0; k < RPT; ++k) {
+        const int j = tid + k * kWindowPrepThreads;
+        if (j < N) sorted[cell_off[cell[k]] + rank[k]] = make_float4(px[k], py[k], pz[k], 0.f);
+    }
+    int* home = L.home + b * M;
+#pragma unroll
+    for (int k = 0; k < QPT; ++k) {
+        const int m = tid + k * kWindowPrepThreads;
+        if (m < M) {
+            const int c = static_cast<int>(window_cell(qx[k], qy[k], qz[k], lo, scale));
+            home[m] = min((cell_off[c] + cell_off[c + 1]) / 2, N - 1);
+        }
+    }
+}
+
 template <int KMAX, int NW, int CAP>
 __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
-    int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
+    int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K, const float4* __restrict__ sorted,
+    const int* __restrict__ home) {
     // Per wave: the candidate buffer during the scan, then the final list.
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
+    __shared__ uint32_t window_max[kWave];  // per lane: the Morton-window limit
     // Per lane and wave: the key of the wave's K-th entry, read by the other
     // waves (one lane's NW keys are contiguous: two 16-byte reads).
     constexpr int kTauRows = (NW + 3) / 4;
@@ -377,7 +548,35 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     uint32_t tau = active ? kEmptyKey : 0u;  // inactive lanes admit nothing
     uint32_t* my_tau = reinterpret_cast<uint32_t*>(&taus[lane][0]) + wave;
     *my_tau = tau;
+    if (wave == 0) window_max[lane] = 0;
     __syncthreads();
+    // Keys at or below the Morton-window limit (sorted != nullptr: set up by
+    // knn_window_prep_kernel for this launch) are admitted from the start;
+    // wave w takes the groups g = w mod NW.  Keys compare as unsigned: NaN
+    // patterns are above +inf, and then nothing is excluded.
+    uint32_t bound = kEmptyKey;
+    if (sorted != nullptr) {
+        const float4* sp = sorted + b * N;
+        const int n = static_cast<int>(N);
+        const int r = min(kWindowGroups, n / K);
+        const int h = active ? home[b * M + m] : 0;
+        const int w0 = min(max(h - r * K / 2, 0), n - r * K);
+        uint32_t wmax = 0;
+        for (int g = wave; g < K; g += NW) {
+            float4 v[kWindowGroups];
+#pragma unroll
+            for (int j = 0; j < kWindowGroups; ++j) v[j] = sp[w0 + g + min(j, r - 1) * K];
+            uint32_t gmin = 0xFFFFFFFFu;
+#pragma unroll
+            for (int j = 0; j < kWindowGroups; ++j)
+                gmin = min(gmin, static_cast<uint32_t>(f2i(sqdist3(v[j].x, v[j].y, v[j].z, qx, qy, qz))));
+            wmax = max(wmax, gmin);
+        }
+        if (wmax != 0) atomicMax(&window_max[lane], wmax);
+        __syncthreads();
+        const uint32_t wm = window_max[lane];
+        bound = wm < kEmptyKey ? wm + 1 : kEmptyKey;  // key < bound <=> key <= wm
+    }
     // Admission limit: this wave's K-th key and the other waves' K-th keys
     // (read without synchronisation: they only decrease, so a stale value is
     // a looser but still valid limit; this wave's own published key is never
@@ -394,13 +593,13 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
             t[4 * v + 2] = q4.z;
             t[4 * v + 3] = q4.w;
         }
-        uint32_t lim = tau;
+        uint32_t lim = min(tau, bound);
 #pragma unroll
         for (int w = 0; w < NW; ++w) lim = min(lim, t[w] + static_cast<uint32_t>(w > wave));
         return lim;
     };
     int cnt = 0;
-    uint32_t lim = tau;
+    uint32_t lim = min(tau, bound);
     auto visit = [&](float rx, float ry, float rz, int j) {
         const uint32_t key = static_cast<uint32_t>(f2i(sqdist3(rx, ry, rz, qx, qy, qz)));
         if (key < lim) {  // rare once the lists fill: the masked store is skipped
@@ -592,14 +791,16 @@ hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, i
 
 template <int KMAX>
 hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
-                       int64_t M, int64_t N, int K, hipStream_t stream) {
+                       int64_t M, int64_t N, int K, hipStream_t stream,
+                       const WindowLayout* window = nullptr) {
     const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave * B));  // cloud_block order
     // Small lists: 8 waves per 64 queries (more waves in flight, 16-entry
     // buffers); K up to 32: 4 waves with 32-entry buffers.
     constexpr int NW = KMAX <= 16 ? 8 : 4;
     constexpr int CAP = KMAX <= 16 ? 16 : 32;
     hipLaunchKernelGGL((knn3_lane_kernel<KMAX, NW, CAP>), grid, dim3(NW * kWave), 0, stream, query,
-                       ref, dist, idx, M, N, K);
+                       ref, dist, idx, M, N, K, window ? window->sorted : nullptr,
+                       window ? window->home : nullptr);
     return hipGetLastError();
 }
 
@@ -665,6 +866,32 @@ hipError_t pointops_knn3(const float* query, const float* ref, float* dist, int6
     if (B == 0 || M == 0 || K == 0) return hipSuccess;
     if (N > INT32_MAX - kWave || !grid_ok(B * M)) return hipErrorInvalidValue;
     return launch_dense<true>(query, ref, dist, idx, B, M, N, 3, static_cast<int>(K), stream);
+}
+
+size_t pointops_knn3_windowed_workspace_bytes(int64_t B, int64_t M, int64_t N) {
+    if (B <= 0 || M <= 0 || N <= 0) return 0;
+    return window_layout_bytes(B, M, N, nullptr, nullptr);
+}
+
+hipError_t pointops_knn3_windowed(const float* query, const float* ref, float* dist, int64_t* idx,
+                                  void* workspace, int64_t B, int64_t M, int64_t N, int64_t K,
+                                  hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0 || K < 0 || K > 32 || K > N) return hipErrorInvalidValue;
+    if (B == 0 || M == 0 || K == 0) return hipSuccess;
+    if (N > kWindowMaxRefs || M > kWindowMaxQueries || workspace == nullptr || B > INT32_MAX ||
+        (M + kWave - 1) / kWave * B > INT32_MAX)
+        return hipErrorInvalidValue;
+    WindowLayout L;
+    window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
+    hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
+                       dim3(kWindowPrepThreads), 0, stream, query, ref, L, static_cast<int>(M),
+                       static_cast<int>(N));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int k = static_cast<int>(K);
+    if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, k, stream, &L);
+    if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, k, stream, &L);
+    return launch_lane<32>(query, ref, dist, idx, B, M, N, k, stream, &L);
 }
 
 hipError_t pointops_knn_feat(const float* query, const float* ref, float* dist, int64_t* idx,

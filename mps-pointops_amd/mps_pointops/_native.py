@@ -35,6 +35,7 @@ _SIGNATURES: dict[str, list] = {
     "pointops_fps_flat": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_knn3": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_knn3_grid": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
+    "pointops_knn3_windowed": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_knn_feat": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
     "pointops_knn_flat": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_ball_query_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
@@ -60,6 +61,7 @@ _SIZE_QUERIES: dict[str, list] = {
     "pointops_fps_large_workspace_bytes": [_i64, _i64],
     "pointops_fps_flat_scratch_bytes": [_i64, _i64],
     "pointops_knn3_grid_workspace_bytes": [_i64, _i64, _i64],
+    "pointops_knn3_windowed_workspace_bytes": [_i64, _i64, _i64],
     "pointops_ball_query_grid_workspace_bytes": [_i64, _i64, _i64],
     "pointops_cloud_bounds_workspace_bytes": [_i64],
     "pointops_group_points_backward_workspace_bytes": [_i64, _i64, _i64, _i64],

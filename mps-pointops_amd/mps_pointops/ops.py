@@ -31,6 +31,15 @@ _KNN_MAX_K = 256
 _KNN_GRID_MAX_K = 32
 _KNN_GRID_MIN_N = 32_768
 _KNN_GRID_MIN_PAIRS = 1 << 26
+# 3-D kNN with at most 32 neighbours over clouds of 2048 to 8192 references
+# (and at most 16384 queries per cloud) first sorts each cloud by Morton cell
+# and starts every query from a limit set by its neighbours in that order
+# (pointops_knn3_windowed): same results, about 15% faster at config 2's
+# shape; below 2048 references the extra launch does not pay.
+_KNN_WINDOW_MAX_K = 32
+_KNN_WINDOW_MIN_N = 2048
+_KNN_WINDOW_MAX_N = 8192
+_KNN_WINDOW_MAX_M = 16384
 
 
 def _check_large_status(workspace: Tensor) -> None:
@@ -155,6 +164,12 @@ def knn(query: Tensor, ref: Tensor, k: int) -> tuple[Tensor, Tensor]:
         size = _native.size_query("pointops_knn3_grid_workspace_bytes", B, M, N)
         workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
         _native.call("pointops_knn3_grid", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
+                     idx.data_ptr(), workspace.data_ptr(), B, M, N, k, stream)
+    elif (D == 3 and k <= _KNN_WINDOW_MAX_K and _KNN_WINDOW_MIN_N <= N <= _KNN_WINDOW_MAX_N
+          and M <= _KNN_WINDOW_MAX_M):
+        size = _native.size_query("pointops_knn3_windowed_workspace_bytes", B, M, N)
+        workspace = torch.empty(size, dtype=torch.uint8, device=query.device)
+        _native.call("pointops_knn3_windowed", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
                      idx.data_ptr(), workspace.data_ptr(), B, M, N, k, stream)
     elif D == 3:
         _native.call("pointops_knn3", query.data_ptr(), ref.data_ptr(), dist.data_ptr(),
