@@ -479,12 +479,18 @@ def run_other(args) -> dict:
 
 
 def probe() -> None:
-    """One pass of each config-2 kernel plus a 256 MiB device copy, for
-    hardware-counter runs (the copy's FETCH_SIZE/WRITE_SIZE give the scale of
-    the counters against known bytes)."""
+    """One pass of each config-2 kernel (the metric's FPS, ball queries and
+    kNN, then three_nn and three_interpolate forward and backward of C=128
+    features) plus a 256 MiB device copy, three times, for hardware-counter
+    runs (the copy's FETCH_SIZE/WRITE_SIZE give the scale of the counters
+    against known bytes)."""
     import mps_pointops as mp
 
     xyz = make_c2().cuda()
+    B, N, _ = xyz.shape
+    g = torch.Generator().manual_seed(9)
+    feats = torch.randn(B, 128, C2_NPOINT, generator=g).cuda().requires_grad_()
+    upstream = torch.randn(B, 128, N, generator=g).cuda()
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -493,9 +499,15 @@ def probe() -> None:
         for radius, k in C2_RADII:
             mp.ball_query(centres, xyz, radius, k)
         mp.knn(centres, xyz, C2_KNN_K)
+        tn_d, tn_i = mp.three_nn(xyz, centres)
+        inv = 1.0 / (tn_d + 1e-8)
+        w = (inv / inv.sum(-1, keepdim=True)).contiguous()
+        feats.grad = None
+        mp.three_interpolate(feats, tn_i, w).backward(upstream)
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("probe: 3 x (fps, 3 ball queries, knn, 256 MiB copy) done", flush=True)
+    print("probe: 3 x (fps, 3 ball queries, knn, three_nn, three_interpolate fwd+bwd, "
+          "256 MiB copy) done", flush=True)
 
 
 def main() -> None:

@@ -217,6 +217,19 @@ hipError_t pointops_three_interpolate_backward(const float *grad_out, const int3
                                                const float *weights, float *grad_features,
                                                int64_t B, int64_t C, int64_t M, int64_t N,
                                                hipStream_t stream);
+/* The same gradient, always in (n, t) order (deterministic), for M <= 4096
+ * known points and N <= 4096 unknowns with N % 4 == 0 (grad_out 16-byte
+ * aligned), without atomics: a CSR of the entries by known index is built in
+ * `workspace` (256-byte aligned,
+ * pointops_three_interpolate_backward_workspace_bytes(B, M, N) bytes, no
+ * initialisation needed), then every element of grad_features is written
+ * once (it need not be zero-filled).  Indices outside [0, M) contribute
+ * nothing.  Replaces pointnet2.py:179-186 (kernels/pointnet2.metal:85-103). */
+size_t pointops_three_interpolate_backward_workspace_bytes(int64_t B, int64_t M, int64_t N);
+hipError_t pointops_three_interpolate_backward_csr(const float *grad_out, const int32_t *idx,
+                                                   const float *weights, float *grad_features,
+                                                   void *workspace, int64_t B, int64_t C,
+                                                   int64_t M, int64_t N, hipStream_t stream);
 
 /* --------------------------------------------------- PointNet++ grouping */
 

@@ -369,6 +369,351 @@ __global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_g
     }
 }
 
+// Backward over a CSR of the entries, for M <= 4096 known points and
+// N <= 4096 unknowns (N a multiple of 4), with a caller workspace:
+//   three_interp_csr_kernel (one workgroup per batch): counting sort of the
+//   entry ids e = 3n + t by known index m = idx[b,n,t] in LDS; an entry's
+//   place in its bucket is the number of smaller ids there, so each bucket
+//   lists its entries in ascending order; the sorted ids and the bucket
+//   starts are copied out with coalesced stores.
+//   three_interp_backward_csr_kernel (one workgroup per batch and block of
+//   kTiCsrBlock channels): stages the batch's CSR once (ids, starts and each
+//   entry's weight, gathered by id), then walks its channels CG at a time
+//   with the CG rows of grad_out double-buffered in LDS (the next rows' loads
+//   are in flight while the current ones are summed).  Thread m sums
+//   grad_out[c, e/3] * w over its list in order -- the order of a sequential
+//   scatter loop into a zero-filled array, so the result is deterministic --
+//   and writes every element once (zero for a known point no entry selects).
+//   No atomics on the gradients.
+constexpr int kTiCsrThreads = 1024;
+constexpr int kTiCsrMaxM = 4096;
+constexpr int kTiCsrMaxN = 4096;
+constexpr int kTiCsrEntriesPerThread = 3 * kTiCsrMaxN / kTiCsrThreads;
+constexpr int kTiCsrBlock = 16;                    // channels per gather workgroup
+constexpr int kTiCsrLdsBytes = 160 * 1024 - 1024;  // gather LDS budget
+constexpr int kTiCsrStage = 8;                     // 16-byte chunks a thread stages at once
+constexpr int kTiCsrRegEntries = 16;               // list entries a gather thread keeps in registers
+
+// Per batch, each array is padded to whole 16-byte chunks, so that a batch's
+// part starts 16-byte aligned.
+struct TiCsr {
+    int* start;      // [B][sstride]: bucket starts, M+1 used
+    float* weight;   // [B][wstride]: w[e] in list order, 3N used
+    uint16_t* list;  // [B][lstride]: entry ids by known index, ascending, 3N used
+    int sstride, wstride, lstride;
+};
+
+__host__ __device__ inline size_t ti_csr_bytes(int64_t B, int64_t M, int64_t N, TiCsr* out,
+                                               char* base) {
+    auto up = [](size_t v) { return (v + 255) & ~size_t(255); };
+    const int64_t ss = (M + 1 + 3) & ~int64_t(3), ws = (3 * N + 3) & ~int64_t(3),
+                  ls = (3 * N + 7) & ~int64_t(7);
+    const size_t start_bytes = up(static_cast<size_t>(B * ss) * sizeof(int));
+    const size_t weight_bytes = up(static_cast<size_t>(B * ws) * sizeof(float));
+    if (out != nullptr) {
+        out->start = reinterpret_cast<int*>(base);
+        out->weight = reinterpret_cast<float*>(base + start_bytes);
+        out->list = reinterpret_cast<uint16_t*>(base + start_bytes + weight_bytes);
+        out->sstride = static_cast<int>(ss);
+        out->wstride = static_cast<int>(ws);
+        out->lstride = static_cast<int>(ls);
+    }
+    return start_bytes + weight_bytes + static_cast<size_t>(B * ls) * sizeof(uint16_t);
+}
+
+__global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
+    const int32_t* __restrict__ idx, const float* __restrict__ weights, TiCsr csr, int M, int N) {
+    constexpr int T = kTiCsrThreads;
+    constexpr int EPT = kTiCsrEntriesPerThread;
+    constexpr int MPT = kTiCsrMaxM / T;  // buckets per thread in the scan
+    __shared__ int cursor[kTiCsrMaxM];
+    __shared__ __align__(16) uint16_t list[3 * kTiCsrMaxN];  // by bucket, unordered within one
+    __shared__ uint16_t sorted[3 * kTiCsrMaxN];  // by bucket, ascending within one
+    __shared__ int wave_sum[T / kWave];
+    const int tid = threadIdx.x;
+    const int lane = tid % kWave, wave = tid / kWave;
+    const int64_t b = blockIdx.x;
+    const int e_count = 3 * N;
+    const int32_t* ib = idx + b * e_count;
+    // This thread's entries e = tid + k*T, all requested before the first
+    // use.  Indices outside [0, M) (callers validate them) become -1 and
+    // contribute nothing.
+    int em[EPT];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) em[k] = ib[min(tid + k * T, e_count - 1)];
+#pragma unroll
+    for (int k = 0; k < EPT; ++k)
+        if (tid + k * T >= e_count || static_cast<unsigned>(em[k]) >= static_cast<unsigned>(M))
+            em[k] = -1;
+    for (int m = tid; m < kTiCsrMaxM; m += T) cursor[m] = 0;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < EPT; ++k)
+        if (em[k] >= 0) atomicAdd(&cursor[em[k]], 1);
+    __syncthreads();
+    // Exclusive scan of the counts: MPT consecutive buckets per thread.
+    int run = 0;
+#pragma unroll
+    for (int k = 0; k < MPT; ++k) {
+        const int v = cursor[tid * MPT + k];
+        cursor[tid * MPT + k] = run;
+        run += v;
+    }
+    int incl = run;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) {
+        const int up = __shfl_up(incl, d, kWave);
+        if (lane >= d) incl += up;
+    }
+    if (lane == kWave - 1) wave_sum[wave] = incl;
+    __syncthreads();
+    int before = incl - run;
+    for (int w = 0; w < wave; ++w) before += wave_sum[w];
+    int* start = csr.start + b * csr.sstride;
+#pragma unroll
+    for (int k = 0; k < MPT; ++k) {
+        const int m = tid * MPT + k;
+        cursor[m] += before;
+        if (m < M) start[m] = cursor[m];
+    }
+    if (tid == T - 1) start[M] = before + run;
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < EPT; ++k)
+        if (em[k] >= 0) list[atomicAdd(&cursor[em[k]], 1)] = static_cast<uint16_t>(tid + k * T);
+    __syncthreads();
+    // cursor[m] is now the end of bucket m and its start the previous end.
+    // Entry ids are distinct, so an entry's place in its bucket is the count
+    // of smaller ids there.
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        if (em[k] < 0) continue;
+        const int e = tid + k * T;
+        const int m = em[k];
+        const int p0 = m == 0 ? 0 : cursor[m - 1], p1 = cursor[m];
+        int rank = 0;
+        // Eight ids per 16-byte read, over the aligned chunks covering the
+        // bucket (3 * kTiCsrMaxN is a multiple of 8: the reads stay inside).
+        for (int q = p0 & ~7; q < p1; q += 8) {
+            const uint4 v = *reinterpret_cast<const uint4*>(&list[q]);
+            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const int id = static_cast<int>((w4[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
+                rank += (q + j >= p0 && q + j < p1 && id < e) ? 1 : 0;
+            }
+        }
+        sorted[p0 + rank] = static_cast<uint16_t>(e);
+    }
+    __syncthreads();
+    const int total = cursor[M - 1];
+    uint16_t* out = csr.list + b * csr.lstride;
+    float* wout = csr.weight + b * csr.wstride;
+    const float* wb = weights + b * e_count;
+    constexpr int kW = EPT;  // entries per thread in the copy: all loads first
+    float wv[kW];
+#pragma unroll
+    for (int u = 0; u < kW; ++u) wv[u] = wb[sorted[min(tid + u * T, max(total - 1, 0))]];
+#pragma unroll
+    for (int u = 0; u < kW; ++u) {
+        const int p = tid + u * T;
+        if (p < total) {
+            out[p] = sorted[p];
+            wout[p] = wv[u];
+        }
+    }
+}
+
+// Copies up to kTiCsrStage 16-byte chunks per thread from three consecutive
+// source ranges [0, e0), [e0, e1), [e1, e2) of chunk indices into LDS chunks
+// dst[...], every load issued before the first store.
+__device__ __forceinline__ void stage3(float4* __restrict__ dst, const float4* __restrict__ s0,
+                                       const float4* __restrict__ s1,
+                                       const float4* __restrict__ s2, int e0, int e1, int e2) {
+    if (e2 <= 0) return;
+    constexpr int kHalf = kTiCsrStage / 2;  // two arrays: a longer one goes to scratch
+    float4 va[kHalf], vb[kHalf];
+    auto chunk = [&](int u) {  // past the end: the last chunk again, not stored
+        const int i = min(static_cast<int>(threadIdx.x) + u * kTiCsrThreads, e2 - 1);
+        return *(i < e0 ? s0 + i : i < e1 ? s1 + (i - e0) : s2 + (i - e1));  // s2 unused if e1 == e2
+    };
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) va[u] = chunk(u);
+#pragma unroll
+    for (int u = 0; u < kHalf; ++u) vb[u] = chunk(kHalf + u);
+    // Keeps the scheduler from sinking each load down to its store.
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int u = 0; u < kTiCsrStage; ++u) {
+        const int i = threadIdx.x + u * kTiCsrThreads;
+        if (i < e2) dst[i] = u < kHalf ? va[u] : vb[u - kHalf];
+    }
+}
+
+// LDS bytes of the gather for CG channels per step: weights [3N], ids
+// [lstride], starts [sstride], two row buffers [CG][N].
+__host__ __device__ inline int64_t csr_lds_bytes(int cg, int64_t M, int64_t N) {
+    const int64_t ss = (M + 1 + 3) & ~int64_t(3), ls = (3 * N + 7) & ~int64_t(7);
+    const int64_t ws = (3 * N + 3) & ~int64_t(3);
+    return 4 * ws + 2 * ls + 4 * ss + 2 * 4 * cg * N;
+}
+
+template <int CG>
+__global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kernel(
+    const float* __restrict__ grad_out, const float* __restrict__ weights, TiCsr csr,
+    float* __restrict__ grad_features, int64_t C, int M, int N) {
+    static_assert(CG == 1 || CG == 2 || CG == 4, "channels per step");
+    extern __shared__ float4 lds4[];
+    const int e_count = 3 * N;
+    const int w_chunks = csr.wstride / 4, l_chunks = csr.lstride / 8, s_chunks = csr.sstride / 4;
+    const int r_chunks = CG * N / 4;  // one row buffer: [N][CG] floats, channels interleaved
+    float* wl = reinterpret_cast<float*>(lds4);
+    uint16_t* list = reinterpret_cast<uint16_t*>(lds4 + w_chunks);
+    int* start = reinterpret_cast<int*>(lds4 + w_chunks + l_chunks);
+    float4* const rb0 = lds4 + w_chunks + l_chunks + s_chunks;  // row buffers
+    float4* const rb1 = rb0 + r_chunks;
+    const int64_t b = blockIdx.y;
+    const int64_t c_lo = static_cast<int64_t>(blockIdx.x) * kTiCsrBlock;
+    const int cb = static_cast<int>(min<int64_t>(kTiCsrBlock, C - c_lo));
+    const int steps = (cb + CG - 1) / CG;
+    const int tid = threadIdx.x;
+    const int n_chunks = N / 4;  // <= kTiCsrThreads: one 4-unknown chunk per thread
+    const float4* gsrc = reinterpret_cast<const float4*>(grad_out + (b * C + c_lo) * N);
+    // Step g's rows for this thread's chunk: CG float4 (zero past the block).
+    float4 nx0 = make_float4(0.f, 0.f, 0.f, 0.f), nx1 = nx0, nx2 = nx0, nx3 = nx0;
+    auto fetch = [&](int g) {
+        const int cg = min(CG, cb - g * CG);
+        if (tid >= n_chunks) return;
+        const float4* src = gsrc + static_cast<int64_t>(g) * CG * n_chunks + tid;
+        nx0 = src[0];
+        if (CG > 1) nx1 = cg > 1 ? src[n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (CG > 2) nx2 = cg > 2 ? src[2 * n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (CG > 3) nx3 = cg > 3 ? src[3 * n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
+    };
+    auto put = [&](float4* dst) {  // unknowns 4*tid .. 4*tid+3, CG channels each
+        if (tid >= n_chunks) return;
+        if (CG == 1) {
+            dst[tid] = nx0;
+        } else if (CG == 2) {
+            dst[2 * tid] = make_float4(nx0.x, nx1.x, nx0.y, nx1.y);
+            dst[2 * tid + 1] = make_float4(nx0.z, nx1.z, nx0.w, nx1.w);
+        } else {
+            dst[4 * tid] = make_float4(nx0.x, nx1.x, nx2.x, nx3.x);
+            dst[4 * tid + 1] = make_float4(nx0.y, nx1.y, nx2.y, nx3.y);
+            dst[4 * tid + 2] = make_float4(nx0.z, nx1.z, nx2.z, nx3.z);
+            dst[4 * tid + 3] = make_float4(nx0.w, nx1.w, nx2.w, nx3.w);
+        }
+    };
+    // Prologue, one round trip: weights, ids and starts (contiguous in LDS,
+    // in that order) and step 0's rows.
+    fetch(0);
+    stage3(lds4, reinterpret_cast<const float4*>(csr.weight + b * csr.wstride),
+           reinterpret_cast<const float4*>(csr.list + b * csr.lstride),
+           reinterpret_cast<const float4*>(csr.start + b * csr.sstride), w_chunks,
+           w_chunks + l_chunks, w_chunks + l_chunks + s_chunks);
+    put(rb0);
+    if (steps > 1) fetch(1);  // step 1's rows in registers while step 0 is summed
+    __syncthreads();
+    // When every thread has one known point (M <= threads), its first
+    // kTiCsrRegEntries entries (row offset and weight) stay in registers for
+    // all steps; the rest of a longer list is read from LDS.  Otherwise every
+    // entry is read from LDS.
+    constexpr int kReg = kTiCsrRegEntries;
+    const bool one_each = M <= kTiCsrThreads;
+    const int m0 = tid;
+    const int pb = (one_each && m0 < M) ? start[m0] : 0;
+    const int pe = (one_each && m0 < M) ? start[m0 + 1] : 0;
+    int ek[kReg];
+    float wk[kReg];
+#pragma unroll
+    for (int k = 0; k < kReg; ++k) {
+        const int q = min(pb + k, max(pe - 1, pb));  // an unused slot repeats a valid one
+        ek[k] = (pe > pb ? list[q] / 3 : 0) * CG;
+        wk[k] = pe > pb ? wl[q] : 0.f;
+    }
+    for (int g = 0; g < steps; ++g) {
+        const float* rows = reinterpret_cast<const float*>((g & 1) ? rb1 : rb0);
+        const int cg = min(CG, cb - g * CG);
+        const int64_t c0 = c_lo + static_cast<int64_t>(g) * CG;
+        if (one_each) {
+            if (m0 < M) {
+                float acc[CG];
+#pragma unroll
+                for (int cc = 0; cc < CG; ++cc) acc[cc] = 0.f;
+#pragma unroll
+                for (int k = 0; k < kReg; ++k) {
+                    const bool ok = pb + k < pe;
+#pragma unroll
+                    for (int cc = 0; cc < CG; ++cc) {
+                        const float t = rows[ek[k] + cc] * wk[k];
+                        acc[cc] = ok ? acc[cc] + t : acc[cc];
+                    }
+                }
+                // The rest of a long list: eight entries' reads at once (past
+                // the end: the last entry again, not added), added in order.
+                for (int p = pb + kReg; p < pe; p += 8) {
+                    int off[8];
+                    float w[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const int q = min(p + u, pe - 1);
+                        off[u] = (list[q] / 3) * CG;
+                        w[u] = wl[q];
+                    }
+                    float v[8][CG];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u)
+#pragma unroll
+                        for (int cc = 0; cc < CG; ++cc) v[u][cc] = rows[off[u] + cc];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const bool ok = p + u < pe;
+#pragma unroll
+                        for (int cc = 0; cc < CG; ++cc) {
+                            const float t = v[u][cc] * w[u];
+                            acc[cc] = ok ? acc[cc] + t : acc[cc];
+                        }
+                    }
+                }
+#pragma unroll
+                for (int cc = 0; cc < CG; ++cc)
+                    if (cc < cg) grad_features[(b * C + c0 + cc) * M + m0] = acc[cc];
+            }
+        } else {
+            for (int m = tid; m < M; m += kTiCsrThreads) {
+                float acc[CG];
+#pragma unroll
+                for (int cc = 0; cc < CG; ++cc) acc[cc] = 0.f;
+                const int p1 = start[m + 1];
+                for (int p = start[m]; p < p1; ++p) {
+                    const float* col = rows + (list[p] / 3) * CG;
+                    const float w = wl[p];
+#pragma unroll
+                    for (int cc = 0; cc < CG; ++cc) acc[cc] = acc[cc] + col[cc] * w;
+                }
+#pragma unroll
+                for (int cc = 0; cc < CG; ++cc)
+                    if (cc < cg) grad_features[(b * C + c0 + cc) * M + m] = acc[cc];
+            }
+        }
+        if (g + 1 < steps) {
+            // Buffer (g+1)&1 last held step g-1, finished before the previous
+            // barrier.
+            put(((g + 1) & 1) ? rb1 : rb0);
+            if (g + 2 < steps) fetch(g + 2);
+        }
+        __syncthreads();
+    }
+}
+
+// Channels per step of the CSR gather: the largest CG in {4, 2, 1} whose
+// LDS fits the budget (0: none).
+int csr_channel_group(int64_t M, int64_t N) {
+    for (int cg : {4, 2, 1})
+        if (csr_lds_bytes(cg, M, N) <= kTiCsrLdsBytes) return cg;
+    return 0;
+}
+
 // Channels per block so that CG rows of M floats fit the LDS budget (0: too big).
 int lds_channel_group(int64_t M) {
     // At most 4 rows (16 KiB for M = 1024): more, smaller workgroups keep
@@ -444,6 +789,52 @@ hipError_t pointops_three_interpolate(const float* features, const int32_t* idx,
                     static_cast<uint32_t>(B));
     hipLaunchKernelGGL(three_interpolate_kernel, grid, dim3(kTiThreads), 0, stream, features, idx,
                        weights, out, C, M, N);
+    return hipGetLastError();
+}
+
+size_t pointops_three_interpolate_backward_workspace_bytes(int64_t B, int64_t M, int64_t N) {
+    if (B <= 0 || M <= 0 || N <= 0) return 0;
+    return ti_csr_bytes(B, M, N, nullptr, nullptr);
+}
+
+hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const int32_t* idx,
+                                                   const float* weights, float* grad_features,
+                                                   void* workspace, int64_t B, int64_t C, int64_t M,
+                                                   int64_t N, hipStream_t stream) {
+    if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
+    if (B == 0 || C == 0 || M == 0) return hipSuccess;
+    // grad_out rows are staged with 16-byte loads: N % 4 == 0, 16-byte aligned.
+    if (N == 0 || M > kTiCsrMaxM || N > kTiCsrMaxN || N % 4 != 0 || workspace == nullptr ||
+        B > 65535 || (C + kTiCsrBlock - 1) / kTiCsrBlock > INT32_MAX ||
+        reinterpret_cast<uintptr_t>(grad_out) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return hipErrorInvalidValue;
+    const int cg = csr_channel_group(M, N);
+    if (cg == 0) return hipErrorInvalidValue;
+    TiCsr csr;
+    ti_csr_bytes(B, M, N, &csr, static_cast<char*>(workspace));
+    hipLaunchKernelGGL(three_interp_csr_kernel, dim3(static_cast<uint32_t>(B)), dim3(kTiCsrThreads), 0,
+                       stream, idx, weights, csr, static_cast<int>(M), static_cast<int>(N));
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const size_t shmem = static_cast<size_t>(csr_lds_bytes(cg, M, N));
+    const dim3 grid(static_cast<uint32_t>((C + kTiCsrBlock - 1) / kTiCsrBlock),
+                    static_cast<uint32_t>(B));
+    const int m = static_cast<int>(M), n = static_cast<int>(N);
+    switch (cg) {
+        case 4:
+            hipLaunchKernelGGL((three_interp_backward_csr_kernel<4>), grid, dim3(kTiCsrThreads), shmem,
+                               stream, grad_out, weights, csr, grad_features, C, m, n);
+            break;
+        case 2:
+            hipLaunchKernelGGL((three_interp_backward_csr_kernel<2>), grid, dim3(kTiCsrThreads), shmem,
+                               stream, grad_out, weights, csr, grad_features, C, m, n);
+            break;
+        default:
+            hipLaunchKernelGGL((three_interp_backward_csr_kernel<1>), grid, dim3(kTiCsrThreads), shmem,
+                               stream, grad_out, weights, csr, grad_features, C, m, n);
+            break;
+    }
     return hipGetLastError();
 }
 

@@ -45,6 +45,8 @@ _SIGNATURES: dict[str, list] = {
     "pointops_three_nn": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
+    "pointops_three_interpolate_backward_csr": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                                _vp],
     "pointops_ball_query_grid_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_cloud_bounds": [_vp, _vp, _vp, _i64, _i64, _vp],
     "pointops_nearest3_grid": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
@@ -62,6 +64,7 @@ _SIZE_QUERIES: dict[str, list] = {
     "pointops_fps_flat_scratch_bytes": [_i64, _i64],
     "pointops_knn3_grid_workspace_bytes": [_i64, _i64, _i64],
     "pointops_knn3_windowed_workspace_bytes": [_i64, _i64, _i64],
+    "pointops_three_interpolate_backward_workspace_bytes": [_i64, _i64, _i64],
     "pointops_ball_query_grid_workspace_bytes": [_i64, _i64, _i64],
     "pointops_cloud_bounds_workspace_bytes": [_i64],
     "pointops_group_points_backward_workspace_bytes": [_i64, _i64, _i64, _i64],

@@ -11,6 +11,9 @@ from torch.autograd.function import once_differentiable
 from . import _native
 
 _MAX_INDEX = (1 << 31) - 1
+# The deterministic CSR backward covers up to this many known / unknown points.
+_CSR_MAX_KNOWN = 4096
+_CSR_MAX_UNKNOWN = 4096
 
 
 def _validate_three_nn(unknown: Tensor, known: Tensor) -> tuple[int, int, int]:
@@ -117,13 +120,29 @@ class _ThreeInterpolate(torch.autograd.Function):
         batch, queries, _ = indices.shape
         grad_features = None
         if ctx.needs_input_grad[0]:
-            grad_features = torch.zeros((batch, ctx.channels, ctx.points),
-                                        device=indices.device, dtype=torch.float32)
-            if batch * ctx.channels * queries:
-                _native.call("pointops_three_interpolate_backward",
-                             grad_output.contiguous().data_ptr(), indices.data_ptr(),
-                             weights.data_ptr(), grad_features.data_ptr(), batch, ctx.channels,
-                             ctx.points, queries, _native.stream(indices.device))
+            shape = (batch, ctx.channels, ctx.points)
+            stream = _native.stream(indices.device)
+            if (0 < ctx.points <= _CSR_MAX_KNOWN and 0 < queries <= _CSR_MAX_UNKNOWN
+                    and queries % 4 == 0 and batch <= 65535):
+                # Deterministic gather over a CSR of the entries; writes every
+                # element, so no zero fill.
+                grad_features = torch.empty(shape, device=indices.device, dtype=torch.float32)
+                if batch * ctx.channels:
+                    size = _native.size_query("pointops_three_interpolate_backward_workspace_bytes",
+                                              batch, ctx.points, queries)
+                    workspace = torch.empty(size, dtype=torch.uint8, device=indices.device)
+                    _native.call("pointops_three_interpolate_backward_csr",
+                                 grad_output.contiguous().data_ptr(), indices.data_ptr(),
+                                 weights.data_ptr(), grad_features.data_ptr(),
+                                 workspace.data_ptr(), batch, ctx.channels, ctx.points, queries,
+                                 stream)
+            else:
+                grad_features = torch.zeros(shape, device=indices.device, dtype=torch.float32)
+                if batch * ctx.channels * queries:
+                    _native.call("pointops_three_interpolate_backward",
+                                 grad_output.contiguous().data_ptr(), indices.data_ptr(),
+                                 weights.data_ptr(), grad_features.data_ptr(), batch,
+                                 ctx.channels, ctx.points, queries, stream)
         grad_weights = torch.zeros_like(weights) if ctx.needs_input_grad[2] else None
         return grad_features, None, grad_weights
 
@@ -133,8 +152,9 @@ def three_interpolate(features: Tensor, indices: Tensor, weights: Tensor) -> Ten
 
     ``out[b,c,n] = (features[b,c,i0]*w0 + features[b,c,i1]*w1) + features[b,c,i2]*w2``.
     Backward accumulates ``grad_out * w`` at the selected source positions
-    (in (n, t) order for up to 1024 sources and 6826 queries, deterministic;
-    by hardware float atomics otherwise, whose order sets the last bits); the weight
+    in (n, t) order, deterministic, for up to 4096 sources and 4096 queries
+    (a multiple of 4)
+    (beyond that by hardware float atomics, whose order sets the last bits); the weight
     gradient is an explicit zero tensor, as in the original PointNet++ wrapper
     (pointnet2.py:191-211).
     """
