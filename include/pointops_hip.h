@@ -169,14 +169,21 @@ size_t pointops_ball_query_grid_workspace_bytes(int64_t B, int64_t Q, int64_t P)
 hipError_t pointops_ball_query_grid_f32(const float *queries, const float *points, int64_t *idx,
                                         float *dist2, void *workspace, int64_t B, int64_t Q,
                                         int64_t P, int64_t K, float radius_sq, hipStream_t stream);
-/* Bounding box of each cloud's finite points: out (B, 6) = min xyz, max xyz
- * (+inf, -inf for a cloud with none).  `workspace` holds
- * pointops_cloud_bounds_workspace_bytes(B) bytes.  No reference
- * counterpart: the density check that chooses between the grid and the
- * index-order ball query. */
-size_t pointops_cloud_bounds_workspace_bytes(int64_t B);
-hipError_t pointops_cloud_bounds(const float *points, float *out, void *workspace, int64_t B,
-                                 int64_t N, hipStream_t stream);
+/* The ball query of pointops_ball_query_f32 without lengths (identical
+ * results), choosing on the device between the grid search above and the
+ * index-order scan: from the grid build's bounding boxes it estimates the
+ * points per ball, lambda = P (4/3) pi r^3 / V (V the smallest per-cloud box
+ * volume, each side at least 2r), and takes the grid when lambda <
+ * sqrt(P K / 6.4); the other search's launches return at once.  No host
+ * synchronisation, so the call can be captured in a HIP graph.  After the
+ * call the first int32 of `workspace` holds the choice (1 grid, 0 index
+ * order).  `workspace`: pointops_ball_query_auto_workspace_bytes(B, Q, P)
+ * bytes, no initialisation needed; 1 <= K <= 64, B <= 65535.  Replaces
+ * _ball_query_mps.py:139-162 for that case. */
+size_t pointops_ball_query_auto_workspace_bytes(int64_t B, int64_t Q, int64_t P);
+hipError_t pointops_ball_query_auto_f32(const float *queries, const float *points, int64_t *idx,
+                                        float *dist2, void *workspace, int64_t B, int64_t Q,
+                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream);
 
 /* Flat radius search (torch_cluster convention): first K global x indices
  * with squared distance < radius_sq, padded with -1, (Q,K); optional

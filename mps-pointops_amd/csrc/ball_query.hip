@@ -29,15 +29,10 @@ namespace {
 constexpr int kBqThreads = 256;
 constexpr int kBqWaves = kBqThreads / kWave;
 constexpr int kBqDepth = 8;  // 64-point blocks in flight per wave (even)
-// Queries (waves) per workgroup of the LDS-staged dense kernel.
-#ifndef POINTOPS_BQ_LDS_QUERIES
-#define POINTOPS_BQ_LDS_QUERIES 8
-#endif
-constexpr int kBqLdsQueries = POINTOPS_BQ_LDS_QUERIES;
-#ifndef POINTOPS_BQ_LDS_DEPTH
-#define POINTOPS_BQ_LDS_DEPTH 32
-#endif
-constexpr int kBqLdsDepth = POINTOPS_BQ_LDS_DEPTH;  // 64-point blocks per LDS tile
+// LDS-staged dense kernel: queries (waves) per workgroup and 64-point blocks
+// per LDS tile (measured best of 2-16 waves and 8-48 blocks per tile).
+constexpr int kBqLdsQueries = 8;
+constexpr int kBqLdsDepth = 32;
 
 template <typename S>
 __device__ __forceinline__ float widen(S v);
@@ -121,12 +116,15 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
 // load each tile of kBqDepth * 64 points once, and every wave tests its query
 // against the tile.  The workgroup stops after the tile in which its last
 // query reached K hits, so a tile is read from L2 once per NWQ queries.
+// With `skip` set, every workgroup returns at once when *skip != 0 (another
+// search of the same call, chosen on the device, writes the outputs).
 template <typename S, int NWQ>
 __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     const S* __restrict__ queries, const S* __restrict__ points,
     const int64_t* __restrict__ query_lengths, const int64_t* __restrict__ point_lengths,
     int64_t* __restrict__ out_idx, float* __restrict__ out_dist, int64_t Q, int64_t P, int K,
-    float r2) {
+    float r2, const int* __restrict__ skip) {
+    if (skip != nullptr && *skip != 0) return;  // uniform, before any barrier
     constexpr int kTile = kBqLdsDepth * kWave;
     constexpr int kPer = kTile / (NWQ * kWave);  // points each thread stages per tile
     static_assert(kPer * NWQ * kWave == kTile && kBqLdsDepth % 2 == 0, "tile shape");
@@ -272,26 +270,27 @@ __global__ __launch_bounds__(kBqThreads) void radius_flat_kernel(
     for (int s = found + lane; s < K; s += kWave) o[s] = -1;
 }
 
+// `skip` (device word, may be null) is honoured by the LDS-staged kernel
+// only, so a call with `skip` must fit it (B <= 65535).
 template <typename S>
 hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t* pl, int64_t* idx,
                        float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K, float r2,
-                       hipStream_t stream) {
+                       const int* skip, hipStream_t stream) {
     if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kBqDepth * kWave)
         return hipErrorInvalidValue;
     if (B == 0 || Q == 0 || K == 0) return hipSuccess;
-    if constexpr (kBqLdsQueries > 0) {
-        constexpr int NWQ = kBqLdsQueries;
-        const int64_t qblocks = (Q + NWQ - 1) / NWQ;
-        if (B <= 65535 && qblocks <= INT32_MAX) {
-            // Clouds are spread over all XCDs (blockIdx.x fastest), which
-            // balances clouds of different scan lengths across them.
-            hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ>),
-                               dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
-                               dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,
-                               static_cast<int>(K), r2);
-            return hipGetLastError();
-        }
+    constexpr int NWQ = kBqLdsQueries;
+    const int64_t qblocks = (Q + NWQ - 1) / NWQ;
+    if (B <= 65535 && qblocks <= INT32_MAX) {
+        // Clouds are spread over all XCDs (blockIdx.x fastest), which
+        // balances clouds of different scan lengths across them.
+        hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ>),
+                           dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
+                           dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,
+                           static_cast<int>(K), r2, skip);
+        return hipGetLastError();
     }
+    if (skip != nullptr) return hipErrorInvalidValue;
     const int64_t blocks = (B * Q + kBqWaves - 1) / kBqWaves;
     if (blocks > INT32_MAX) return hipErrorInvalidValue;
     hipLaunchKernelGGL((ball_query_kernel<S>), dim3(static_cast<uint32_t>(blocks)), dim3(kBqThreads),
@@ -314,6 +313,14 @@ hipError_t launch_radius(const S* y, const S* x, const int64_t* ptr_y, const int
 }
 
 }  // namespace
+
+hipError_t ball_query_f32_unless(const float* queries, const float* points, int64_t* idx,
+                                 float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K,
+                                 float radius_sq, const int* skip, hipStream_t stream) {
+    return launch_ball<float>(queries, points, nullptr, nullptr, idx, dist2, B, Q, P, K, radius_sq,
+                              skip, stream);
+}
+
 }  // namespace pointops
 
 using namespace pointops;
@@ -325,7 +332,7 @@ hipError_t pointops_ball_query_f32(const float* queries, const float* points,
                                    int64_t* idx, float* dist2, int64_t B, int64_t Q, int64_t P,
                                    int64_t K, float radius_sq, hipStream_t stream) {
     return launch_ball<float>(queries, points, query_lengths, point_lengths, idx, dist2, B, Q, P, K,
-                              radius_sq, stream);
+                              radius_sq, nullptr, stream);
 }
 
 hipError_t pointops_ball_query_f16(const uint16_t* queries, const uint16_t* points,
@@ -333,7 +340,7 @@ hipError_t pointops_ball_query_f16(const uint16_t* queries, const uint16_t* poin
                                    int64_t* idx, float* dist2, int64_t B, int64_t Q, int64_t P,
                                    int64_t K, float radius_sq, hipStream_t stream) {
     return launch_ball<uint16_t>(queries, points, query_lengths, point_lengths, idx, dist2, B, Q, P,
-                                 K, radius_sq, stream);
+                                 K, radius_sq, nullptr, stream);
 }
 
 hipError_t pointops_radius_flat_f32(const float* y, const float* x, const int64_t* ptr_y,

@@ -37,13 +37,10 @@ constexpr int kGridMaxDim = 1024;
 constexpr int kGridSearchWaves = 4;
 constexpr int kGridCap = 16;  // buffered candidates per lane
 constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
-#ifndef POINTOPS_GRID_NEAREST_GROW
-#define POINTOPS_GRID_NEAREST_GROW 6
-#endif
-// Nearest mode: box faces a lane may add before its query is left to the scan.
-constexpr int kGridNearestGrow = POINTOPS_GRID_NEAREST_GROW;
+// Nearest mode: box faces a lane may add before its query is left to the
+// fill pass (measured best of 4-24).
+constexpr int kGridNearestGrow = 6;
 constexpr int kGridQueriesPerWave = kWave / 4;  // one quad of lanes per query
-constexpr uint32_t kGridEmpty = 0xFFFFFFFFu;
 constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
 
 struct alignas(16) GridParams {
@@ -66,6 +63,8 @@ __host__ __device__ inline int64_t grid_cell_cap(int64_t N) { return N / 2 > 64 
 __host__ __device__ inline double grid_per_cell(int K) { return K * 0.4 > 3.0 ? K * 0.4 : 3.0; }
 
 struct GridLayout {
+    int* control;    // 64 words: control[0] is the ball query's device-side choice
+    const int* gate; // null, or control: the build and ball search skip when *gate == 0
     GridParams* params;
     float* partial;  // [B][kGridBoundBlocks][8]: bounding-box partials
     int* ref_off;    // [B][stride]: cell counts, then offsets
@@ -91,6 +90,7 @@ __host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_
         o = align256(o + bytes);
         return at;
     };
+    const size_t p_ctrl = take(64 * sizeof(int));
     const size_t p_params = take(static_cast<size_t>(B) * sizeof(GridParams));
     const size_t p_part = take(static_cast<size_t>(B) * kGridBoundBlocks * 8 * sizeof(float));
     const size_t p_roff = take(static_cast<size_t>(B * stride) * sizeof(int));
@@ -101,6 +101,8 @@ __host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_
     const size_t p_sorted = take(static_cast<size_t>(B * N) * sizeof(float4));
     const size_t p_qord = take(static_cast<size_t>(B * M) * sizeof(int));
     if (out != nullptr) {
+        out->control = reinterpret_cast<int*>(base + p_ctrl);
+        out->gate = nullptr;
         out->params = reinterpret_cast<GridParams*>(base + p_params);
         out->partial = reinterpret_cast<float*>(base + p_part);
         out->ref_off = reinterpret_cast<int*>(base + p_roff);
@@ -114,6 +116,12 @@ __host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_
         out->tiles = tiles;
     }
     return o;
+}
+
+// True when the call's device-side choice went to the index-order search:
+// the grid's sort and search then return at once.
+__device__ __forceinline__ bool grid_gated_off(const GridLayout& L) {
+    return L.gate != nullptr && *L.gate == 0;
 }
 
 __device__ __forceinline__ bool finite3(float x, float y, float z) {
@@ -301,6 +309,7 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const floa
                                                                       GridLayout L, int64_t N, int64_t M,
                                                                       uint32_t ref_blocks, int parts,
                                                                       int K, float hmin) {
+    if (grid_gated_off(L)) return;  // uniform, before any barrier
     __shared__ GridParams shared_params;
     const int64_t b = blockIdx.y;
     if (threadIdx.x < kWave) grid_params(L, b, N, parts, K, hmin, &shared_params);
@@ -352,6 +361,7 @@ __device__ __forceinline__ void load8(const int* a, int at, int count, int (&v)[
 
 // Pass 1: the total of each tile.
 __global__ __launch_bounds__(kGridPrepThreads) void grid_tile_sum_kernel(GridLayout L) {
+    if (grid_gated_off(L)) return;
     __shared__ int red[kGridPrepThreads / kWave];
     const int64_t b = blockIdx.y;
     const bool queries = blockIdx.z != 0;
@@ -371,6 +381,7 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_tile_sum_kernel(GridLay
 // Pass 2: exclusive offsets of each tile's entries, in place, after the
 // totals of the tiles before it.
 __global__ __launch_bounds__(kGridPrepThreads) void grid_tile_scan_kernel(GridLayout L) {
+    if (grid_gated_off(L)) return;
     __shared__ int red[kGridPrepThreads / kWave];
     __shared__ int wsum[kGridPrepThreads / kWave];
     const int64_t b = blockIdx.y;
@@ -424,6 +435,7 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_scatter_kernel(const fl
                                                                         const float* __restrict__ query,
                                                                         GridLayout L, int64_t N, int64_t M,
                                                                         uint32_t ref_blocks) {
+    if (grid_gated_off(L)) return;
     const PrepItem it = prep_item(ref, query, N, M, ref_blocks);
     if (it.j >= it.n) return;
     const int64_t b = blockIdx.y;
@@ -782,6 +794,7 @@ template <int S>
 __global__ __launch_bounds__(kGridSearchWaves * kWave) void ball3_grid_kernel(
     const float* __restrict__ query, GridLayout L, int64_t* __restrict__ out_idx,
     float* __restrict__ out_dist, int64_t B, int64_t M, int64_t N, int K, float r2) {
+    if (grid_gated_off(L)) return;
     constexpr int KMAX = 4 * S;
     __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
     const int lane = lane_id();
@@ -878,66 +891,56 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void ball3_grid_kernel(
     }
 }
 
-// Bounding box of each cloud's finite points, (min xyz, max xyz) per batch:
-// partial boxes of up to kGridBoundBlocks workgroups per batch, then one wave
-// per batch combines them.  Used by callers that size a search from the
-// clouds' density.
-__global__ __launch_bounds__(kGridPrepThreads) void cloud_bounds_partial_kernel(
-    const float* __restrict__ pts, float* __restrict__ partial, int64_t N) {
-    __shared__ float red[6][kGridPrepThreads / kWave];
-    const int64_t b = blockIdx.y;
-    const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
-    const int64_t step = static_cast<int64_t>(gridDim.x) * kGridPrepThreads;
-    const float* r = pts + 3 * b * N;
-    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
-    for (int64_t j = static_cast<int64_t>(blockIdx.x) * kGridPrepThreads + tid; j < N; j += step) {
-        const float x = r[3 * j], y = r[3 * j + 1], z = r[3 * j + 2];
-        if (finite3(x, y, z)) {
-            mn[0] = fminf(mn[0], x); mx[0] = fmaxf(mx[0], x);
-            mn[1] = fminf(mn[1], y); mx[1] = fmaxf(mx[1], y);
-            mn[2] = fminf(mn[2], z); mx[2] = fmaxf(mx[2], z);
-        }
-    }
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        const float wmn = wave_min(mn[a]), wmx = wave_max(mx[a]);
-        if (lane == 0) {
-            red[a][wave] = wmn;
-            red[3 + a][wave] = wmx;
-        }
-    }
-    __syncthreads();
-    if (tid >= 6) return;
-    float v = red[tid][0];
-    for (int w = 1; w < kGridPrepThreads / kWave; ++w) v = tid < 3 ? fminf(v, red[tid][w]) : fmaxf(v, red[tid][w]);
-    partial[(b * gridDim.x + blockIdx.x) * 6 + tid] = v;
-}
+// Device-side choice of the ball query between the grid and the index-order
+// scan, from the grid build's bounding-box partials: the expected points
+// per ball, lambda = N (4/3) pi r^3 / V with V the smallest per-cloud box
+// volume (each side at least 2r; float32 products), against sqrt(N K / 6.4):
+// the grid examines about 6.4 lambda points per query, the index-order scan
+// stops after about N K / lambda.  Writes 1 (grid) or 0 to *choice.  One
+// workgroup; wave w reduces the partials of batches w, w + NW, ...
+constexpr int kGateThreads = 1024;
 
-__global__ __launch_bounds__(kWave) void cloud_bounds_final_kernel(const float* __restrict__ partial,
-                                                                  float* __restrict__ out, int parts) {
-    const int64_t b = blockIdx.x;
-    const int lane = threadIdx.x;
-    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
-    for (int i = lane; i < parts; i += kWave) {
-        const float* t = partial + (b * parts + i) * 6;
+__global__ __launch_bounds__(kGateThreads) void ball_grid_choice_kernel(GridLayout L, int64_t B,
+                                                                        int64_t N, int parts, int K,
+                                                                        float radius_sq,
+                                                                        int* __restrict__ choice) {
+    constexpr int NW = kGateThreads / kWave;
+    __shared__ float wave_vol[NW];
+    const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+    const double radius = sqrt(static_cast<double>(radius_sq));
+    const float side = static_cast<float>(2.0 * radius);
+    float vmin = INFINITY;
+    for (int64_t b = wave; b < B; b += NW) {
+        float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+        for (int i = lane; i < parts; i += kWave) {
+            const float* t = L.partial + (b * kGridBoundBlocks + i) * 8;
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                mn[a] = fminf(mn[a], t[a]);
+                mx[a] = fmaxf(mx[a], t[3 + a]);
+            }
+        }
+        float vol = 1.f;
 #pragma unroll
         for (int a = 0; a < 3; ++a) {
-            mn[a] = fminf(mn[a], t[a]);
-            mx[a] = fmaxf(mx[a], t[3 + a]);
+            // No finite point: max - min = -inf, so the side is 2r.
+            vol = vol * fmaxf(wave_max(mx[a]) - wave_min(mn[a]), side);
         }
+        vmin = fminf(vmin, vol);
     }
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        mn[a] = wave_min(mn[a]);
-        mx[a] = wave_max(mx[a]);
+    if (lane == 0) wave_vol[wave] = vmin;
+    __syncthreads();
+    if (threadIdx.x != 0) return;
+    float v = wave_vol[0];
+    for (int w = 1; w < NW; ++w) v = fminf(v, wave_vol[w]);
+    bool grid = false;
+    if (radius_sq > 0.f && radius_sq < INFINITY && v > 0.f && v < INFINITY) {
+        constexpr double kPi = 3.14159265358979323846;
+        const double per_ball =
+            static_cast<double>(N) * (4.0 / 3.0) * kPi * radius * radius * radius / v;
+        grid = per_ball < sqrt(static_cast<double>(N) * K / 6.4);
     }
-    if (lane == 0) {
-#pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            out[b * 6 + a] = mn[a];
-            out[b * 6 + 3 + a] = mx[a];
-        }
-    }
+    *choice = grid ? 1 : 0;
 }
 
 // Nearest mode's second pass over each cloud's list of the queries the grid
@@ -1028,18 +1031,29 @@ using namespace pointops;
 
 namespace {
 
-// The five build launches shared by the kNN and ball-query searches.
+// Bounding-box partials per batch (grid_bounds_kernel), their count per batch.
+int grid_partial_count(int64_t N) {
+    return static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
+}
+
+// The five build launches shared by the kNN and ball-query searches; with
+// `choice` (ball query only) the device-side choice runs after the bounds and
+// L.gate must point at it.
 void grid_build(const float* query, const float* ref, const GridLayout& L, int64_t B, int64_t M,
-                int64_t N, int K, float hmin, hipStream_t stream) {
+                int64_t N, int K, float hmin, hipStream_t stream, int* choice = nullptr,
+                float radius_sq = 0.f) {
     const uint32_t nb = static_cast<uint32_t>(B);
     const uint32_t ref_blocks = static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads);
     const uint32_t q_blocks = static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads);
     const dim3 point_grid(ref_blocks + q_blocks, nb);
     const dim3 scan_grid(static_cast<uint32_t>(L.tiles), nb, 2);
-    const int parts = static_cast<int>(std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096));
+    const int parts = grid_partial_count(N);
     const dim3 prep(kGridPrepThreads);
     hipLaunchKernelGGL(grid_bounds_kernel, dim3(static_cast<uint32_t>(parts), nb), prep, 0, stream,
                        ref, L, N);
+    if (choice != nullptr)
+        hipLaunchKernelGGL(ball_grid_choice_kernel, dim3(1), dim3(kGateThreads), 0, stream, L, B, N,
+                           parts, K, radius_sq, choice);
     hipLaunchKernelGGL(grid_count_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks,
                        parts, K, hmin);
     hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
@@ -1120,31 +1134,20 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     return hipGetLastError();
 }
 
-size_t pointops_cloud_bounds_workspace_bytes(int64_t B) {
-    return B <= 0 ? 0 : static_cast<size_t>(B) * kGridBoundBlocks * 6 * sizeof(float);
-}
-
-hipError_t pointops_cloud_bounds(const float* points, float* out, void* workspace, int64_t B,
-                                 int64_t N, hipStream_t stream) {
-    if (B < 0 || N < 0 || B > 65535) return hipErrorInvalidValue;
-    if (B == 0) return hipSuccess;
-    if (workspace == nullptr || out == nullptr || points == nullptr) return hipErrorInvalidValue;
-    const int parts = static_cast<int>(std::max<int64_t>(1, std::min<int64_t>(kGridBoundBlocks, (N + 4095) / 4096)));
-    auto* partial = static_cast<float*>(workspace);
-    hipLaunchKernelGGL(cloud_bounds_partial_kernel, dim3(static_cast<uint32_t>(parts), static_cast<uint32_t>(B)),
-                       dim3(kGridPrepThreads), 0, stream, points, partial, N);
-    hipLaunchKernelGGL(cloud_bounds_final_kernel, dim3(static_cast<uint32_t>(B)), dim3(kWave), 0, stream,
-                       partial, out, parts);
-    return hipGetLastError();
-}
-
 size_t pointops_ball_query_grid_workspace_bytes(int64_t B, int64_t Q, int64_t P) {
     return pointops_knn3_grid_workspace_bytes(B, Q, P);
 }
 
-hipError_t pointops_ball_query_grid_f32(const float* queries, const float* points, int64_t* idx,
-                                        float* dist2, void* workspace, int64_t B, int64_t Q,
-                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream) {
+}  // extern "C"
+
+namespace {
+
+// The grid ball query; with `choose`, its sort and search are skipped on the
+// device unless ball_grid_choice_kernel picks them, and the index-order
+// kernel runs otherwise.
+hipError_t ball_query_grid(const float* queries, const float* points, int64_t* idx, float* dist2,
+                           void* workspace, int64_t B, int64_t Q, int64_t P, int64_t K,
+                           float radius_sq, bool choose, hipStream_t stream) {
     if (B < 0 || Q < 0 || P < 0 || K < 0 || K > 64) return hipErrorInvalidValue;
     if (B == 0 || Q == 0 || K == 0) return hipSuccess;
     if (P == 0 || P >= (int64_t(1) << 31) - 64 || Q >= (int64_t(1) << 31) - 64 || B > 65535 ||
@@ -1154,8 +1157,10 @@ hipError_t pointops_ball_query_grid_f32(const float* queries, const float* point
     if (!grid_search_grid(B, Q, grid)) return hipErrorInvalidValue;
     GridLayout L;
     grid_layout_bytes(B, Q, P, &L, static_cast<char*>(workspace));
+    if (choose) L.gate = L.control;
     const float hmin = (radius_sq > 0.f && radius_sq < INFINITY) ? sqrtf(radius_sq) : 0.f;
-    grid_build(queries, points, L, B, Q, P, static_cast<int>(K), hmin, stream);
+    grid_build(queries, points, L, B, Q, P, static_cast<int>(K), hmin, stream,
+               choose ? L.control : nullptr, radius_sq);
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
@@ -1168,7 +1173,32 @@ hipError_t pointops_ball_query_grid_f32(const float* queries, const float* point
         hipLaunchKernelGGL((ball3_grid_kernel<8>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
     else
         hipLaunchKernelGGL((ball3_grid_kernel<16>), grid, block, 0, stream, queries, L, idx, dist2, B, Q, P, k, radius_sq);
-    return hipGetLastError();
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess || !choose) return err;
+    return ball_query_f32_unless(queries, points, idx, dist2, B, Q, P, K, radius_sq, L.control,
+                                 stream);
+}
+
+}  // namespace
+
+extern "C" {
+
+hipError_t pointops_ball_query_grid_f32(const float* queries, const float* points, int64_t* idx,
+                                        float* dist2, void* workspace, int64_t B, int64_t Q,
+                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream) {
+    return ball_query_grid(queries, points, idx, dist2, workspace, B, Q, P, K, radius_sq, false,
+                           stream);
+}
+
+size_t pointops_ball_query_auto_workspace_bytes(int64_t B, int64_t Q, int64_t P) {
+    return pointops_knn3_grid_workspace_bytes(B, Q, P);
+}
+
+hipError_t pointops_ball_query_auto_f32(const float* queries, const float* points, int64_t* idx,
+                                        float* dist2, void* workspace, int64_t B, int64_t Q,
+                                        int64_t P, int64_t K, float radius_sq, hipStream_t stream) {
+    return ball_query_grid(queries, points, idx, dist2, workspace, B, Q, P, K, radius_sq, true,
+                           stream);
 }
 
 }  // extern "C"

@@ -10,10 +10,12 @@
 //
 // three_interpolate: out[b,c,n] = (f[i0]*w0 + f[i1]*w1) + f[i2]*w2
 // (kernels/pointnet2.metal:52-71).  When a group of feature rows fits LDS
-// (M <= 16384) a block stages CG rows of one batch and gathers from LDS; the
-// backward accumulates g*w_t into LDS rows with LDS float atomics and writes
-// each row once.  Larger M falls back to one lane per (b, n) over 4 channels,
-// gathering from memory, with hardware float atomics in the backward.
+// (M <= 16384) a block stages CG rows of one batch and gathers from LDS.
+// Larger M falls back to one lane per (b, n) over 4 channels, gathering from
+// memory.  The backward sums g*w_t per known point in (n, t) order from a
+// per-batch CSR of the entries (deterministic, no float atomics) where the
+// shape allows, else accumulates into LDS rows with LDS float atomics, or
+// into memory with hardware float atomics.
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -174,12 +176,9 @@ __global__ __launch_bounds__(kTiThreads) void three_interpolate_backward_kernel(
 // unknowns of its (batch, channel group).
 constexpr int kTiLdsFloats = 16384;  // 64 KiB of dynamic LDS
 constexpr int kTiSlices = 1;         // unknown-slices per (batch, channel group) in the forward
-#ifndef POINTOPS_TI_BWD_THREADS
-#define POINTOPS_TI_BWD_THREADS 1024
-#endif
 // Backward: one block covers all unknowns of its (batch, channel group), so it
 // is wide to keep enough loads and LDS atomics in flight.
-constexpr int kTiBwdThreads = POINTOPS_TI_BWD_THREADS;
+constexpr int kTiBwdThreads = 1024;
 
 // Copy `count` floats from global memory to LDS with float4 loads, eight in
 // flight per thread (the source is 16-byte aligned when count % 4 == 0).

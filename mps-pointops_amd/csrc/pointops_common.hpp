@@ -202,7 +202,11 @@ __device__ __forceinline__ CloudBlock cloud_block(uint32_t per_cloud) {
     return {blk % per_cloud, blk / per_cloud};
 }
 
-}  // namespace pointops
+// ball_query.hip: the index-order float32 ball query without lengths (the
+// LDS-staged kernel, B <= 65535), every workgroup returning at once when
+// `skip` is non-null and *skip != 0 at launch time.
+hipError_t ball_query_f32_unless(const float* queries, const float* points, int64_t* idx,
+                                 float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K,
+                                 float radius_sq, const int* skip, hipStream_t stream);
 
-// Host-side launch helper: checks the launch and returns its status.
-#define POINTOPS_LAUNCH_STATUS() (hipGetLastError())
+}  // namespace pointops

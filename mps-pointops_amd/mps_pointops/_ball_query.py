@@ -77,36 +77,16 @@ def _checked_radius_and_k(radius: float, k: int) -> tuple[float, float]:
 
 
 # Without lengths, float32 clouds of at least this many points, at most this
-# many neighbours and at least this many query-point pairs in all may use the
-# grid search (the same results).  It scans the cells around each query
-# (about 6.4 lambda points for lambda points per ball), where the index-order
-# scan stops after about N K / lambda points: the grid is chosen while
-# lambda < sqrt(N K / 6.4), lambda estimated from each cloud's bounding box.
+# many neighbours and at least this many query-point pairs in all go to
+# pointops_ball_query_auto_f32, which chooses on the device between the grid
+# search and the index-order scan (the same results): the grid scans the
+# cells around each query (about 6.4 lambda points for lambda points per
+# ball), the index-order scan stops after about N K / lambda points, so the
+# grid is taken while lambda < sqrt(N K / 6.4), lambda estimated from each
+# cloud's bounding box.  No host synchronisation is involved.
 _GRID_MIN_POINTS = 32_768
 _GRID_MAX_K = 64
 _GRID_MIN_PAIRS = 1 << 26
-
-
-def _grid_pays(points: torch.Tensor, radius_sq: float, k: int) -> bool:
-    """Expected points per ball, from the densest cloud's bounding box (each
-    side at least the ball's diameter), against sqrt(N K / 6.4); one
-    device-to-host synchronisation."""
-    if not (0.0 < radius_sq < math.inf):
-        return False
-    radius = math.sqrt(radius_sq)
-    batch, n, _ = points.shape
-    box = torch.empty((batch, 6), dtype=torch.float32, device=points.device)
-    size = _native.size_query("pointops_cloud_bounds_workspace_bytes", batch)
-    workspace = torch.empty(size, dtype=torch.uint8, device=points.device)
-    _native.call("pointops_cloud_bounds", points.contiguous().data_ptr(), box.data_ptr(),
-                 workspace.data_ptr(), batch, n, _native.stream(points.device))
-    box = box.cpu()
-    extent = (box[:, 3:] - box[:, :3]).clamp_min(2.0 * radius)
-    volume = float(extent.prod(dim=1).amin())
-    if not math.isfinite(volume) or volume <= 0.0:
-        return False
-    per_ball = n * (4.0 / 3.0) * math.pi * radius ** 3 / volume
-    return per_ball < math.sqrt(n * k / 6.4)
 
 
 def _launch(queries, points, query_lengths, point_lengths, radius_sq, k):
@@ -118,13 +98,11 @@ def _launch(queries, points, query_lengths, point_lengths, radius_sq, k):
     if (indices.numel() and query_lengths is None and point_lengths is None
             and queries.dtype == torch.float32 and k <= _GRID_MAX_K
             and point_count >= _GRID_MIN_POINTS and batch <= 65_535
-            and batch * query_count * point_count >= _GRID_MIN_PAIRS
-            and not torch.cuda.is_current_stream_capturing()  # the check below syncs
-            and _grid_pays(points.detach(), radius_sq, k)):
-        size = _native.size_query("pointops_ball_query_grid_workspace_bytes", batch,
+            and batch * query_count * point_count >= _GRID_MIN_PAIRS):
+        size = _native.size_query("pointops_ball_query_auto_workspace_bytes", batch,
                                   query_count, point_count)
         workspace = torch.empty(size, dtype=torch.uint8, device=device)
-        _native.call("pointops_ball_query_grid_f32", queries.data_ptr(), points.data_ptr(),
+        _native.call("pointops_ball_query_auto_f32", queries.data_ptr(), points.data_ptr(),
                      indices.data_ptr(), distances.data_ptr(), workspace.data_ptr(), batch,
                      query_count, point_count, k, radius_sq, _native.stream(device))
         return distances, indices

@@ -48,7 +48,7 @@ _SIGNATURES: dict[str, list] = {
     "pointops_three_interpolate_backward_csr": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _vp],
     "pointops_ball_query_grid_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
-    "pointops_cloud_bounds": [_vp, _vp, _vp, _i64, _i64, _vp],
+    "pointops_ball_query_auto_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_nearest3_grid": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_group_points": [_vp, _vp, _i32, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_group_points_backward": [_vp, _i64, _vp, _i32, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
@@ -66,7 +66,7 @@ _SIZE_QUERIES: dict[str, list] = {
     "pointops_knn3_windowed_workspace_bytes": [_i64, _i64, _i64],
     "pointops_three_interpolate_backward_workspace_bytes": [_i64, _i64, _i64],
     "pointops_ball_query_grid_workspace_bytes": [_i64, _i64, _i64],
-    "pointops_cloud_bounds_workspace_bytes": [_i64],
+    "pointops_ball_query_auto_workspace_bytes": [_i64, _i64, _i64],
     "pointops_group_points_backward_workspace_bytes": [_i64, _i64, _i64, _i64],
 }
 

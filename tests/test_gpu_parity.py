@@ -8,6 +8,8 @@ a tolerance (rtol 1e-5 / atol 1e-6, stated per test).
 
 from __future__ import annotations
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -1345,30 +1347,100 @@ def test_ball_query_grid_public_path(cuda_device):
     assert q.grad is not None and torch.isfinite(q.grad).all()
 
 
-def test_cloud_bounds_matches_numpy(cuda_device):
-    """pointops_cloud_bounds: per-cloud min/max of the finite points (exact,
-    min/max round nothing); a cloud with none gives +inf/-inf; many blocks."""
+def _expected_choice(ref: np.ndarray, radius_sq: float, k: int) -> int:
+    """The documented grid/index-order rule restated on the host: lambda =
+    P (4/3) pi r^3 / V, V the smallest per-cloud box volume (float32, each
+    side at least 2r), grid while lambda < sqrt(P K / 6.4)."""
+    if not 0.0 < radius_sq < math.inf:
+        return 0
+    r = math.sqrt(radius_sq)
+    side = np.float32(2.0 * r)
+    volumes = []
+    for cloud in ref:
+        finite = cloud[np.isfinite(cloud).all(axis=1)]
+        ext = (finite.max(0) - finite.min(0)) if len(finite) else np.full(3, -np.inf, np.float32)
+        ext = np.maximum(ext.astype(np.float32), side)
+        volumes.append(np.float32(np.float32(ext[0] * ext[1]) * ext[2]))
+    v = float(min(volumes))
+    if not 0.0 < v < math.inf:
+        return 0
+    n = ref.shape[1]
+    return int(n * (4.0 / 3.0) * math.pi * r ** 3 / v < math.sqrt(n * k / 6.4))
+
+
+def _ball_auto(query: torch.Tensor, ref: torch.Tensor, radius: float, k: int):
+    """pointops_ball_query_auto_f32 through the C ABI into outputs filled
+    with garbage (every slot must be written); returns the device's choice."""
     from mps_pointops import _native
 
-    rng = np.random.default_rng(5)
-    for B, N in ((1, 1), (3, 1000), (2, 300_000), (4, 4097)):
-        pts = (rng.standard_normal((B, N, 3)) * rng.uniform(0.1, 50, (B, 1, 3))).astype(np.float32)
-        if N > 10:
-            pts[0, 3] = (np.inf, 0.0, 0.0)
-            pts[-1, N // 2] = (np.nan, 1e30, -1e30)
-        if B > 2:
-            pts[1] = np.nan
-        x = torch.from_numpy(pts).cuda()
-        out = torch.empty((B, 6), dtype=torch.float32, device=x.device)
-        size = _native.size_query("pointops_cloud_bounds_workspace_bytes", B)
-        ws = torch.empty(size, dtype=torch.uint8, device=x.device)
-        _native.call("pointops_cloud_bounds", x.data_ptr(), out.data_ptr(), ws.data_ptr(), B, N,
-                     _native.stream(x.device))
-        got = host(out)
-        for b in range(B):
-            finite = pts[b][np.isfinite(pts[b]).all(axis=1)]
-            if len(finite) == 0:
-                want = np.array([np.inf] * 3 + [-np.inf] * 3, dtype=np.float32)
-            else:
-                want = np.concatenate([finite.min(axis=0), finite.max(axis=0)])
-            np.testing.assert_array_equal(got[b], want, err_msg=f"B={B} N={N} b={b}")
+    q, r = query.cuda().contiguous(), ref.cuda().contiguous()
+    B, Q, _ = q.shape
+    P = r.shape[1]
+    dist = torch.full((B, Q, k), float("nan"), device="cuda")
+    idx = torch.full((B, Q, k), 7, dtype=torch.long, device="cuda")
+    size = _native.size_query("pointops_ball_query_auto_workspace_bytes", B, Q, P)
+    ws = torch.full((size,), 0xAB, dtype=torch.uint8, device="cuda")
+    _native.call("pointops_ball_query_auto_f32", q.data_ptr(), r.data_ptr(), idx.data_ptr(),
+                 dist.data_ptr(), ws.data_ptr(), B, Q, P, k, O.ball_radius_sq(radius),
+                 _native.stream(q.device))
+    choice = int(ws[:4].view(torch.int32).item())
+    return host(dist), host(idx), choice
+
+
+@pytest.mark.parametrize("name,radius,k", [
+    ("uniform", 0.4, 16), ("uniform", 3.0, 64), ("uniform", 0.0, 8), ("uniform", 1e30, 4),
+    ("slab", 0.5, 32), ("one_point", 0.5, 16), ("non_finite_refs", 0.2, 16),
+    ("far_queries", 0.3, 1), ("sparse_clusters", 2.0, 64), ("ties", 1.0, 32)])
+def test_ball_query_auto_choice_and_results(cuda_device, name, radius, k):
+    """The device-side choice follows the documented rule, and whichever
+    search it takes, the result is the index-order answer bit for bit with
+    every output slot written."""
+    query, ref = _grid_case(name)
+    want_d, want_i = O.ball_query(query, ref, radius, k)
+    d, i, choice = _ball_auto(query, ref, radius, k)
+    assert choice == _expected_choice(ref.numpy(), O.ball_radius_sq(radius), k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
+
+
+def test_ball_query_auto_takes_both_paths(cuda_device):
+    """The cases above cover both choices (sparse balls: grid, dense or
+    degenerate ones: index order)."""
+    query, ref = _grid_case("uniform")
+    assert _ball_auto(query, ref, 0.4, 16)[2] == 1
+    assert _ball_auto(query, ref, 3.0, 64)[2] == 0
+
+
+def test_ball_query_public_path_in_a_graph(cuda_device):
+    """ops.ball_query on a grid-eligible shape synchronises nothing, so it
+    can be captured; every replay (new point data copied into the captured
+    input between replays, which flips the device-side choice, and eager
+    work in between) equals the eager call on the same data."""
+    import mps_pointops as mp
+
+    g = torch.Generator().manual_seed(21)
+    sparse = torch.rand(1, 40_000, 3, generator=g) * 10
+    dense = torch.rand(1, 40_000, 3, generator=g) * 0.5
+    queries = (torch.rand(1, 3000, 3, generator=g) * 10).cuda()
+    points = sparse.cuda()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        mp.ball_query(queries, points, 0.4, 16)  # warm-up off the capture
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        d, i = mp.ball_query(queries, points, 0.4, 16)
+    for cloud in (sparse, dense, sparse, dense):
+        points.copy_(cloud.cuda())
+        graph.replay()
+        torch.cuda.synchronize()
+        want_d, want_i = mp.ball_query(queries, points, 0.4, 16)
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(host(i), host(want_i))
+        same_bits(host(d), host(want_d))
+    oracle_d, oracle_i = O.ball_query(queries.cpu(), dense, 0.4, 16)
+    np.testing.assert_array_equal(host(i), oracle_i)
+    same_bits(host(d), oracle_d)
+
+
