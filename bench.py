@@ -82,6 +82,19 @@ def make_c3(seed: int = 3, N: int = 1 << 20) -> torch.Tensor:
     return torch.cat([xy, z], 1).float().unsqueeze(0).contiguous()
 
 
+def make_c4_clustered(seed: int = 41) -> tuple[torch.Tensor, torch.Tensor]:
+    """Config 4's sizes on clustered data: 1,048,576 references in 40 tight
+    Gaussian clusters (sigma 0.1) at uniform centres in [0,100]^3, and 131072
+    queries uniform over the same box, so most queries lie far from every
+    reference (the grid search's worst case)."""
+    g = torch.Generator().manual_seed(seed)
+    n = 1 << 20
+    centres = torch.rand(40, 3, generator=g) * 100
+    ref = centres.repeat_interleave(n // 40 + 1, 0)[:n] + torch.randn(n, 3, generator=g) * 0.1
+    query = torch.rand(131072, 3, generator=g) * 100
+    return ref[None].contiguous(), query[None].contiguous()
+
+
 def make_c4(seed: int = 4) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Config 4: ref 1,048,576 and 131,072 queries uniform in [0,10]^3, plus
     DGCNN features randn(8, 2048, 64)."""
@@ -445,16 +458,30 @@ def run_other(args) -> dict:
                    ops_ms={"fps": t_fps * 1e3, "ball_query": t_ball * 1e3},
                    tops={"fps": fps_ops / t_fps / 1e12, "ball_query": ball_ops / t_ball / 1e12})
     elif args.config == "c4":
+        from mps_pointops import _native
+
         ref, query, feat = (t.to(dev) for t in make_c4())
         r = max(1, reps // 5)
         t_knn = timer.time(lambda: mp.knn(query, ref, 16), r)
         t_feat = timer.time(lambda: mp.knn(feat, feat, 20), reps)
         M, N = query.shape[1], ref.shape[1]
         Bf, Nf, D = feat.shape
+        # The same sizes on clustered references with uniform queries, through
+        # the public call (grid search, far queries left to the linear pass)
+        # and through the brute-force kernel alone, for comparison.
+        cref, cquery = (t.to(dev) for t in make_c4_clustered())
+        t_clustered = timer.time(lambda: mp.knn(cquery, cref, 16), r)
+        bd = torch.empty(1, M, 16, device=dev)
+        bi = torch.empty(1, M, 16, dtype=torch.long, device=dev)
+        t_brute = timer.time(lambda: _native.call(
+            "pointops_knn3", cquery.data_ptr(), cref.data_ptr(), bd.data_ptr(), bi.data_ptr(),
+            1, M, N, 16, _native.stream(dev)), 1)
         out.update(metric="queries/sec for exact kNN16, 131072 queries x 1048576 refs",
                    value=M / t_knn, unit="queries/s",
                    config={"workload": "c4 kNN at scale + DGCNN feature kNN (8,2048,64) K=20"},
-                   ops_ms={"knn": t_knn * 1e3, "dgcnn_feature_knn": t_feat * 1e3},
+                   ops_ms={"knn": t_knn * 1e3, "dgcnn_feature_knn": t_feat * 1e3,
+                           "knn_clustered_uniform_queries": t_clustered * 1e3,
+                           "knn_clustered_brute_force_kernel": t_brute * 1e3},
                    knn_path="grid search (knn_grid.hip): examines the cells around each query, "
                             "not all M x N pairs",
                    tops={"knn_brute_force_equivalent": PAIR_OPS * M * N / t_knn / 1e12,

@@ -19,9 +19,10 @@
 //      3 x 3 x 3 box of cells around its own query and stops once its K-th
 //      squared distance is below that of the nearest unscanned cell face,
 //      less a slack for float rounding (box_bound), else grows the box by
-//      that face.  A non-finite query, a batch with
-//      non-finite references, or a lane that needs more than kGridMaxGrow
-//      faces make the wave scan every reference.
+//      that face.  A non-finite query or a batch with non-finite
+//      references lists the wave's queries, a walk that needs more than
+//      kGridMaxGrow faces its own query, for a linear pass in the same call
+//      (knn3_lane_listed: the brute-force lane kernel over the listed rows).
 #include <algorithm>
 
 #include "pointops_common.hpp"
@@ -621,11 +622,8 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     // (the admission bound) is always the last rank.  Inactive quads hold
     // zeros and admit nothing.
     uint64_t slot[S];
-    auto reset = [&]() {
 #pragma unroll
-        for (int s = 0; s < S; ++s) slot[s] = (active && S * qi + s >= KMAX - K) ? ~0ull : 0ull;
-    };
-    reset();
+    for (int s = 0; s < S; ++s) slot[s] = (active && S * qi + s >= KMAX - K) ? ~0ull : 0ull;
     uint64_t tau = active ? ~0ull : 0ull;
     int cnt = 0;
 
@@ -651,7 +649,11 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     };
 
     const bool qfinite = finite3(q[0], q[1], q[2]);
-    bool full = P.nonfinite > 0 || ballot(active && !qfinite) != 0;
+    // Queries left to the linear pass: the whole wave when the batch has
+    // non-finite references or the wave a non-finite query, else the quads
+    // whose walk needs more faces than the mode allows.
+    const bool full = P.nonfinite > 0 || ballot(active && !qfinite) != 0;
+    bool listed = false;
     if (!full) {
         // The quad scans the box around its query, 32 references of its
         // current segment per step (lane j of the quad takes every fourth
@@ -660,7 +662,7 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
         // copies of the walk's state.  When the box is done the quad stops if
         // its K-th key is below the squared bound of everything outside;
         // otherwise it grows the box by its nearest face.  A quad that needs
-        // more than kGridMaxGrow faces sends the wave to the full scan.
+        // more faces than its mode's limit is listed for the linear pass.
         const float h = 1.f / P.inv_h;
         int c[3];
         GridBox X;
@@ -684,7 +686,6 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             want = false;
             int qc = cnt | dpp<kDppQuadXor1>(cnt);
             qc |= dpp<kDppQuadXor2>(qc);
-            bool escalate = false;
             while (!done && !want && p >= e) {  // uniform within each quad
                 const int nseg = box_segments(X, face);
                 if (g < nseg) {
@@ -702,7 +703,7 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
                 } else if (qc != 0) {
                     want = true;  // merge first, then check again
                 } else if (grow == (nearest ? kGridNearestGrow : kGridMaxGrow)) {
-                    escalate = true;
+                    listed = true;
                     done = true;
                 } else {
                     float best = INFINITY;
@@ -726,10 +727,6 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
                     fetch();
                 }
             }
-            if (ballot(escalate) != 0) {
-                full = true;
-                break;
-            }
             if (ballot(!done) == 0) break;
             const bool has = p < e;
             const int base = has ? p + qi : 0, last = has ? e - 1 : 0;
@@ -740,31 +737,18 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             if (has) p += 32;
         }
     }
-    if (full && nearest) {
-        // Nearest mode appends such queries to its cloud's list for the
-        // linear-scan pass (nearest_fill_kernel), which writes their results.
-        if (active && qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
-        return;
-    }
+    // A listed query goes to its cloud's list (one atomic per query), and the
+    // linear pass of the same call writes its results.
     if (full) {
-        // Every reference (the finite ones and the overflow cell), 32 per
-        // step per quad.  A list may hold references already, so start over
-        // rather than insert duplicates.
-        reset();
-        tau = active ? ~0ull : 0ull;
-        cnt = 0;
-        const int hi = off[P.cells + 1];
-        for (int g0 = 0; g0 < hi; g0 += 32) {
-            drain(false);
-            const int base = g0 + qi;
-            float4 rv[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) rv[u] = srt[min(base + 4 * u, hi - 1)];
-            admit8s(rv, hi - base);
-        }
+        if (active && qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
+        return;  // whole wave
     }
     quad_merge<S>(slot, tau, buf, lane, cnt);
     if (!active) return;
+    if (listed) {
+        if (qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
+        return;
+    }
     const int64_t row = (b * M + m) * K;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -1086,24 +1070,32 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     if (B < 0 || M < 0 || N < 0 || K < 0 || K > 32 || K > N) return hipErrorInvalidValue;
     if (B == 0 || M == 0 || K == 0) return hipSuccess;
     if (N >= (int64_t(1) << 31) - 64 || M >= (int64_t(1) << 31) - 64 || B > 65535 ||
-        workspace == nullptr)
+        workspace == nullptr || (M + kWave - 1) / kWave * B > INT32_MAX)
         return hipErrorInvalidValue;
     dim3 grid;
     if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     grid_build(query, ref, L, B, M, N, static_cast<int>(K), 0.f, stream);
+    // The build's scan totals and query ranks are dead once the queries are
+    // placed: they hold the per-cloud counts and lists of listed queries.
+    int* miss_count = L.tile_sum;  // B * 2 * tiles >= B ints
+    int* miss_list = L.q_rank;     // B * M ints
+    hipLaunchKernelGGL(grid_zero_kernel, dim3(static_cast<uint32_t>((B + 255) / 256)), dim3(256), 0,
+                       stream, miss_count, B);
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
-        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
+        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
     else if (K <= 8)
-        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
+        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
     else if (K <= 16)
-        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
+        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
     else
-        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, nullptr, nullptr);
-    return hipGetLastError();
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    return knn3_lane_listed(query, ref, dist, idx, B, M, N, k, miss_count, miss_list, stream);
 }
 
 hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* dist2,

@@ -512,6 +512,29 @@ def test_knn3_grid_matches_oracle(cuda_device, name, k):
     same_bits(d, want_d)
 
 
+@pytest.mark.parametrize("k", [1, 16, 32])
+def test_knn3_grid_listed_far_queries(cuda_device, k):
+    """Tight clusters queried both on the clusters and uniformly over their
+    box, shuffled, so that the walk lists some quads of a wave for the linear
+    pass and finishes the others: every row equals the brute-force answer,
+    in two batches with different mixes."""
+    g = torch.Generator().manual_seed(40 + k)
+    refs, queries = [], []
+    for b in range(2):
+        centres = torch.rand(10, 3, generator=g) * 100
+        ref = centres.repeat_interleave(4000, 0) + torch.randn(40_000, 3, generator=g) * 0.1
+        near = ref[torch.randperm(40_000, generator=g)[: 1500 + 1000 * b]]
+        far = torch.rand(2500 - 1000 * b, 3, generator=g) * 100
+        both = torch.cat([near, far])
+        refs.append(ref)
+        queries.append(both[torch.randperm(4000, generator=g)])
+    query, ref = torch.stack(queries), torch.stack(refs)
+    want_d, want_i = O.knn3(query, ref, k)
+    d, i = _knn3_grid(query, ref, k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
+
+
 def test_knn3_grid_public_path(cuda_device):
     """ops.knn uses the grid search for large clouds; results match the
     brute-force kernel on the same inputs."""
