@@ -452,11 +452,18 @@ def run_other(args) -> dict:
         t_ball = timer.time(lambda: mp.ball_query(c, x, 0.5, 32), r)
         fps_ops = FPS_OPS_PER_POINT_STEP * 16384 * N
         ball_ops = PAIR_OPS * ball_scanned_pairs(mp.ball_query(c, x, 0.5, 32)[1], N)
+        # Beside the metric: the same slab generator at 4x the points, which
+        # takes the streaming kernel (above 2^21 points).
+        x4 = make_c3(N=1 << 22).to(dev)
+        t_fps4 = timer.time(lambda: mp.furthest_point_sample(x4, 16384), r)
         out.update(metric="points/sec for FPS16384+ball(0.5,32) at B=1,N=1048576",
                    value=N / (t_fps + t_ball), unit="points/s",
                    config={"workload": "c3 large single-cloud FPS (LiDAR-like slab) + ball query"},
-                   ops_ms={"fps": t_fps * 1e3, "ball_query": t_ball * 1e3},
-                   tops={"fps": fps_ops / t_fps / 1e12, "ball_query": ball_ops / t_ball / 1e12})
+                   ops_ms={"fps": t_fps * 1e3, "ball_query": t_ball * 1e3,
+                           "fps_4194304_points_streaming": t_fps4 * 1e3},
+                   tops={"fps": fps_ops / t_fps / 1e12, "ball_query": ball_ops / t_ball / 1e12,
+                         "fps_4194304_points_streaming":
+                             FPS_OPS_PER_POINT_STEP * 16384 * (1 << 22) / t_fps4 / 1e12})
     elif args.config == "c4":
         from mps_pointops import _native
 

@@ -46,11 +46,16 @@ hipError_t pointops_fps_dense(const float *xyz, int64_t *out, void *scratch, int
                               int64_t N, int64_t npoint, int64_t start_idx,
                               int32_t skip_near_origin, hipStream_t stream);
 
-/* Large single-cloud FPS (B = 1): one persistent cooperative launch over all
- * CUs with a per-step device-wide argmax.  Replaces the 2*(npoint-1)
- * dispatch loop of ops.py:119-136 (kernels/fps_multigroup.metal:10-133).
- * `workspace` must hold pointops_fps_large_workspace_bytes(N, npoint) bytes
- * and be zero-filled by the caller before every call. */
+/* Large single-cloud FPS (B = 1, 1 <= N <= 2^32 - 1): one persistent
+ * cooperative launch over all CUs exchanging per-wave candidates every few
+ * steps.  Up to 2^21 points the cloud lives in registers; above, each
+ * exchange streams it from HBM with the running distances in the workspace.
+ * Replaces the 2*(npoint-1) dispatch loop of ops.py:119-136
+ * (kernels/fps_multigroup.metal:10-133).  `workspace` must hold
+ * pointops_fps_large_workspace_bytes(N, npoint) bytes (4 bytes per point
+ * more above 2^21 points) and be zero-filled by the caller before every
+ * call; afterwards its first 32-bit word is non-zero if the kernel gave up
+ * waiting for a workgroup (then every output slot not written holds -1). */
 size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint);
 hipError_t pointops_fps_large(const float *xyz, int64_t *out, void *workspace, int64_t N,
                               int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
@@ -61,8 +66,8 @@ hipError_t pointops_fps_large(const float *xyz, int64_t *out, void *workspace, i
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc).  The workspace is a 640 KiB array in the library's
  * device memory, one per GPU, held until the process ends; each call clears
- * it with a fill kernel on `stream` before the launch.  Limits as
- * pointops_fps_large: 1 <= N <= 2^21 points, else hipErrorInvalidValue
+ * it with a fill kernel on `stream` before the launch.  Limit: 1 <= N <=
+ * 2^21 points (the clouds that fit in registers), else hipErrorInvalidValue
  * before anything is enqueued.  Calls that overlap on one GPU (several
  * streams or host threads) share the array and race: serialise them.  A give-up
  * of the kernel shows as -1 in every output slot it did not write. */

@@ -802,6 +802,253 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
     }
 }
 
+// fps_stream_kernel<T>: the same lazy exchange for clouds too large for the
+// registers of the chip (more than 2^21 points; up to 2^32 - 1).  Workgroup
+// g owns points [g*chunk, min(N, g*chunk + chunk)) and keeps their running
+// distances in `md` (HBM, N floats, written on the first exchange): every
+// exchange streams its chunk once -- coordinates and running distances in,
+// the pending centroids applied, running distances out -- and each wave
+// keeps, per lane, its largest running distance (smallest index on ties)
+// with that point, and its second largest value.  The wave's candidate is
+// the largest of its lanes' (smallest index on ties) and its bound the
+// largest of the other lanes' maxima and the winner's second value, i.e. the
+// largest running distance of every point it did not publish.  Records are
+// those of fps_lazy_kernel (kLazyCand = 1) with the index split over two
+// words: bits 0-20 beside the key, bits 21-31 beside x.
+constexpr int kStreamUnroll = 8;  // points per thread per batch (two batches in flight)
+constexpr int64_t kStreamMaxN = (int64_t(1) << 32) - 1;  // indices below 2^32 - 1
+
+template <int T>
+__global__ __launch_bounds__(T) void fps_stream_kernel(
+    const float* __restrict__ xyz, float* __restrict__ md, int64_t* __restrict__ out,
+    uint64_t* __restrict__ records, uint32_t* __restrict__ status, int64_t N, int64_t npoint,
+    int64_t start, int skip, int64_t chunk, uint32_t spin_limit) {
+    constexpr int NW = T / kWave;
+    static_assert(NW <= 8 && kLazyCand == 1, "shape");
+    constexpr int RPT = kLazyMaxWaves / T;  // records read per thread at most
+    __shared__ float4 pend[kLazyMaxPending];
+    __shared__ WaveBest slots[2][8];
+    __shared__ int wave_bound[NW];
+    __shared__ int abort_flag;
+
+    const int G = gridDim.x;
+    const int waves = G * NW;
+    const int g = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int wave = tid / kWave;
+    const int lane = tid % kWave;
+    const int64_t lo = static_cast<int64_t>(g) * chunk;
+    const int64_t hi = min(N, lo + chunk);
+    if (tid == 0) {
+        abort_flag = 0;
+        pend[0] = make_float4(xyz[3 * start], xyz[3 * start + 1], xyz[3 * start + 2], 0.f);
+        if (g == 0) out[0] = start;
+    }
+    int npend = 1;
+    int64_t step = 1;
+    int sim_par = 0;
+    for (uint32_t exch = 0; step < npoint; ++exch) {
+        __syncthreads();  // pend[] complete
+        // Stream the chunk: apply the pending centroids, keep this lane's
+        // best point (running distance, index, xyz) and its second value.
+        int bv = static_cast<int>(0x80000000u), sv = static_cast<int>(0x80000000u);
+        uint32_t bi = 0xFFFFFFFFu;  // indices are below 2^32 - 1
+        float bx = 0.f, by = 0.f, bz = 0.f;
+        // Software-pipelined: the next batch's loads (clamped, so always in
+        // bounds) are issued before the current batch is computed.
+        constexpr int64_t kBatch = static_cast<int64_t>(kStreamUnroll) * T;
+        float x[kStreamUnroll], y[kStreamUnroll], z[kStreamUnroll], m[kStreamUnroll];
+        auto fetch = [&](int64_t j0, float (&fx)[kStreamUnroll], float (&fy)[kStreamUnroll],
+                         float (&fz)[kStreamUnroll], float (&fm)[kStreamUnroll]) {
+#pragma unroll
+            for (int u = 0; u < kStreamUnroll; ++u) {
+                const int64_t j = min(j0 + static_cast<int64_t>(u) * T, hi - 1);
+                fx[u] = xyz[3 * j];
+                fy[u] = xyz[3 * j + 1];
+                fz[u] = xyz[3 * j + 2];
+                fm[u] = exch == 0 ? 0.f : md[j];
+            }
+        };
+        if (lo + tid < hi) fetch(lo + tid, x, y, z, m);
+        for (int64_t j0 = lo + tid; j0 < hi; j0 += kBatch) {
+            float nx[kStreamUnroll], ny[kStreamUnroll], nz[kStreamUnroll], nm[kStreamUnroll];
+            fetch(j0 + kBatch, nx, ny, nz, nm);
+            float v[kStreamUnroll];
+#pragma unroll
+            for (int u = 0; u < kStreamUnroll; ++u)
+                v[u] = exch != 0 ? m[u]
+                                 : ((skip && near_origin(x[u], y[u], z[u])) ? -INFINITY : INFINITY);
+            for (int i = 0; i < npend; ++i) {  // each centroid read once per batch
+                const float4 c = pend[i];
+#pragma unroll
+                for (int u = 0; u < kStreamUnroll; ++u)
+                    v[u] = running_min(v[u], sqdist3(x[u], y[u], z[u], c.x, c.y, c.z));
+            }
+#pragma unroll
+            for (int u = 0; u < kStreamUnroll; ++u) {
+                const int64_t j = j0 + static_cast<int64_t>(u) * T;
+                if (j >= hi) break;  // uniform per thread; j grows with u
+                md[j] = v[u];
+                const int key = f2i(v[u]);  // -inf orders below every distance
+                // Indices grow along this thread's walk: strict `>` keeps the
+                // smallest index among equal values.
+                if (key > bv) {
+                    sv = bv;
+                    bv = key;
+                    bi = static_cast<uint32_t>(j);
+                    bx = x[u];
+                    by = y[u];
+                    bz = z[u];
+                } else {
+                    sv = max(sv, key);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < kStreamUnroll; ++u) {
+                x[u] = nx[u];
+                y[u] = ny[u];
+                z[u] = nz[u];
+                m[u] = nm[u];
+            }
+        }
+        npend = 0;
+
+        // The wave's candidate (largest value, then smallest index) and bound.
+        const int wv = wave_max_i32_l63(bv);
+        const uint32_t ci = bv == wv ? bi : 0xFFFFFFFFu;
+        const uint32_t gidx = ~wave_max_u32_l63(~ci);  // smallest index holding wv
+        const int wl = static_cast<int>(__builtin_ctzll(ballot(bv == wv && ci == gidx)));
+        const int other = lane == wl ? sv : bv;
+        const int bound_w = wave_max_i32_l63(other);
+        const uint32_t tag = (exch & 0x3FFu) | 0x400u;
+        const int gw = g * NW + wave;
+        uint64_t words[kLazyRecWords];
+        words[0] = (static_cast<uint64_t>(static_cast<uint32_t>(wv)) << 32) |
+                   (static_cast<uint64_t>(tag) << kLargeIdxBits) | (gidx & kLargeIdxMask);
+        words[1] = (static_cast<uint64_t>(static_cast<uint32_t>(readlane(f2i(bx), wl))) << 32) |
+                   (static_cast<uint64_t>(gidx >> kLargeIdxBits) << 11) | tag;
+        words[2] = (static_cast<uint64_t>(static_cast<uint32_t>(readlane(f2i(by), wl))) << 32) | tag;
+        words[3] = (static_cast<uint64_t>(static_cast<uint32_t>(readlane(f2i(bz), wl))) << 32) | tag;
+        words[4] = (static_cast<uint64_t>(static_cast<uint32_t>(bound_w)) << 32) | tag;
+        const int par = static_cast<int>(exch & 1);
+        uint64_t* base = records + static_cast<int64_t>(par) * kLargeReplicas * kLazyCopyWords;
+        if (lane < kLargeReplicas) {
+            uint64_t* rec = base + lane * kLazyCopyWords + gw;
+#pragma unroll
+            for (int w = 0; w < kLazyRecWords; ++w)
+                __hip_atomic_store(rec + static_cast<int64_t>(w) * kLazyMaxWaves, words[w],
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+
+        // Read every wave's record (copy g % kLargeReplicas).
+        const uint64_t* copy = base + (g % kLargeReplicas) * kLazyCopyWords;
+        int cmd[RPT];
+        uint32_t cidx[RPT];
+        float cx_[RPT], cy_[RPT], cz_[RPT];
+        int bmax = static_cast<int>(0x80000000u);
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            const int rw = tid + r * T;
+            cmd[r] = static_cast<int>(0x80000000u);
+            cidx[r] = 0xFFFFFFFFu;
+            cx_[r] = cy_[r] = cz_[r] = 0.f;
+            if (rw >= waves) continue;
+            const uint64_t* q = copy + rw;
+            for (uint32_t spins = 0;; ++spins) {
+                if (poll_give_up(status, spins, spin_limit)) {
+                    abort_flag = 1;
+                    break;
+                }
+                const uint64_t wb = __hip_atomic_load(q + static_cast<int64_t>(kLazyRecWords - 1) * kLazyMaxWaves,
+                                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                if (static_cast<uint32_t>(wb) != tag) continue;
+                uint64_t rw_[kLazyRecWords - 1];
+#pragma unroll
+                for (int w = 0; w < kLazyRecWords - 1; ++w)
+                    rw_[w] = __hip_atomic_load(q + static_cast<int64_t>(w) * kLazyMaxWaves,
+                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const bool ok = static_cast<uint32_t>((rw_[0] >> kLargeIdxBits) & 0x7FFu) == tag &&
+                                (static_cast<uint32_t>(rw_[1]) & 0x7FFu) == tag &&
+                                static_cast<uint32_t>(rw_[2]) == tag &&
+                                static_cast<uint32_t>(rw_[3]) == tag;
+                if (!ok) continue;
+                bmax = max(bmax, static_cast<int>(wb >> 32));
+                cmd[r] = static_cast<int>(rw_[0] >> 32);
+                cidx[r] = static_cast<uint32_t>(rw_[0] & kLargeIdxMask) |
+                          (((static_cast<uint32_t>(rw_[1]) >> 11) & 0x7FFu) << kLargeIdxBits);
+                cx_[r] = i2f(static_cast<int>(rw_[1] >> 32));
+                cy_[r] = i2f(static_cast<int>(rw_[2] >> 32));
+                cz_[r] = i2f(static_cast<int>(rw_[3] >> 32));
+                break;
+            }
+        }
+        bmax = wave_max_i32_l63(bmax);
+        if (lane == 0) wave_bound[wave] = bmax;
+        __syncthreads();
+        if (abort_flag) {  // uniform: written before the barrier
+            if (g == 0)
+                for (int64_t s = step + tid; s < npoint; s += T) out[s] = -1;
+            return;
+        }
+        int bound = wave_bound[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) bound = max(bound, wave_bound[w]);
+
+        // Steps over the candidates alone (as in fps_lazy_kernel).
+        for (bool first = true; step < npoint; first = false) {
+            int sbv = static_cast<int>(0x80000000u);
+            uint32_t sbi = 0xFFFFFFFFu;
+            float sx = 0.f, sy = 0.f, sz = 0.f;
+#pragma unroll
+            for (int r = 0; r < RPT; ++r) {
+                const bool better = cmd[r] > sbv || (cmd[r] == sbv && cidx[r] < sbi);
+                sbv = better ? cmd[r] : sbv;
+                sbi = better ? cidx[r] : sbi;
+                sx = better ? cx_[r] : sx;
+                sy = better ? cy_[r] : sy;
+                sz = better ? cz_[r] : sz;
+            }
+            const int swv = wave_max_i32_l63(sbv);
+            const uint32_t sci = sbv == swv ? sbi : 0xFFFFFFFFu;
+            const uint32_t cmin = ~wave_max_u32_l63(~sci);
+            const int swl = static_cast<int>(__builtin_ctzll(ballot(sbv == swv && sci == cmin)));
+            WaveBest* buf = slots[sim_par];
+            sim_par ^= 1;
+            const float wx = i2f(readlane(f2i(sx), swl));
+            const float wy = i2f(readlane(f2i(sy), swl));
+            const float wz = i2f(readlane(f2i(sz), swl));
+            if (lane == 0) {
+                WaveBest e;
+                e.key = swv;
+                e.index = static_cast<int>(cmin);  // bit pattern of the uint32 index
+                e.x = wx;
+                e.y = wy;
+                e.z = wz;
+                e.pad[0] = e.pad[1] = e.pad[2] = 0;
+                buf[wave] = e;
+            }
+            __syncthreads();
+            WaveBest best = buf[0];
+#pragma unroll
+            for (int w = 1; w < NW; ++w) {
+                const WaveBest e = buf[w];
+                if (e.key > best.key ||
+                    (e.key == best.key && static_cast<uint32_t>(e.index) < static_cast<uint32_t>(best.index)))
+                    best = e;
+            }
+            if (!first && !(best.key > bound)) break;  // an unpublished point may tie or beat it
+            if (g == 0 && tid == 0) out[step] = static_cast<int64_t>(static_cast<uint32_t>(best.index));
+            if (tid == 0) pend[npend] = make_float4(best.x, best.y, best.z, 0.f);
+            ++npend;
+            ++step;
+#pragma unroll
+            for (int r = 0; r < RPT; ++r)
+                cmd[r] = f2i(running_min(i2f(cmd[r]), sqdist3(cx_[r], cy_[r], cz_[r], best.x, best.y, best.z)));
+            if (npend == kLazyMaxPending) break;
+        }
+    }
+}
+
 // ------------------------------------------------------------ dispatch
 
 constexpr int kRegsThreads = 512;  // 8 waves: two per SIMD hide each other's reduction latency
@@ -852,6 +1099,28 @@ uint32_t spin_limit() {
     const char* env = std::getenv("POINTOPS_FPS_SPIN_LIMIT");
     if (env == nullptr || *env == '\0') return kSpinLimit;
     return static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
+}
+
+// The streaming kernel over one workgroup per CU (at most kLargeMaxGrid).
+constexpr int kStreamThreads = kLargeThreads;
+
+hipError_t launch_stream(const float* xyz, float* md, int64_t* out, uint64_t* records,
+                         uint32_t* status, int64_t N, int64_t npoint, int64_t start, int skip,
+                         int device, hipStream_t stream) {
+    const void* kernel = reinterpret_cast<const void*>(&fps_stream_kernel<kStreamThreads>);
+    int per_cu = 0, cus = 0;
+    hipError_t err = hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kStreamThreads, 0);
+    if (err != hipSuccess) return err;
+    err = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device);
+    if (err != hipSuccess) return err;
+    if (per_cu < 1 || cus < 1) return hipErrorInvalidValue;
+    int grid = min(cus, kLargeMaxGrid);
+    int64_t chunk = (N + grid - 1) / grid;
+    uint32_t limit = spin_limit();
+    void* args[] = {(void*)&xyz, (void*)&md, (void*)&out, (void*)&records, (void*)&status,
+                    (void*)&N, (void*)&npoint, (void*)&start, (void*)&skip, (void*)&chunk,
+                    (void*)&limit};
+    return hipLaunchCooperativeKernel(kernel, dim3(grid), dim3(kStreamThreads), args, 0, stream);
 }
 
 template <int P>
@@ -957,7 +1226,8 @@ hipError_t pointops_fps_flat(const float* x, const int64_t* ptr, const int64_t* 
 size_t pointops_fps_large_workspace_bytes(int64_t N, int64_t npoint) {
     (void)npoint;
     if (N <= 0) return 0;
-    return kLargeWorkspaceBytes;
+    if (N <= kLargeMaxN) return kLargeWorkspaceBytes;
+    return kLargeWorkspaceBytes + static_cast<size_t>(N) * sizeof(float);  // running distances
 }
 
 }  // extern "C"
@@ -968,11 +1238,11 @@ namespace {
 // Checks shared by both large-cloud entry points; hipSuccess with *run = false
 // when there is nothing to do.
 hipError_t check_large(const float* xyz, const int64_t* out, int64_t N, int64_t npoint,
-                       int64_t start_idx, bool* run) {
+                       int64_t start_idx, int64_t max_n, bool* run) {
     *run = false;
     if (N < 0 || npoint < 0) return hipErrorInvalidValue;
     if (npoint == 0) return hipSuccess;
-    if (N == 0 || N > kLargeMaxN || start_idx < 0 || start_idx >= N) return hipErrorInvalidValue;
+    if (N == 0 || N > max_n || start_idx < 0 || start_idx >= N) return hipErrorInvalidValue;
     if (xyz == nullptr || out == nullptr) return hipErrorInvalidValue;
     *run = true;
     return hipSuccess;
@@ -986,6 +1256,11 @@ hipError_t launch_large_any(const float* xyz, int64_t* out, void* workspace, int
                             hipStream_t stream) {
     auto* status = static_cast<uint32_t*>(workspace);
     auto* records = reinterpret_cast<uint64_t*>(static_cast<char*>(workspace) + 256);
+    if (N > kLargeMaxN) {  // running distances after the records
+        auto* md = reinterpret_cast<float*>(static_cast<char*>(workspace) + kLargeWorkspaceBytes);
+        return launch_stream(xyz, md, out, records, status, N, npoint, start_idx, skip, device,
+                             stream);
+    }
     const int n32 = static_cast<int>(N);
     const int s32 = static_cast<int>(start_idx);
     const int choices[] = {1, 2, 4, 8, 16, 32};
@@ -1026,7 +1301,7 @@ hipError_t pointops_fps_large(const float* xyz, int64_t* out, void* workspace, i
                               int64_t npoint, int64_t start_idx, int32_t skip_near_origin,
                               hipStream_t stream) {
     bool run = false;
-    hipError_t err = check_large(xyz, out, N, npoint, start_idx, &run);
+    hipError_t err = check_large(xyz, out, N, npoint, start_idx, kStreamMaxN, &run);
     if (err != hipSuccess || !run) return err;
     if (workspace == nullptr) return hipErrorInvalidValue;
     int device = 0;
@@ -1040,7 +1315,7 @@ hipError_t pointops_fps_large_noalloc(const float* xyz, int64_t* out, int64_t N,
                                       int64_t start_idx, int32_t skip_near_origin,
                                       hipStream_t stream) {
     bool run = false;
-    hipError_t err = check_large(xyz, out, N, npoint, start_idx, &run);
+    hipError_t err = check_large(xyz, out, N, npoint, start_idx, kLargeMaxN, &run);
     if (err != hipSuccess || !run) return err;
     int device = 0;
     err = hipGetDevice(&device);

@@ -18,7 +18,8 @@ from ._ball_query import _checked_radius_and_k, ball_query as _native_ball_query
 
 # Largest cloud the single-launch large-cloud FPS path addresses (21-bit index
 # in its per-step records).
-_FPS_LARGE_MAX_N = 1 << 21
+# The persistent kernel's index range (ops.py:108-109): fewer than 2**32 points.
+_FPS_LARGE_MAX_N = (1 << 32) - 1
 # One cloud with at least this many points uses the all-CU persistent kernel
 # under strategy="auto"; smaller clouds fit one workgroup's registers and LDS.
 _FPS_MULTIGROUP_MIN_N = 65_536
@@ -101,9 +102,7 @@ def furthest_point_sample(
         strategy == "multigroup" or (strategy == "auto" and N >= _FPS_MULTIGROUP_MIN_N)
     )
     if use_large and N > _FPS_LARGE_MAX_N:
-        if strategy == "multigroup":
-            raise ValueError(f"multigroup FPS requires at most {_FPS_LARGE_MAX_N} points")
-        use_large = False
+        raise ValueError("multigroup FPS requires fewer than 2**32 points")
     out = torch.empty((B, npoint), dtype=torch.long, device=xyz.device)
     if B == 0 or npoint == 0:
         return out

@@ -55,7 +55,7 @@ def test_capi_rejects_bad_arguments_before_any_launch():
     assert lib.pointops_knn_feat(None, None, None, None, 1, 1, 10, 0, 3, None) == 1  # D == 0
     assert lib.pointops_fps_dense(None, None, None, 1, 10, 4, 10, 0, None) == 1  # start >= N
     assert lib.pointops_fps_dense(None, None, None, 2, 0, 0, 0, 0, None) == 0    # npoint == 0
-    assert lib.pointops_fps_large(None, None, None, (1 << 21) + 1, 4, 0, 0, None) == 1
+    assert lib.pointops_fps_large(None, None, None, 1 << 32, 4, 0, 0, None) == 1
     assert lib.pointops_three_nn(None, None, None, None, 1, 5, 2, None) == 1     # M < 3
     assert lib.pointops_ball_query_f32(None, None, None, None, None, None, 1, 1, 1, -1,
                                        ctypes.c_float(1.0), None) == 1
@@ -71,6 +71,9 @@ def test_scratch_size_queries():
     assert _native.size_query("pointops_fps_dense_scratch_bytes", 2, 100_000) == 2 * 100_000 * 4
     assert _native.size_query("pointops_fps_flat_scratch_bytes", 50_000, 9000) == 50_000 * 4
     assert _native.size_query("pointops_fps_large_workspace_bytes", 1 << 20, 16384) > 0
+    # Above 2^21 points the running distances live in the workspace too.
+    small = _native.size_query("pointops_fps_large_workspace_bytes", 1 << 21, 16)
+    assert _native.size_query("pointops_fps_large_workspace_bytes", 3 << 20, 16) == small + (3 << 22)
 
 
 # ------------------------------------------------------------ public API

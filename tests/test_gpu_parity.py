@@ -287,6 +287,55 @@ def test_fps_large_forced_give_up_is_reported(cuda_device, monkeypatch):
     np.testing.assert_array_equal(got, O.fps(xyz, 300, 11)[0])
 
 
+@pytest.mark.parametrize("case", ["random", "ties", "exhausted", "mostly_skipped", "last_start"])
+def test_fps_stream_matches_oracle(cuda_device, case):
+    """Clouds above 2^21 points (the streaming kernel, running distances in
+    the workspace): a random cloud, duplicated points (ties by index), a run
+    past the number of distinct points, a cloud whose points are nearly all
+    skipped, and a start at the last index of an odd-sized cloud."""
+    import mps_pointops as mp
+
+    g = torch.Generator().manual_seed(900 + len(case))
+    n = (1 << 21) + 4099
+    skip = case == "mostly_skipped"
+    start = 12345
+    npoint = 300
+    if case == "random":
+        xyz = torch.randn(1, n, 3, generator=g)
+    elif case == "ties":
+        xyz = torch.randn(1, n, 3, generator=g)
+        xyz[0, : n // 3] = xyz[0, n // 3: 2 * (n // 3)]
+    elif case == "exhausted":
+        base = torch.randn(250, 3, generator=g)
+        xyz = base[torch.randint(0, 250, (n,), generator=g)][None].contiguous()
+    elif case == "mostly_skipped":
+        xyz = torch.randn(1, n, 3, generator=g) * 1e-3
+        xyz[0, ::40_000] = torch.randn(xyz[0, ::40_000].shape[0], 3, generator=g)
+        npoint, start = 120, 0
+    else:
+        n = 3_000_001
+        xyz = torch.rand(1, n, 3, generator=g)
+        start = n - 1
+    print(f"fps stream case={case} n={n} npoint={npoint}", flush=True)
+    want = O.fps(xyz, npoint, start, skip)
+    got = mp.furthest_point_sample(xyz.cuda(), npoint, start, skip)
+    np.testing.assert_array_equal(host(got), want)
+
+
+def test_fps_stream_status_and_forced_give_up(cuda_device, monkeypatch):
+    """The streaming kernel reports success in the status word, and a poll
+    limit of 0 (set from the host) makes it give up at its first exchange
+    with every later slot -1; every wave exits normally."""
+    xyz = rand_cloud(1, (1 << 21) + 1, 8)
+    got, status = _fps_large_abi(xyz, 200, 17)
+    assert status == 0
+    np.testing.assert_array_equal(got, O.fps(xyz, 200, 17)[0])
+    monkeypatch.setenv("POINTOPS_FPS_SPIN_LIMIT", "0")
+    got, status = _fps_large_abi(xyz, 200, 17)
+    assert status == 1
+    assert got[0] == 17 and (got[1:] == -1).all()
+
+
 @pytest.mark.parametrize("n,distinct", [(4096, 300), (1000, 40), (8192, 3000)])
 def test_fps_dense_repeated_points(cuda_device, n, distinct):
     """Clouds built from few distinct points (equal distances everywhere, and
