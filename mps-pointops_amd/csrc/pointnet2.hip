@@ -16,6 +16,8 @@
 // per-batch CSR of the entries (deterministic, no float atomics) where the
 // shape allows, else accumulates into LDS rows with LDS float atomics, or
 // into memory with hardware float atomics.
+#include <algorithm>
+
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -370,11 +372,13 @@ __global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_g
 
 // Backward over a CSR of the entries, for M <= 4096 known points and
 // N <= 4096 unknowns (N a multiple of 4), with a caller workspace:
-//   three_interp_csr_kernel (one workgroup per batch): counting sort of the
-//   entry ids e = 3n + t by known index m = idx[b,n,t] in LDS; an entry's
-//   place in its bucket is the number of smaller ids there, so each bucket
-//   lists its entries in ascending order; the sorted ids and the bucket
-//   starts are copied out with coalesced stores.
+//   three_interp_csr_kernel (per batch, R workgroups, each owning a range
+//   of known indices): every workgroup reads all of the batch's entries,
+//   counts those below its range (its offset in the CSR) and counting-sorts
+//   the entry ids e = 3n + t of its range by known index m = idx[b,n,t] in
+//   LDS; an entry's place in its bucket is the number of smaller ids there,
+//   so each bucket lists its entries in ascending order; the sorted ids, their
+//   weights and the bucket starts are copied out with coalesced stores.
 //   three_interp_backward_csr_kernel (one workgroup per batch and block of
 //   kTiCsrBlock channels): stages the batch's CSR once (ids, starts and each
 //   entry's weight, gathered by id), then walks its channels CG at a time
@@ -392,6 +396,7 @@ constexpr int kTiCsrBlock = 16;                    // channels per gather workgr
 constexpr int kTiCsrLdsBytes = 160 * 1024 - 1024;  // gather LDS budget
 constexpr int kTiCsrStage = 8;                     // 16-byte chunks a thread stages at once
 constexpr int kTiCsrRegEntries = 16;               // list entries a gather thread keeps in registers
+constexpr int kTiCsrRanges = 8;                    // build workgroups per batch at most
 
 // Per batch, each array is padded to whole 16-byte chunks, so that a batch's
 // part starts 16-byte aligned.
@@ -428,23 +433,39 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
     __shared__ int cursor[kTiCsrMaxM];
     __shared__ __align__(16) uint16_t list[3 * kTiCsrMaxN];  // by bucket, unordered within one
     __shared__ uint16_t sorted[3 * kTiCsrMaxN];  // by bucket, ascending within one
+    __shared__ float sorted_w[3 * kTiCsrMaxN];   // their weights
     __shared__ int wave_sum[T / kWave];
+    __shared__ int wave_below[T / kWave];
     const int tid = threadIdx.x;
     const int lane = tid % kWave, wave = tid / kWave;
     const int64_t b = blockIdx.x;
+    // This workgroup's buckets [m_lo, m_hi).
+    const int span = (M + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
+    const int m_lo = min(static_cast<int>(blockIdx.y) * span, M);
+    const int m_hi = min(m_lo + span, M);
     const int e_count = 3 * N;
     const int32_t* ib = idx + b * e_count;
     // This thread's entries e = tid + k*T, all requested before the first
-    // use.  Indices outside [0, M) (callers validate them) become -1 and
-    // contribute nothing.
+    // use.  Indices outside [0, M) (callers validate them) contribute
+    // nothing; entries of other ranges become -1 once counted.
     int em[EPT];
+    float ew[EPT];
+    const float* wb = weights + b * e_count;
 #pragma unroll
     for (int k = 0; k < EPT; ++k) em[k] = ib[min(tid + k * T, e_count - 1)];
 #pragma unroll
-    for (int k = 0; k < EPT; ++k)
-        if (tid + k * T >= e_count || static_cast<unsigned>(em[k]) >= static_cast<unsigned>(M))
-            em[k] = -1;
+    for (int k = 0; k < EPT; ++k) ew[k] = wb[min(tid + k * T, e_count - 1)];
+    int below = 0;
+#pragma unroll
+    for (int k = 0; k < EPT; ++k) {
+        const bool valid = tid + k * T < e_count && static_cast<unsigned>(em[k]) < static_cast<unsigned>(M);
+        below += (valid && em[k] < m_lo) ? 1 : 0;
+        em[k] = (valid && em[k] >= m_lo && em[k] < m_hi) ? em[k] - m_lo : -1;
+    }
     for (int m = tid; m < kTiCsrMaxM; m += T) cursor[m] = 0;
+#pragma unroll
+    for (int d = 1; d < kWave; d <<= 1) below += __shfl_xor(below, d, kWave);
+    if (lane == 0) wave_below[wave] = below;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < EPT; ++k)
@@ -468,22 +489,25 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
     __syncthreads();
     int before = incl - run;
     for (int w = 0; w < wave; ++w) before += wave_sum[w];
+    int base = 0;  // entries of the batch in buckets below m_lo
+#pragma unroll
+    for (int w = 0; w < T / kWave; ++w) base += wave_below[w];
     int* start = csr.start + b * csr.sstride;
 #pragma unroll
     for (int k = 0; k < MPT; ++k) {
         const int m = tid * MPT + k;
         cursor[m] += before;
-        if (m < M) start[m] = cursor[m];
+        if (m < m_hi - m_lo) start[m_lo + m] = base + cursor[m];
     }
-    if (tid == T - 1) start[M] = before + run;
+    if (tid == T - 1 && m_hi == M) start[M] = base + before + run;
     __syncthreads();
 #pragma unroll
     for (int k = 0; k < EPT; ++k)
         if (em[k] >= 0) list[atomicAdd(&cursor[em[k]], 1)] = static_cast<uint16_t>(tid + k * T);
     __syncthreads();
-    // cursor[m] is now the end of bucket m and its start the previous end.
-    // Entry ids are distinct, so an entry's place in its bucket is the count
-    // of smaller ids there.
+    // cursor[m] is now the end of local bucket m and its start the previous
+    // end.  Entry ids are distinct, so an entry's place in its bucket is the
+    // count of smaller ids there.
 #pragma unroll
     for (int k = 0; k < EPT; ++k) {
         if (em[k] < 0) continue;
@@ -503,23 +527,15 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
             }
         }
         sorted[p0 + rank] = static_cast<uint16_t>(e);
+        sorted_w[p0 + rank] = ew[k];
     }
     __syncthreads();
-    const int total = cursor[M - 1];
-    uint16_t* out = csr.list + b * csr.lstride;
-    float* wout = csr.weight + b * csr.wstride;
-    const float* wb = weights + b * e_count;
-    constexpr int kW = EPT;  // entries per thread in the copy: all loads first
-    float wv[kW];
-#pragma unroll
-    for (int u = 0; u < kW; ++u) wv[u] = wb[sorted[min(tid + u * T, max(total - 1, 0))]];
-#pragma unroll
-    for (int u = 0; u < kW; ++u) {
-        const int p = tid + u * T;
-        if (p < total) {
-            out[p] = sorted[p];
-            wout[p] = wv[u];
-        }
+    const int total = m_hi > m_lo ? cursor[m_hi - m_lo - 1] : 0;
+    uint16_t* out = csr.list + b * csr.lstride + base;
+    float* wout = csr.weight + b * csr.wstride + base;
+    for (int p = tid; p < total; p += T) {
+        out[p] = sorted[p];
+        wout[p] = sorted_w[p];
     }
 }
 
@@ -563,7 +579,6 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kerne
     float* __restrict__ grad_features, int64_t C, int M, int N) {
     static_assert(CG == 1 || CG == 2 || CG == 4, "channels per step");
     extern __shared__ float4 lds4[];
-    const int e_count = 3 * N;
     const int w_chunks = csr.wstride / 4, l_chunks = csr.lstride / 8, s_chunks = csr.sstride / 4;
     const int r_chunks = CG * N / 4;  // one row buffer: [N][CG] floats, channels interleaved
     float* wl = reinterpret_cast<float*>(lds4);
@@ -578,40 +593,47 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kerne
     const int tid = threadIdx.x;
     const int n_chunks = N / 4;  // <= kTiCsrThreads: one 4-unknown chunk per thread
     const float4* gsrc = reinterpret_cast<const float4*>(grad_out + (b * C + c_lo) * N);
-    // Step g's rows for this thread's chunk: CG float4 (zero past the block).
-    float4 nx0 = make_float4(0.f, 0.f, 0.f, 0.f), nx1 = nx0, nx2 = nx0, nx3 = nx0;
-    auto fetch = [&](int g) {
+    // A step's rows for this thread's chunk: CG float4 (zero past the block).
+    // Two steps are in flight in registers (x: the next step, y: the one
+    // after) while the current one is summed from LDS.
+    struct Rows {
+        float4 r0, r1, r2, r3;
+    };
+    const float4 zero4 = make_float4(0.f, 0.f, 0.f, 0.f);
+    Rows x{zero4, zero4, zero4, zero4}, y = x;
+    auto fetch = [&](int g, Rows& to) {
         const int cg = min(CG, cb - g * CG);
         if (tid >= n_chunks) return;
         const float4* src = gsrc + static_cast<int64_t>(g) * CG * n_chunks + tid;
-        nx0 = src[0];
-        if (CG > 1) nx1 = cg > 1 ? src[n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (CG > 2) nx2 = cg > 2 ? src[2 * n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
-        if (CG > 3) nx3 = cg > 3 ? src[3 * n_chunks] : make_float4(0.f, 0.f, 0.f, 0.f);
+        to.r0 = src[0];
+        if (CG > 1) to.r1 = cg > 1 ? src[n_chunks] : zero4;
+        if (CG > 2) to.r2 = cg > 2 ? src[2 * n_chunks] : zero4;
+        if (CG > 3) to.r3 = cg > 3 ? src[3 * n_chunks] : zero4;
     };
-    auto put = [&](float4* dst) {  // unknowns 4*tid .. 4*tid+3, CG channels each
+    auto put = [&](const Rows& v, float4* dst) {  // unknowns 4*tid .. 4*tid+3, CG channels each
         if (tid >= n_chunks) return;
         if (CG == 1) {
-            dst[tid] = nx0;
+            dst[tid] = v.r0;
         } else if (CG == 2) {
-            dst[2 * tid] = make_float4(nx0.x, nx1.x, nx0.y, nx1.y);
-            dst[2 * tid + 1] = make_float4(nx0.z, nx1.z, nx0.w, nx1.w);
+            dst[2 * tid] = make_float4(v.r0.x, v.r1.x, v.r0.y, v.r1.y);
+            dst[2 * tid + 1] = make_float4(v.r0.z, v.r1.z, v.r0.w, v.r1.w);
         } else {
-            dst[4 * tid] = make_float4(nx0.x, nx1.x, nx2.x, nx3.x);
-            dst[4 * tid + 1] = make_float4(nx0.y, nx1.y, nx2.y, nx3.y);
-            dst[4 * tid + 2] = make_float4(nx0.z, nx1.z, nx2.z, nx3.z);
-            dst[4 * tid + 3] = make_float4(nx0.w, nx1.w, nx2.w, nx3.w);
+            dst[4 * tid] = make_float4(v.r0.x, v.r1.x, v.r2.x, v.r3.x);
+            dst[4 * tid + 1] = make_float4(v.r0.y, v.r1.y, v.r2.y, v.r3.y);
+            dst[4 * tid + 2] = make_float4(v.r0.z, v.r1.z, v.r2.z, v.r3.z);
+            dst[4 * tid + 3] = make_float4(v.r0.w, v.r1.w, v.r2.w, v.r3.w);
         }
     };
     // Prologue, one round trip: weights, ids and starts (contiguous in LDS,
-    // in that order) and step 0's rows.
-    fetch(0);
+    // in that order) and step 0's rows; steps 1 and 2 requested behind them.
+    fetch(0, x);
     stage3(lds4, reinterpret_cast<const float4*>(csr.weight + b * csr.wstride),
            reinterpret_cast<const float4*>(csr.list + b * csr.lstride),
            reinterpret_cast<const float4*>(csr.start + b * csr.sstride), w_chunks,
            w_chunks + l_chunks, w_chunks + l_chunks + s_chunks);
-    put(rb0);
-    if (steps > 1) fetch(1);  // step 1's rows in registers while step 0 is summed
+    put(x, rb0);
+    if (steps > 1) fetch(1, x);
+    if (steps > 2) fetch(2, y);
     __syncthreads();
     // When every thread has one known point (M <= threads), its first
     // kTiCsrRegEntries entries (row offset and weight) stay in registers for
@@ -698,8 +720,9 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kerne
         if (g + 1 < steps) {
             // Buffer (g+1)&1 last held step g-1, finished before the previous
             // barrier.
-            put(((g + 1) & 1) ? rb1 : rb0);
-            if (g + 2 < steps) fetch(g + 2);
+            put(x, ((g + 1) & 1) ? rb1 : rb0);
+            x = y;
+            if (g + 3 < steps) fetch(g + 3, y);
         }
         __syncthreads();
     }
@@ -812,8 +835,12 @@ hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const 
     if (cg == 0) return hipErrorInvalidValue;
     TiCsr csr;
     ti_csr_bytes(B, M, N, &csr, static_cast<char*>(workspace));
-    hipLaunchKernelGGL(three_interp_csr_kernel, dim3(static_cast<uint32_t>(B)), dim3(kTiCsrThreads), 0,
-                       stream, idx, weights, csr, static_cast<int>(M), static_cast<int>(N));
+    // Bucket ranges per batch: enough workgroups to cover the CUs, each
+    // still holding at least 64 buckets.
+    const int64_t ranges = std::max<int64_t>(1, std::min<int64_t>({kTiCsrRanges, (256 + B - 1) / B, (M + 63) / 64}));
+    hipLaunchKernelGGL(three_interp_csr_kernel, dim3(static_cast<uint32_t>(B), static_cast<uint32_t>(ranges)),
+                       dim3(kTiCsrThreads), 0, stream, idx, weights, csr, static_cast<int>(M),
+                       static_cast<int>(N));
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const size_t shmem = static_cast<size_t>(csr_lds_bytes(cg, M, N));
