@@ -46,10 +46,17 @@ __global__ __launch_bounds__(kGroupThreads) void group_points_kernel(
     if (p >= P) return;
     const int64_t j = group_index(idx, b * P + p, N);
     const int64_t c0 = static_cast<int64_t>(blockIdx.z) * kGroupChannels;
-    const int64_t c1 = c0 + kGroupChannels < C ? c0 + kGroupChannels : C;
+    const int nc = static_cast<int>(c0 + kGroupChannels < C ? kGroupChannels : C - c0);
     const float* src = f + (b * C + c0) * N + j;
     float* dst = out + (b * C + c0) * P + p;
-    for (int64_t c = c0; c < c1; ++c, src += N, dst += P) *dst = *src;
+    // Every channel's load in flight before the first store (channels past
+    // the block read the last one again and are not stored).
+    float v[kGroupChannels];
+#pragma unroll
+    for (int k = 0; k < kGroupChannels; ++k) v[k] = src[min(k, nc - 1) * N];
+#pragma unroll
+    for (int k = 0; k < kGroupChannels; ++k)
+        if (k < nc) dst[k * P] = v[k];
 }
 
 // Channels 0-2: xyz[b, j, a] - centre[b, p / S, a]; channels 3..: features.
@@ -63,17 +70,30 @@ __global__ __launch_bounds__(kGroupThreads) void group_points_rel_kernel(
     if (p >= P) return;
     const int64_t j = group_index(idx, b * P + p, N);
     const int64_t CT = C + 3;
-    int64_t c0 = static_cast<int64_t>(blockIdx.z) * kGroupChannels;
-    const int64_t c1 = c0 + kGroupChannels < CT ? c0 + kGroupChannels : CT;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.z) * kGroupChannels;
+    const int nc = static_cast<int>(c0 + kGroupChannels < CT ? kGroupChannels : CT - c0);
     float* dst = out + (b * CT + c0) * P + p;
-    if (c0 < 3) {
+    // Channel c0 + k: relative xyz below 3, else feature c0 + k - 3.  Every
+    // load is issued before the first store (channels past the block read a
+    // valid one again and are not stored).
+    // kx: the block's leading xyz channels (3 in the first block, whose c0
+    // is 0, else none: kGroupChannels >= 3).
+    const int kx = c0 == 0 ? 3 : 0;
+    float v[kGroupChannels];
+    if (nc > kx) {  // feature channels c0 + k - 3 for k in [kx, nc)
+        const float* src = f + (b * C + c0 - 3) * N + j;
+#pragma unroll
+        for (int k = 0; k < kGroupChannels; ++k) v[k] = src[min(max(k, kx), nc - 1) * N];
+    }
+    if (kx > 0) {
         const float* q = xyz + (b * N + j) * 3;
         const float* m = centres + (b * M + p / S) * 3;
-        for (; c0 < 3 && c0 < c1; ++c0, dst += P) *dst = q[c0] - m[c0];
+#pragma unroll
+        for (int a = 0; a < 3; ++a) v[a] = q[a] - m[a];
     }
-    if (c0 >= c1) return;  // also when there are no feature channels
-    const float* src = f + (b * C + (c0 - 3)) * N + j;
-    for (int64_t c = c0; c < c1; ++c, src += N, dst += P) *dst = *src;
+#pragma unroll
+    for (int k = 0; k < kGroupChannels; ++k)
+        if (k < nc) dst[k * P] = v[k];
 }
 
 // Backward: grad_features[b,c,n] = sum of grad_out[b,c,p] over the p with
@@ -236,6 +256,119 @@ __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
     if (live) gf[(b * C + c) * N + n] = acc;
 }
 
+// LDS-staged grouping for clouds whose channel rows fit in LDS: one
+// workgroup per (group of CG channels, batch, slice of the output columns)
+// stages its batch's CG source rows -- feature rows, and for REL the
+// coordinates for channels 0-2 -- with coalesced loads, then walks its
+// columns: each column's index is read once (four columns per thread in
+// flight) and its CG values come from LDS, so the gathers never touch L2;
+// stores along p are coalesced.  HBM traffic: the output, the source rows
+// once per slice (L2 after the first) and the index once per channel group.
+constexpr int kGroupLdsThreads = 512;
+// Rows per workgroup: up to 32 KiB (measured at config 2's shape: 8 KiB
+// rows, 2 per workgroup, 83 us; 1 row 104 us, 4 rows 94 us, 8 rows 134 us),
+// or one row of up to 64 KiB.
+constexpr int kGroupLdsBytes = 32 * 1024;
+constexpr int kGroupLdsRowBytes = 64 * 1024;
+constexpr int kGroupLdsCols = 4;           // output columns per thread per step
+
+template <bool REL, int CG, typename I>
+__global__ __launch_bounds__(kGroupLdsThreads) void group_lds_kernel(
+    const float* __restrict__ xyz, const float* __restrict__ centres, const float* __restrict__ f,
+    const I* __restrict__ idx, float* __restrict__ out, int64_t C, int64_t N, int64_t M,
+    int64_t S) {
+    constexpr int T = kGroupLdsThreads;
+    constexpr int U = kGroupLdsCols;
+    extern __shared__ float rows[];  // [CG][N]
+    const int64_t CT = REL ? C + 3 : C;
+    const int64_t P = M * S;
+    const int64_t b = blockIdx.y;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * CG;
+    const int nc = static_cast<int>(c0 + CG < CT ? CG : CT - c0);
+    const int tid = threadIdx.x;
+    // Stage: row k is channel c0 + k; eight loads per thread in flight.
+    for (int k = 0; k < nc; ++k) {
+        const int64_t c = c0 + k;
+        const bool coord = REL && c < 3;
+        const float* src = coord ? xyz + b * N * 3 + c : f + (b * C + c - (REL ? 3 : 0)) * N;
+        const int64_t stride = coord ? 3 : 1;
+        float* dst = rows + static_cast<int64_t>(k) * N;
+        for (int64_t n0 = 0; n0 < N; n0 += 8 * T) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) v[u] = src[min(n0 + u * T + tid, N - 1) * stride];
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+                if (n0 + u * T + tid < N) dst[n0 + u * T + tid] = v[u];
+        }
+    }
+    __syncthreads();
+    const int64_t per = (P + gridDim.z - 1) / gridDim.z;
+    const int64_t p_lo = static_cast<int64_t>(blockIdx.z) * per;
+    const int64_t p_hi = min(P, p_lo + per);
+    const I* ib = idx + b * P;
+    float* ob = out + (b * CT + c0) * P;
+    for (int64_t p0 = p_lo + tid; p0 < p_hi; p0 += static_cast<int64_t>(U) * T) {
+        int64_t j[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {  // clamped loads, all in flight
+            const int64_t v = static_cast<int64_t>(ib[min(p0 + u * T, p_hi - 1)]);
+            j[u] = v < 0 ? 0 : (v >= N ? N - 1 : v);
+        }
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t p = p0 + u * T;
+            if (p >= p_hi) break;
+            // The first group's relative channels subtract the column's
+            // centre (P < 2^31: 32-bit division, once per column).
+            const float* ctr = nullptr;
+            if (REL && c0 < 3)
+                ctr = centres + (b * M + static_cast<uint32_t>(p) / static_cast<uint32_t>(S)) * 3;
+#pragma unroll
+            for (int k = 0; k < CG; ++k) {
+                if (k >= nc) break;
+                float v = rows[static_cast<int64_t>(k) * N + j[u]];
+                if (REL && c0 + k < 3) v = v - ctr[c0 + k];
+                ob[static_cast<int64_t>(k) * P + p] = v;
+            }
+        }
+    }
+}
+
+// Channels per workgroup of group_lds_kernel (0: rows of N floats do not fit).
+int group_lds_channels(int64_t N) {
+    const int64_t row = N * static_cast<int64_t>(sizeof(float));
+    for (int cg : {8, 4, 2})
+        if (cg * row <= kGroupLdsBytes) return cg;
+    return row <= kGroupLdsRowBytes ? 1 : 0;
+}
+
+// Launches group_lds_kernel when the rows fit; returns false otherwise.
+template <bool REL, typename I>
+bool launch_group_lds(const float* xyz, const float* centres, const float* f, const I* idx,
+                      float* out, int64_t B, int64_t C, int64_t N, int64_t M, int64_t S,
+                      hipStream_t stream, hipError_t* err) {
+    const int cg = group_lds_channels(N);
+    const int64_t CT = REL ? C + 3 : C;
+    const int64_t groups = cg > 0 ? (CT + cg - 1) / cg : 0;
+    if (cg == 0 || B > 65535 || groups > INT32_MAX || M * S >= INT32_MAX) return false;
+    // Slices of the columns: at least 2048 workgroups in all (eight per
+    // resident slot, so the last round is a small part of the run), each
+    // slice at least 2048 columns.
+    const int64_t want = (2048 + groups * B - 1) / (groups * B);
+    const int64_t slices = std::max<int64_t>(1, std::min<int64_t>({65535, want, (M * S + 2047) / 2048}));
+    const dim3 grid(static_cast<uint32_t>(groups), static_cast<uint32_t>(B), static_cast<uint32_t>(slices));
+    const size_t shmem = static_cast<size_t>(cg) * static_cast<size_t>(N) * sizeof(float);
+    switch (cg) {
+        case 8: hipLaunchKernelGGL((group_lds_kernel<REL, 8, I>), grid, dim3(kGroupLdsThreads), shmem, stream, xyz, centres, f, idx, out, C, N, M, S); break;
+        case 4: hipLaunchKernelGGL((group_lds_kernel<REL, 4, I>), grid, dim3(kGroupLdsThreads), shmem, stream, xyz, centres, f, idx, out, C, N, M, S); break;
+        case 2: hipLaunchKernelGGL((group_lds_kernel<REL, 2, I>), grid, dim3(kGroupLdsThreads), shmem, stream, xyz, centres, f, idx, out, C, N, M, S); break;
+        default: hipLaunchKernelGGL((group_lds_kernel<REL, 1, I>), grid, dim3(kGroupLdsThreads), shmem, stream, xyz, centres, f, idx, out, C, N, M, S); break;
+    }
+    *err = hipGetLastError();
+    return true;
+}
+
 bool group_grid(int64_t B, int64_t channels, int64_t P, dim3& grid) {
     const int64_t x = (P + kGroupThreads - 1) / kGroupThreads;
     const int64_t z = (channels + kGroupChannels - 1) / kGroupChannels;
@@ -258,6 +391,12 @@ hipError_t pointops_group_points(const float* features, const void* idx, int idx
     if (B == 0 || C == 0 || P == 0) return hipSuccess;
     dim3 grid;
     if (N == 0 || !group_grid(B, C, P, grid)) return hipErrorInvalidValue;
+    hipError_t err = hipSuccess;
+    if (idx_bits == 32 ? launch_group_lds<false>(nullptr, nullptr, features, static_cast<const int32_t*>(idx),
+                                                 out, B, C, N, P, 1, stream, &err)
+                       : launch_group_lds<false>(nullptr, nullptr, features, static_cast<const int64_t*>(idx),
+                                                 out, B, C, N, P, 1, stream, &err))
+        return err;
     if (idx_bits == 32)
         hipLaunchKernelGGL(group_points_kernel<int32_t>, grid, dim3(kGroupThreads), 0, stream,
                            features, static_cast<const int32_t*>(idx), out, C, N, P);
@@ -333,6 +472,12 @@ hipError_t pointops_group_points_rel(const float* xyz, const float* centres, con
     dim3 grid;
     if (N == 0 || M > INT64_MAX / S || !group_grid(B, C + 3, M * S, grid))
         return hipErrorInvalidValue;
+    hipError_t err = hipSuccess;
+    if (idx_bits == 32 ? launch_group_lds<true>(xyz, centres, features, static_cast<const int32_t*>(idx),
+                                                out, B, C, N, M, S, stream, &err)
+                       : launch_group_lds<true>(xyz, centres, features, static_cast<const int64_t*>(idx),
+                                                out, B, C, N, M, S, stream, &err))
+        return err;
     if (idx_bits == 32)
         hipLaunchKernelGGL(group_points_rel_kernel<int32_t>, grid, dim3(kGroupThreads), 0, stream,
                            xyz, centres, features, static_cast<const int32_t*>(idx), out, C, N, M, S);

@@ -1047,6 +1047,36 @@ def test_group_points_matches_oracle(cuda_device, bits, B, C, N, P):
     same_bits(host(fc.grad), O.group_points_backward(go.numpy(), idx.numpy(), N))
 
 
+@pytest.mark.parametrize("bits", [32, 64])
+@pytest.mark.parametrize("B,C,N,M,S", [(2, 5, 100, 30, 10),    # 8 rows per workgroup, one group
+                                       (2, 67, 2049, 70, 9),   # 4 rows, a partial last group
+                                       (1, 9, 8193, 50, 7),    # 1 row per workgroup
+                                       (1, 3, 20_000, 40, 8),  # rows too long for LDS
+                                       (3, 0, 4096, 64, 32)])  # relative xyz only
+def test_group_points_and_rel_lds_and_fallback(cuda_device, bits, B, C, N, M, S):
+    """Both grouping kernels (LDS-staged rows for clouds whose rows fit, the
+    L2 gather otherwise) against the oracle, bit for bit, with out-of-order
+    and repeated indices."""
+    from mps_pointops import group
+
+    g = torch.Generator().manual_seed(B * 7 + C * 11 + N + M * S + bits)
+    x = torch.randn(B, N, 3, generator=g)
+    centres = torch.randn(B, M, 3, generator=g)
+    f = torch.randn(B, C, N, generator=g)
+    idx = torch.randint(0, N, (B, M, S), generator=g, dtype=torch.int64)
+    idx[:, :, 1] = idx[:, :, 0]
+    idx = idx.to(torch.int32 if bits == 32 else torch.int64)
+    xc, cc, fc, ic = x.cuda(), centres.cuda(), f.cuda(), idx.cuda()
+    print(f"group lds B={B} C={C} N={N} M={M} S={S} bits={bits}", flush=True)
+    rel = group.query_and_group(xc, cc, fc if C else None, ic)
+    want = O.group_points_rel(x.numpy(), centres.numpy(), f.numpy() if C else None, idx.numpy())
+    np.testing.assert_array_equal(host(rel), want)
+    if C:
+        flat = ic.reshape(B, M * S)
+        out = group.group_points(fc, flat)
+        np.testing.assert_array_equal(host(out), O.group_points(f.numpy(), flat.cpu().numpy()))
+
+
 def test_compat_gather_grouping_known_answers(cuda_device):
     """tests/test_compat.py:121-137 on the GPU path."""
     from mps_pointops import compat
