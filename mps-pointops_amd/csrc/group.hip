@@ -22,6 +22,7 @@
 // bounds).
 #include <algorithm>
 
+#include "csr_sort.hpp"
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -256,6 +257,119 @@ __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
     if (live) gf[(b * C + c) * N + n] = acc;
 }
 
+// Backward over a per-batch CSR of the entries, for P <= 32768 entries and
+// N <= 4096 points: group_csr_kernel (per batch up to kGroupCsrRanges
+// workgroups, each owning the points of one residue class) sorts the
+// entries p by their point idx[b,p] (csr_sort_class: ascending p within a
+// point's list of up to 256, the scatter's order beyond);
+// group_csr_grad_kernel (one workgroup per (channel, batch)) stages the
+// channel's grad_out row of P floats in LDS with coalesced loads, and
+// thread n sums row[p] over its point's list in order (ids from L2, the
+// first kGroupCsrFirst requested with the row), writing each element of
+// grad_features once.  No transpose, no
+// atomics on the gradients.
+constexpr int kGroupCsrThreads = 1024;
+constexpr int kGroupCsrMaxP = 32768;
+constexpr int kGroupCsrMaxN = 4096;
+constexpr int kGroupCsrRanges = 8;  // build workgroups per batch at most
+constexpr int kGroupCsrFirst = 8;   // list entries per point requested ahead
+constexpr int kGroupCsrTail = 8;    // further entries requested at once (32: slower)
+
+struct GroupCsr {
+    int* start;      // [B][sstride]: list starts, N + 1 used
+    uint16_t* list;  // [B][lstride]: entries p by point
+    int64_t sstride, lstride;
+};
+
+__host__ __device__ inline size_t group_csr_bytes(int64_t B, int64_t N, int64_t P, GroupCsr* out,
+                                                  char* base) {
+    const int64_t ss = (N + 1 + 63) & ~int64_t(63), ls = (P + 63) & ~int64_t(63);
+    const size_t start_bytes = group_align(static_cast<size_t>(B * ss) * sizeof(int));
+    if (out != nullptr) {
+        out->start = reinterpret_cast<int*>(base);
+        out->list = reinterpret_cast<uint16_t*>(base + start_bytes);
+        out->sstride = ss;
+        out->lstride = ls;
+    }
+    return start_bytes + group_align(static_cast<size_t>(B * ls) * sizeof(uint16_t));
+}
+
+__host__ __device__ inline bool group_csr_fits(int64_t N, int64_t P) {
+    return N >= 1 && N <= kGroupCsrMaxN && P >= 1 && P <= kGroupCsrMaxP;
+}
+
+template <typename I>
+__global__ __launch_bounds__(kGroupCsrThreads) void group_csr_kernel(const I* __restrict__ idx,
+                                                                     GroupCsr csr, int N, int P) {
+    const int64_t b = blockIdx.x;
+    // Indices outside [0, N) are clamped, as the forward gathers them.
+    csr_sort_class<kGroupCsrThreads, kGroupCsrMaxP, kGroupCsrMaxN, 256, I, false, true>(
+        idx + b * P, nullptr, P, N, static_cast<int>(blockIdx.y), static_cast<int>(gridDim.y),
+        csr.start + b * csr.sstride, csr.list + b * csr.lstride, nullptr);
+}
+
+__global__ __launch_bounds__(kGroupCsrThreads) void group_csr_grad_kernel(
+    const float* __restrict__ g, int64_t g_batch, GroupCsr csr, float* __restrict__ gf, int64_t C,
+    int N, int P) {
+    constexpr int T = kGroupCsrThreads;
+    constexpr int NPT = kGroupCsrMaxN / T;  // points per thread
+    constexpr int F = kGroupCsrFirst;
+    constexpr int TB = kGroupCsrTail;
+    extern __shared__ float row[];  // [P]
+    const int64_t c = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x;
+    const int* st = csr.start + b * csr.sstride;
+    const uint16_t* ls = csr.list + b * csr.lstride;
+    // This thread's points n = tid + i*T: list bounds, then the first F
+    // entries of each (an empty list reads entry 0, not added), all in
+    // flight with the row's loads.
+    int pb[NPT], pe[NPT];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int n = tid + i * T;
+        pb[i] = n < N ? st[n] : 0;
+        pe[i] = n < N ? st[n + 1] : 0;
+    }
+    const float* src = g + b * g_batch + c * P;
+    for (int base = 0; base < P; base += 8 * T) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = src[min(base + u * T + tid, P - 1)];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (base + u * T + tid < P) row[base + u * T + tid] = v[u];
+    }
+    int e0[NPT][F];
+#pragma unroll
+    for (int i = 0; i < NPT; ++i)
+#pragma unroll
+        for (int u = 0; u < F; ++u) e0[i][u] = ls[pe[i] > pb[i] ? min(pb[i] + u, pe[i] - 1) : 0];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int n = tid + i * T;
+        if (n >= N) break;
+        float acc = 0.f;
+#pragma unroll
+        for (int u = 0; u < F; ++u) {
+            const float t = row[e0[i][u]];
+            acc = pb[i] + u < pe[i] ? acc + t : acc;
+        }
+        // The rest of a long list: TB ids requested at once from L2.
+        for (int q = pb[i] + F; q < pe[i]; q += TB) {
+            int e[TB];
+#pragma unroll
+            for (int u = 0; u < TB; ++u) e[u] = ls[min(q + u, pe[i] - 1)];
+#pragma unroll
+            for (int u = 0; u < TB; ++u) {
+                const float t = row[e[u]];
+                acc = q + u < pe[i] ? acc + t : acc;
+            }
+        }
+        gf[(b * C + c) * N + n] = acc;
+    }
+}
+
 // LDS-staged grouping for clouds whose channel rows fit in LDS: one
 // workgroup per (group of CG channels, batch, slice of the output columns)
 // stages its batch's CG source rows -- feature rows, and for REL the
@@ -408,6 +522,7 @@ hipError_t pointops_group_points(const float* features, const void* idx, int idx
 
 size_t pointops_group_points_backward_workspace_bytes(int64_t B, int64_t C, int64_t N, int64_t P) {
     if (B <= 0 || C <= 0 || N <= 0 || P <= 0) return 0;
+    if (group_csr_fits(N, P)) return group_csr_bytes(B, N, P, nullptr, nullptr);
     return group_inverse_bytes(B, C, N, P, nullptr, nullptr);
 }
 
@@ -419,6 +534,27 @@ hipError_t pointops_group_points_backward(const float* grad_out, int64_t grad_ba
         grad_batch_stride < C * P)
         return hipErrorInvalidValue;
     if (B == 0 || C == 0 || N == 0) return hipSuccess;
+    if (workspace != nullptr && group_csr_fits(N, P) && B <= 65535 && C <= INT32_MAX) {
+        GroupCsr csr;
+        group_csr_bytes(B, N, P, &csr, static_cast<char*>(workspace));
+        int64_t ranges = 1;  // workgroups per batch: a power of two covering the CUs
+        while (ranges < kGroupCsrRanges && ranges * B < 256) ranges *= 2;
+        const dim3 bgrid(static_cast<uint32_t>(B), static_cast<uint32_t>(ranges));
+        const int n = static_cast<int>(N), p = static_cast<int>(P);
+        if (idx_bits == 32)
+            hipLaunchKernelGGL(group_csr_kernel<int32_t>, bgrid, dim3(kGroupCsrThreads), 0, stream,
+                               static_cast<const int32_t*>(idx), csr, n, p);
+        else
+            hipLaunchKernelGGL(group_csr_kernel<int64_t>, bgrid, dim3(kGroupCsrThreads), 0, stream,
+                               static_cast<const int64_t*>(idx), csr, n, p);
+        const hipError_t err = hipGetLastError();
+        if (err != hipSuccess) return err;
+        hipLaunchKernelGGL(group_csr_grad_kernel,
+                           dim3(static_cast<uint32_t>(C), static_cast<uint32_t>(B)),
+                           dim3(kGroupCsrThreads), static_cast<size_t>(P) * sizeof(float), stream,
+                           grad_out, grad_batch_stride, csr, grad_features, C, n, p);
+        return hipGetLastError();
+    }
     dim3 pgrid, ngrid;
     if (P >= INT32_MAX || N >= INT32_MAX || workspace == nullptr || !group_grid(B, 1, P, pgrid) ||
         !group_grid(B, 1, N, ngrid) || N * ((C + kWave - 1) / kWave) / (kGroupThreads / kWave) >= INT32_MAX)

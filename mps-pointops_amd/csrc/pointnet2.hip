@@ -18,6 +18,7 @@
 // into memory with hardware float atomics.
 #include <algorithm>
 
+#include "csr_sort.hpp"
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
 
@@ -372,13 +373,10 @@ __global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_g
 
 // Backward over a CSR of the entries, for M <= 4096 known points and
 // N <= 4096 unknowns (N a multiple of 4), with a caller workspace:
-//   three_interp_csr_kernel (per batch, R workgroups, each owning a range
-//   of known indices): every workgroup reads all of the batch's entries,
-//   counts those below its range (its offset in the CSR) and counting-sorts
-//   the entry ids e = 3n + t of its range by known index m = idx[b,n,t] in
-//   LDS; an entry's place in its bucket is the number of smaller ids there,
-//   so each bucket lists its entries in ascending order; the sorted ids, their
-//   weights and the bucket starts are copied out with coalesced stores.
+//   three_interp_csr_kernel (per batch, R workgroups, each owning the known
+//   indices of one residue class mod R): csr_sort_class, a counting sort of
+//   the entry ids e = 3n + t by known index m = idx[b,n,t] in LDS, each
+//   bucket in ascending order, written with the entries' weights.
 //   three_interp_backward_csr_kernel (one workgroup per batch and block of
 //   kTiCsrBlock channels): stages the batch's CSR once (ids, starts and each
 //   entry's weight, gathered by id), then walks its channels CG at a time
@@ -391,7 +389,6 @@ __global__ __launch_bounds__(kTiGatherThreads) void three_interpolate_backward_g
 constexpr int kTiCsrThreads = 1024;
 constexpr int kTiCsrMaxM = 4096;
 constexpr int kTiCsrMaxN = 4096;
-constexpr int kTiCsrEntriesPerThread = 3 * kTiCsrMaxN / kTiCsrThreads;
 constexpr int kTiCsrBlock = 16;                    // channels per gather workgroup
 constexpr int kTiCsrLdsBytes = 160 * 1024 - 1024;  // gather LDS budget
 constexpr int kTiCsrStage = 8;                     // 16-byte chunks a thread stages at once
@@ -427,116 +424,13 @@ __host__ __device__ inline size_t ti_csr_bytes(int64_t B, int64_t M, int64_t N, 
 
 __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
     const int32_t* __restrict__ idx, const float* __restrict__ weights, TiCsr csr, int M, int N) {
-    constexpr int T = kTiCsrThreads;
-    constexpr int EPT = kTiCsrEntriesPerThread;
-    constexpr int MPT = kTiCsrMaxM / T;  // buckets per thread in the scan
-    __shared__ int cursor[kTiCsrMaxM];
-    __shared__ __align__(16) uint16_t list[3 * kTiCsrMaxN];  // by bucket, unordered within one
-    __shared__ uint16_t sorted[3 * kTiCsrMaxN];  // by bucket, ascending within one
-    __shared__ float sorted_w[3 * kTiCsrMaxN];   // their weights
-    __shared__ int wave_sum[T / kWave];
-    __shared__ int wave_below[T / kWave];
-    const int tid = threadIdx.x;
-    const int lane = tid % kWave, wave = tid / kWave;
     const int64_t b = blockIdx.x;
-    // This workgroup's buckets [m_lo, m_hi).
-    const int span = (M + static_cast<int>(gridDim.y) - 1) / static_cast<int>(gridDim.y);
-    const int m_lo = min(static_cast<int>(blockIdx.y) * span, M);
-    const int m_hi = min(m_lo + span, M);
-    const int e_count = 3 * N;
-    const int32_t* ib = idx + b * e_count;
-    // This thread's entries e = tid + k*T, all requested before the first
-    // use.  Indices outside [0, M) (callers validate them) contribute
-    // nothing; entries of other ranges become -1 once counted.
-    int em[EPT];
-    float ew[EPT];
-    const float* wb = weights + b * e_count;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) em[k] = ib[min(tid + k * T, e_count - 1)];
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) ew[k] = wb[min(tid + k * T, e_count - 1)];
-    int below = 0;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        const bool valid = tid + k * T < e_count && static_cast<unsigned>(em[k]) < static_cast<unsigned>(M);
-        below += (valid && em[k] < m_lo) ? 1 : 0;
-        em[k] = (valid && em[k] >= m_lo && em[k] < m_hi) ? em[k] - m_lo : -1;
-    }
-    for (int m = tid; m < kTiCsrMaxM; m += T) cursor[m] = 0;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) below += __shfl_xor(below, d, kWave);
-    if (lane == 0) wave_below[wave] = below;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < EPT; ++k)
-        if (em[k] >= 0) atomicAdd(&cursor[em[k]], 1);
-    __syncthreads();
-    // Exclusive scan of the counts: MPT consecutive buckets per thread.
-    int run = 0;
-#pragma unroll
-    for (int k = 0; k < MPT; ++k) {
-        const int v = cursor[tid * MPT + k];
-        cursor[tid * MPT + k] = run;
-        run += v;
-    }
-    int incl = run;
-#pragma unroll
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int up = __shfl_up(incl, d, kWave);
-        if (lane >= d) incl += up;
-    }
-    if (lane == kWave - 1) wave_sum[wave] = incl;
-    __syncthreads();
-    int before = incl - run;
-    for (int w = 0; w < wave; ++w) before += wave_sum[w];
-    int base = 0;  // entries of the batch in buckets below m_lo
-#pragma unroll
-    for (int w = 0; w < T / kWave; ++w) base += wave_below[w];
-    int* start = csr.start + b * csr.sstride;
-#pragma unroll
-    for (int k = 0; k < MPT; ++k) {
-        const int m = tid * MPT + k;
-        cursor[m] += before;
-        if (m < m_hi - m_lo) start[m_lo + m] = base + cursor[m];
-    }
-    if (tid == T - 1 && m_hi == M) start[M] = base + before + run;
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < EPT; ++k)
-        if (em[k] >= 0) list[atomicAdd(&cursor[em[k]], 1)] = static_cast<uint16_t>(tid + k * T);
-    __syncthreads();
-    // cursor[m] is now the end of local bucket m and its start the previous
-    // end.  Entry ids are distinct, so an entry's place in its bucket is the
-    // count of smaller ids there.
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        if (em[k] < 0) continue;
-        const int e = tid + k * T;
-        const int m = em[k];
-        const int p0 = m == 0 ? 0 : cursor[m - 1], p1 = cursor[m];
-        int rank = 0;
-        // Eight ids per 16-byte read, over the aligned chunks covering the
-        // bucket (3 * kTiCsrMaxN is a multiple of 8: the reads stay inside).
-        for (int q = p0 & ~7; q < p1; q += 8) {
-            const uint4 v = *reinterpret_cast<const uint4*>(&list[q]);
-            const uint32_t w4[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-                const int id = static_cast<int>((w4[j >> 1] >> (16 * (j & 1))) & 0xFFFFu);
-                rank += (q + j >= p0 && q + j < p1 && id < e) ? 1 : 0;
-            }
-        }
-        sorted[p0 + rank] = static_cast<uint16_t>(e);
-        sorted_w[p0 + rank] = ew[k];
-    }
-    __syncthreads();
-    const int total = m_hi > m_lo ? cursor[m_hi - m_lo - 1] : 0;
-    uint16_t* out = csr.list + b * csr.lstride + base;
-    float* wout = csr.weight + b * csr.wstride + base;
-    for (int p = tid; p < total; p += T) {
-        out[p] = sorted[p];
-        wout[p] = sorted_w[p];
-    }
+    // Entries e = 3n + t keyed by known index; every bucket in (n, t) order.
+    constexpr int kMaxE = 3 * kTiCsrMaxN;
+    csr_sort_class<kTiCsrThreads, kMaxE, kTiCsrMaxM, kMaxE, int32_t, true, false>(
+        idx + b * 3 * N, weights + b * 3 * N, 3 * N, M, static_cast<int>(blockIdx.y),
+        static_cast<int>(gridDim.y), csr.start + b * csr.sstride, csr.list + b * csr.lstride,
+        csr.weight + b * csr.wstride);
 }
 
 // Copies up to kTiCsrStage 16-byte chunks per thread from three consecutive
@@ -835,9 +729,10 @@ hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const 
     if (cg == 0) return hipErrorInvalidValue;
     TiCsr csr;
     ti_csr_bytes(B, M, N, &csr, static_cast<char*>(workspace));
-    // Bucket ranges per batch: enough workgroups to cover the CUs, each
-    // still holding at least 64 buckets.
-    const int64_t ranges = std::max<int64_t>(1, std::min<int64_t>({kTiCsrRanges, (256 + B - 1) / B, (M + 63) / 64}));
+    // Workgroups per batch (a power of two, each owning the known indices of
+    // one residue class): enough to cover the CUs.
+    int64_t ranges = 1;
+    while (ranges < kTiCsrRanges && ranges * B < 256) ranges *= 2;
     hipLaunchKernelGGL(three_interp_csr_kernel, dim3(static_cast<uint32_t>(B), static_cast<uint32_t>(ranges)),
                        dim3(kTiCsrThreads), 0, stream, idx, weights, csr, static_cast<int>(M),
                        static_cast<int>(N));

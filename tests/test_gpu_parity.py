@@ -1342,6 +1342,29 @@ def test_group_points_backward_heavily_repeated_point(cuda_device):
     same_bits(host(f.grad), O.group_points_backward(go.numpy(), idx.numpy(), 100))
 
 
+@pytest.mark.parametrize("B,C,N,P,repeat", [(2, 70, 100, 30_000, True),   # CSR, one huge list
+                                             (3, 5, 4096, 32_768, False),  # CSR at its limits
+                                             (2, 7, 5000, 3000, False)])   # inverse-index path
+def test_group_points_backward_paths(cuda_device, B, C, N, P, repeat):
+    """Both backward designs (the per-batch CSR for P <= 32768 and N <= 4096,
+    the inverse index with the transposed gradient otherwise) equal the
+    sequential oracle bit for bit; a point listed more than 256 times sums in
+    the scatter's order, exact here with quarter-integer gradients."""
+    from mps_pointops import group
+
+    g = torch.Generator().manual_seed(B + C + N + P)
+    f = torch.randn(B, C, N, generator=g).cuda().requires_grad_()
+    idx = torch.randint(0, N, (B, P), generator=g, dtype=torch.int32)
+    if repeat:
+        idx[:, ::7] = 0
+        idx[:, 1::7] = 0
+        idx[:, 2::3] = 0
+    go = torch.randint(-8, 9, (B, C, P), generator=g).float() / 4
+    print(f"group backward B={B} C={C} N={N} P={P}", flush=True)
+    group.group_points(f, idx.cuda()).backward(go.cuda())
+    same_bits(host(f.grad), O.group_points_backward(go.numpy(), idx.numpy(), N))
+
+
 def _grid_sweep_case(seed: int):
     """Random shapes and distributions for the grid search: uniform boxes,
     Gaussian blobs, sphere surfaces, points on a line (degenerate extents)
