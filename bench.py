@@ -345,11 +345,18 @@ def run(args) -> dict:
         sa_leaf.grad = None
         grouping.query_and_group(xyz, centres, sa_leaf, sa_idx, check=False).backward(sa_up)
 
+    sa_layer = grouping.QueryAndGroup(0.2, 32)
+
+    def group_layer():  # the whole layer step: ball query (pointnet2 form) + grouping
+        return sa_layer(xyz, centres, sa_feats)
+
     group_fwd()
     group_fwd_bwd()
+    group_layer()
     torch.cuda.synchronize()
     t_gf = timer.time(group_fwd, reps)
     t_gfb = timer.time(group_fwd_bwd, reps)
+    t_gl = timer.time(group_layer, reps)
     group_bytes = 4 * (B * 67 * C2_NPOINT * 32 + B * C2_NPOINT * 32 + B * 64 * N + B * N * 3)
     propagation = {
         "three_nn": {"ms": t_tn * 1e3, "tops": PAIR_OPS * B * N * C2_NPOINT / t_tn / 1e12},
@@ -357,6 +364,7 @@ def run(args) -> dict:
         "three_interpolate_fwd_bwd": {"ms": t_tib * 1e3, "gbps": 2 * interp_bytes / t_tib / 1e9},
         "query_and_group_C64_S32": {"ms": t_gf * 1e3, "gbps": group_bytes / t_gf / 1e9},
         "query_and_group_fwd_bwd": {"ms": t_gfb * 1e3},
+        "QueryAndGroup_layer_ball_query_plus_group": {"ms": t_gl * 1e3},
     }
 
     kernel = fps_kernel_name(N)

@@ -164,6 +164,14 @@ hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *poin
                                    const int64_t *query_lengths, const int64_t *point_lengths,
                                    int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
                                    int64_t K, float radius_sq, hipStream_t stream);
+/* The same float32 query without lengths in pointnet2_ops' form: int32
+ * indices only, (B,Q,K), slots past the hits repeating the query's first hit
+ * and all 0 for a query without one.  Replaces compat.py:76-85 (the ball
+ * query, its -1 -> first-neighbour padding and int32 conversion) in one
+ * launch; B <= 65535. */
+hipError_t pointops_ball_query_pn2_f32(const float *queries, const float *points, int32_t *idx,
+                                       int64_t B, int64_t Q, int64_t P, int64_t K, float radius_sq,
+                                       hipStream_t stream);
 /* The same query (identical results) over the uniform grid of
  * pointops_knn3_grid, for large clouds without lengths, 1 <= K <= 64, P >= 1:
  * each query scans the cells that cover its ball and keeps its K smallest

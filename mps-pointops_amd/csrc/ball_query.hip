@@ -118,11 +118,14 @@ __global__ __launch_bounds__(kBqThreads) void ball_query_kernel(
 // query reached K hits, so a tile is read from L2 once per NWQ queries.
 // With `skip` set, every workgroup returns at once when *skip != 0 (another
 // search of the same call, chosen on the device, writes the outputs).
-template <typename S, int NWQ>
+// PN2: the pointnet2_ops output instead -- int32 indices only, unused slots
+// repeating the query's first hit (all 0 without one) -- so that the
+// grouping step needs no padding or conversion kernels.
+template <typename S, int NWQ, bool PN2>
 __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     const S* __restrict__ queries, const S* __restrict__ points,
     const int64_t* __restrict__ query_lengths, const int64_t* __restrict__ point_lengths,
-    int64_t* __restrict__ out_idx, float* __restrict__ out_dist, int64_t Q, int64_t P, int K,
+    void* __restrict__ out_idx, float* __restrict__ out_dist, int64_t Q, int64_t P, int K,
     float r2, const int* __restrict__ skip) {
     if (skip != nullptr && *skip != 0) return;  // uniform, before any barrier
     constexpr int kTile = kBqLdsDepth * kWave;
@@ -147,8 +150,9 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
         qy = widen(qp[1]);
         qz = widen(qp[2]);
     }
-    int64_t* oi = out_idx + row * K;
-    float* od = out_dist + row * K;
+    int64_t* oi = static_cast<int64_t*>(out_idx) + row * K;
+    int32_t* oi32 = static_cast<int32_t*>(out_idx) + row * K;
+    float* od = PN2 ? nullptr : out_dist + row * K;
     const S* pp = points + 3 * b * P;
     // Points of the tile at `base` for this thread (clamped into the cloud;
     // points past n are masked in the test).
@@ -161,6 +165,7 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
         }
     };
     int found = 0;
+    int first = 0;  // PN2: the query's first hit
     // d < r2 is impossible for r2 <= 0 (d is never negative) or NaN r2.
     bool done = !live || !(r2 > 0.f);
     if (n > 0) fetch(0);
@@ -184,13 +189,21 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
                 if ((m0 | m1) == 0) continue;
                 const int s0 = found + lanes_below(m0);
                 const int s1 = found + __popcll(m0) + lanes_below(m1);
-                if (h0 && s0 < K) {
-                    oi[s0] = j0;
-                    od[s0] = d0;
-                }
-                if (h1 && s1 < K) {
-                    oi[s1] = j1;
-                    od[s1] = d1;
+                if constexpr (PN2) {
+                    if (found == 0)
+                        first = m0 != 0 ? base + c * kWave + static_cast<int>(__builtin_ctzll(m0))
+                                        : base + (c + 1) * kWave + static_cast<int>(__builtin_ctzll(m1));
+                    if (h0 && s0 < K) oi32[s0] = j0;
+                    if (h1 && s1 < K) oi32[s1] = j1;
+                } else {
+                    if (h0 && s0 < K) {
+                        oi[s0] = j0;
+                        od[s0] = d0;
+                    }
+                    if (h1 && s1 < K) {
+                        oi[s1] = j1;
+                        od[s1] = d1;
+                    }
                 }
                 found += __popcll(m0) + __popcll(m1);
                 if (found >= K) break;
@@ -211,8 +224,12 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     if (qi >= Q) return;
     found = min(found, K);
     for (int s = found + lane; s < K; s += kWave) {
-        oi[s] = -1;
-        od[s] = 0.f;
+        if constexpr (PN2) {
+            oi32[s] = first;  // 0 when nothing was found
+        } else {
+            oi[s] = -1;
+            od[s] = 0.f;
+        }
     }
 }
 
@@ -284,7 +301,7 @@ hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t*
     if (B <= 65535 && qblocks <= INT32_MAX) {
         // Clouds are spread over all XCDs (blockIdx.x fastest), which
         // balances clouds of different scan lengths across them.
-        hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ>),
+        hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ, false>),
                            dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
                            dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,
                            static_cast<int>(K), r2, skip);
@@ -314,6 +331,21 @@ hipError_t launch_radius(const S* y, const S* x, const int64_t* ptr_y, const int
 
 }  // namespace
 
+hipError_t ball_query_pn2(const float* queries, const float* points, int32_t* idx, int64_t B,
+                          int64_t Q, int64_t P, int64_t K, float r2, hipStream_t stream) {
+    if (B < 0 || Q < 0 || P < 0 || K < 0 || K > INT32_MAX || P > INT32_MAX - kBqDepth * kWave)
+        return hipErrorInvalidValue;
+    if (B == 0 || Q == 0 || K == 0) return hipSuccess;
+    constexpr int NWQ = kBqLdsQueries;
+    const int64_t qblocks = (Q + NWQ - 1) / NWQ;
+    if (B > 65535 || qblocks > INT32_MAX) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((ball_query_lds_kernel<float, NWQ, true>),
+                       dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
+                       dim3(NWQ * kWave), 0, stream, queries, points, nullptr, nullptr, idx, nullptr,
+                       Q, P, static_cast<int>(K), r2, nullptr);
+    return hipGetLastError();
+}
+
 hipError_t ball_query_f32_unless(const float* queries, const float* points, int64_t* idx,
                                  float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K,
                                  float radius_sq, const int* skip, hipStream_t stream) {
@@ -333,6 +365,12 @@ hipError_t pointops_ball_query_f32(const float* queries, const float* points,
                                    int64_t K, float radius_sq, hipStream_t stream) {
     return launch_ball<float>(queries, points, query_lengths, point_lengths, idx, dist2, B, Q, P, K,
                               radius_sq, nullptr, stream);
+}
+
+hipError_t pointops_ball_query_pn2_f32(const float* queries, const float* points, int32_t* idx,
+                                       int64_t B, int64_t Q, int64_t P, int64_t K, float radius_sq,
+                                       hipStream_t stream) {
+    return ball_query_pn2(queries, points, idx, B, Q, P, K, radius_sq, stream);
 }
 
 hipError_t pointops_ball_query_f16(const uint16_t* queries, const uint16_t* points,

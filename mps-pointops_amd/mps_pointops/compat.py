@@ -33,7 +33,7 @@ from importlib.machinery import ModuleSpec
 import torch
 from torch import Tensor
 
-from . import flat, group, ops
+from . import _native, flat, group, ops
 from . import pointcept as pointcept_ops
 
 
@@ -65,11 +65,40 @@ def ball_query(radius: float, nsample: int, xyz: Tensor, new_xyz: Tensor) -> Ten
     -> (B, npoint, nsample) int32 holding the first ``nsample`` points in
     input order with squared distance ``< radius**2``; unused slots repeat
     the query's first neighbour, and a query without neighbours is all 0."""
+    fused = _ball_query_pointnet2(new_xyz, xyz, radius, nsample)
+    if fused is not None:
+        return fused
     _, idx = ops.ball_query(new_xyz, xyz, radius, nsample)
     if idx.shape[-1] == 0:
         return idx.int()
     first = idx.narrow(-1, 0, 1).clamp_min(0)
     return idx.where(idx >= 0, first).int()
+
+
+def _ball_query_pointnet2(queries: Tensor, points: Tensor, radius: float, k: int) -> Tensor | None:
+    """The padded int32 result in one launch (pointops_ball_query_pn2_f32) for
+    float32 ROCm clouds the index-order kernel serves (fewer points than the
+    grid search takes, at most 65535 clouds); None otherwise.  Arguments are
+    checked as ops.ball_query checks them."""
+    from . import _ball_query
+
+    if not (isinstance(queries, Tensor) and isinstance(points, Tensor)):
+        return None
+    if (queries.dim() != 3 or points.dim() != 3 or queries.shape[-1] != 3
+            or points.shape[-1] != 3 or queries.shape[0] != points.shape[0]
+            or queries.device != points.device or queries.device.type != "cuda"
+            or queries.dtype != torch.float32 or points.dtype != torch.float32
+            or queries.shape[0] > 65_535 or points.shape[1] >= _ball_query._GRID_MIN_POINTS):
+        return None  # the general path raises or serves these
+    _, radius_sq = _ball_query._checked_radius_and_k(radius, k)
+    _native.require_device(queries.device)
+    B, Q, _ = queries.shape
+    idx = torch.empty((B, Q, k), dtype=torch.int32, device=queries.device)
+    if idx.numel():
+        _native.call("pointops_ball_query_pn2_f32", queries.contiguous().data_ptr(),
+                     points.contiguous().data_ptr(), idx.data_ptr(), B, Q, points.shape[1], k,
+                     radius_sq, _native.stream(queries.device))
+    return idx
 
 
 class KNN(torch.nn.Module):

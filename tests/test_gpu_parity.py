@@ -1077,6 +1077,53 @@ def test_group_points_and_rel_lds_and_fallback(cuda_device, bits, B, C, N, M, S)
         np.testing.assert_array_equal(host(out), O.group_points(f.numpy(), flat.cpu().numpy()))
 
 
+@pytest.mark.parametrize("case", ["c2", "sparse", "radius_zero", "non_finite", "k_large", "ragged"])
+def test_compat_ball_query_single_launch(cuda_device, case):
+    """compat.ball_query's one-launch int32 path (pointnet2 padding in the
+    kernel) equals the composition it replaces -- the index-order ball
+    query, -1 replaced by the first neighbour (0 without one), int32 -- and
+    the oracle's first-K answer."""
+    from mps_pointops import compat, ops
+
+    g = torch.Generator().manual_seed(len(case) * 13)
+    radius, k = 0.2, 32
+    if case == "c2":
+        x = bench.make_c2(B=3)
+        c = x[:, torch.randperm(4096, generator=g)[:500]].clone()
+    elif case == "sparse":  # many queries with few or no neighbours
+        x = torch.rand(2, 3000, 3, generator=g) * 10
+        c = torch.rand(2, 700, 3, generator=g) * 12 - 1
+        radius = 0.4
+    elif case == "radius_zero":
+        x = torch.rand(2, 500, 3, generator=g)
+        c = x[:, :64].clone()
+        radius = 0.0
+    elif case == "non_finite":
+        x = torch.rand(2, 2000, 3, generator=g)
+        x[0, 5] = float("nan")
+        x[1, 17, 2] = float("inf")
+        c = torch.rand(2, 300, 3, generator=g)
+        c[0, 3] = float("nan")
+    elif case == "k_large":
+        x = torch.rand(1, 5000, 3, generator=g)
+        c = torch.rand(1, 200, 3, generator=g)
+        radius, k = 0.3, 130
+    else:
+        x = torch.rand(3, 1037, 3, generator=g)
+        c = torch.rand(3, 77, 3, generator=g)
+        k = 5
+    xc, cc = x.cuda().contiguous(), c.cuda().contiguous()
+    got = compat.ball_query(radius, k, xc, cc)
+    assert got.dtype == torch.int32 and got.shape == (x.shape[0], c.shape[1], k)
+    _, idx = ops.ball_query(cc, xc, radius, k)
+    first = idx.narrow(-1, 0, 1).clamp_min(0)
+    want = idx.where(idx >= 0, first).int()
+    np.testing.assert_array_equal(host(got), host(want))
+    _, oi = O.ball_query(c, x, radius, k)
+    of = np.where(oi[..., :1] >= 0, oi[..., :1], 0)
+    np.testing.assert_array_equal(host(got), np.where(oi >= 0, oi, of).astype(np.int32))
+
+
 def test_compat_gather_grouping_known_answers(cuda_device):
     """tests/test_compat.py:121-137 on the GPU path."""
     from mps_pointops import compat
