@@ -158,11 +158,12 @@ class KernelTimer:
 
 
 def fps_kernel_name(n: int) -> str:
-    """Template instance fps_tiled_kernel<P,512> that a cloud of n points uses."""
+    """Template instance fps_tiled_kernel<P,512,PO> that a cloud of n points
+    uses (PO: tiles per wave of the first half, 9 for P = 8)."""
     p = 1
     while p * 512 < n:
         p *= 2
-    return f"fps_tiled_kernel<{p},512>"
+    return f"fps_tiled_kernel<{p},512,{9 if p == 8 else p}>"
 
 
 def profiled_traffic(kernel: str, workload: str):

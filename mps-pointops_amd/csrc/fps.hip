@@ -9,7 +9,7 @@
 //
 //
 // Kernels:
-//   fps_tiled_kernel<P,T>   one workgroup per cloud of up to 8192 points
+//   fps_tiled_kernel<P,T,PO> one workgroup per cloud of up to 8192 points
 //                           (batched or ragged), its points and running
 //                           distances in VGPRs, sorted into spatially compact
 //                           64-point tiles so that a step updates only the
@@ -102,16 +102,18 @@ struct alignas(16) WaveBest {
     float x, y, z;
     int pad[3];
 };
-// fps_tiled_kernel<P,T>: the lazy single-workgroup FPS on a spatially sorted
-// cloud, so that most per-step updates can be skipped.
+// fps_tiled_kernel<P,T,PO>: the lazy single-workgroup FPS on a spatially
+// sorted cloud, so that most per-step updates can be skipped.
 //
 // Setup: the cloud is counting-sorted in LDS by a 12-bit Morton key of its
-// 16 x 16 x 16 cell (over the cloud's bounding box); sorted position q goes
-// to wave q / (64 P), slot (q / 64) % P, lane q % 64, so every (wave, slot) --
-// a tile -- holds 64 nearby points.  Each point keeps its original index,
-// which breaks every tie (largest running distance, then smallest index),
-// so results do not depend on the sort.  Lane s of every wave holds the
-// bounding box of the wave's tile s.
+// 16 x 16 x 16 cell (over the cloud's bounding box) and cut into tiles of 64
+// consecutive sorted positions (lane = position % 64), so every tile holds
+// 64 nearby points.  The first half of the waves hold PO tiles each, the
+// others 2P - PO: two waves share a SIMD and the older one is issued first,
+// so tile work moved to it shortens the run's critical wave.  Each point
+// keeps its original index, which breaks every tie (largest running
+// distance, then smallest index), so results do not depend on the sort.
+// Lane s of every wave holds the bounding box of the wave's tile s.
 //
 // Steps are taken lazily: at an exchange every wave publishes its KC best
 // points (largest running distance, then smallest index) and the (KC+1)-th
@@ -128,7 +130,7 @@ struct alignas(16) WaveBest {
 // is at most the rounded squared distance of every point in the box, and
 // every running distance is at most M; a skipped tile therefore has no
 // running distance that the update would lower.
-template <int P, int T>
+template <int P, int T, int PO>
 __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ xyz,
                                                       const int64_t* __restrict__ ptr,
                                                       const int64_t* __restrict__ out_ptr,
@@ -140,6 +142,7 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     constexpr int CAP = P * T;      // points per cloud at most
     constexpr int kCells = 4096;
     static_assert(KC * NW == kWave && KC + 1 <= kWave && P <= 16 && CAP <= 8192, "shape");
+    static_assert(PO >= P && PO < 2 * P && PO <= 16 && NW % 2 == 0, "tile split");
     static_assert(kCells % T == 0, "cells per thread");
     // The sort's arrays, then (from the load of the tiles on) the points'
     // coordinates by sorted position, for the exchange's candidates.
@@ -151,8 +154,12 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     float4* const spts = buf;                              // sorted position -> xyz
     __shared__ float red[6][NW];        // bounding-box partials
     __shared__ int wave_sum[NW];
-    __shared__ WaveBest cands[kWave];
-    __shared__ int bounds[NW];
+    // Candidates and bounds, double-buffered by exchange parity: a wave
+    // writes the next exchange's buffer only after the barrier that every
+    // wave reaches after reading this one, so one barrier per exchange
+    // suffices.
+    __shared__ WaveBest cands[2][kWave];
+    __shared__ int bounds[2][NW];
 
     const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
     if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
@@ -257,8 +264,10 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     __syncthreads();  // permutation complete
 
     // ---- this thread's tile points, their indices and running distances
-    constexpr int PA = P <= 8 ? P + 1 : P;  // see fps_lazy_kernel
-    float px[PA], py[PA], pz[PA], md[P];
+    const int my_tiles = wave < NW / 2 ? PO : 2 * P - PO;
+    const int tile0 = wave < NW / 2 ? wave * PO : (NW / 2) * PO + (wave - NW / 2) * (2 * P - PO);
+    constexpr int PA = PO <= 8 ? PO + 1 : PO;  // see fps_lazy_kernel
+    float px[PA], py[PA], pz[PA], md[PO];
     int pcode[PA];  // local index << 13 | sorted position
 #pragma unroll
     for (int k = 0; k < PA; ++k) {
@@ -272,11 +281,14 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
         cy = p[3 * f + 1];
         cz = p[3 * f + 2];
     }
-    float blo[3] = {INFINITY, INFINITY, INFINITY}, bhi[3] = {-INFINITY, -INFINITY, -INFINITY};
+    // Tile boxes; lanes without a tile, and tiles with no point of finite
+    // coordinates on some axis, keep [+inf, +inf], which the step's box test
+    // never selects.
+    float blo[3] = {INFINITY, INFINITY, INFINITY}, bhi[3] = {INFINITY, INFINITY, INFINITY};
 #pragma unroll
-    for (int k = 0; k < P; ++k) {
-        const int q = (wave * P + k) * kWave + lane;
-        const bool valid = q < n;
+    for (int k = 0; k < PO; ++k) {
+        const int q = (tile0 + k) * kWave + lane;
+        const bool valid = k < my_tiles && q < n;
         const int j = valid ? sorted_index[q] : 0;
         px[k] = valid ? p[3 * j] : 0.f;
         py[k] = valid ? p[3 * j + 1] : 0.f;
@@ -289,7 +301,7 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
         const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
         const float tly = wave_min(valid ? py[k] : INFINITY), thy = wave_max(valid ? py[k] : -INFINITY);
         const float tlz = wave_min(valid ? pz[k] : INFINITY), thz = wave_max(valid ? pz[k] : -INFINITY);
-        if (lane == k) {
+        if (lane == k && tlx <= thx && tly <= thy && tlz <= thz) {
             blo[0] = tlx; bhi[0] = thx;
             blo[1] = tly; bhi[1] = thy;
             blo[2] = tlz; bhi[2] = thz;
@@ -298,9 +310,9 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
 
     __syncthreads();  // every sorted index has been read
 #pragma unroll
-    for (int k = 0; k < P; ++k) {
-        const int q = (wave * P + k) * kWave + lane;
-        if (q < n) spts[q] = make_float4(px[k], py[k], pz[k], 0.f);
+    for (int k = 0; k < PO; ++k) {
+        const int q = (tile0 + k) * kWave + lane;
+        if (k < my_tiles && q < n) spts[q] = make_float4(px[k], py[k], pz[k], 0.f);
     }
     __syncthreads();  // coordinates by sorted position
 
@@ -313,37 +325,42 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     float pfx = 0.f, pfy = 0.f, pfz = 0.f;
     auto apply_pending = [&]() {
 #pragma unroll
-        for (int k = 0; k < P; ++k)
+        for (int k = 0; k < PO; ++k)
             if ((pend >> k) & 1u)
                 md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], pfx, pfy, pfz));
         pend = 0;
     };
     int64_t step = 1;
+    int parity = 0;
     while (step < seg.cnt) {
         // Exchange: this wave's KC best points (largest running distance,
         // then smallest index) and its bound, the (KC+1)-th.  Keys pack
         // (running distance bits ^ sign, ~code) into 64 bits, so one
-        // unsigned compare orders them; each lane keeps its two largest keys
-        // below `lim` (the last key it published) and rescans its slots only
-        // when it publishes a second time in one exchange.  Candidate r
-        // collects in lane r; its coordinates are read from LDS afterwards.
-        uint64_t lim = ~uint64_t(0), h1 = 0, h2 = 0;  // 0: no key; 1: not yet known
-        auto rescan = [&]() {
-            h1 = 0;
-            h2 = 0;
+        // unsigned compare orders them (0: no key).  Each lane keeps its two
+        // largest keys; after a lane publishes its first, its second moves
+        // up and the lane is marked in `unknown` (a wave-uniform mask), and
+        // only if it wins again are its slots rescanned, below the key it
+        // just published.  Candidate r collects in lane r; its coordinates
+        // are read from LDS afterwards.
+        auto top2 = [&](bool limited, uint64_t lim, uint64_t& a1, uint64_t& a2) {
+            a1 = 0;
+            a2 = 0;
 #pragma unroll
-            for (int k = 0; k < P; ++k) {
+            for (int k = 0; k < PO; ++k) {
+                if (k >= my_tiles) break;  // wave-uniform
                 const uint64_t key =
                     (static_cast<uint64_t>(static_cast<uint32_t>(f2i(md[k])) ^ 0x80000000u) << 32) |
                     static_cast<uint32_t>(~pcode[k]);
-                const bool below = key < lim;
-                const bool first = below && key > h1;
-                const bool second = below && !first && key > h2;
-                h2 = first ? h1 : (second ? key : h2);
-                h1 = first ? key : h1;
+                const bool below = !limited || key < lim;
+                const bool first = below && key > a1;
+                const bool second = below && !first && key > a2;
+                a2 = first ? a1 : (second ? key : a2);
+                a1 = first ? key : a1;
             }
         };
-        rescan();
+        uint64_t h1, h2;
+        top2(false, 0, h1, h2);
+        uint64_t unknown = 0;
         int ck = 0, cc = 0x7FFFFFFF;
         int bound = 0;
 #pragma unroll
@@ -352,30 +369,29 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
             const uint32_t wv = wave_max_u32_l63(hh);
             const uint64_t at = ballot(hh == wv);
             int wl = static_cast<int>(__builtin_ctzll(at));
+            uint32_t wlo;
             if (__popcll(at) > 1) {  // equal distances: the largest ~code (smallest index)
-                const uint32_t wlo = wave_max_u32_l63(hh == wv ? static_cast<uint32_t>(h1) : 0u);
+                wlo = wave_max_u32_l63(hh == wv ? static_cast<uint32_t>(h1) : 0u);
                 wl = static_cast<int>(__builtin_ctzll(ballot(hh == wv && static_cast<uint32_t>(h1) == wlo)));
+            } else {
+                wlo = static_cast<uint32_t>(readlane(static_cast<int>(h1), wl));
             }
             if (r == KC) {
                 bound = static_cast<int>(wv ^ 0x80000000u);
                 break;
             }
-            const int code = static_cast<int>(~static_cast<uint32_t>(readlane(static_cast<int>(h1), wl)));
-            ck = lane == r ? static_cast<int>(wv ^ 0x80000000u) : ck;
-            cc = lane == r ? code : cc;
-            // The winner's next key is its second (known) or needs a rescan
-            // below the key just published.
-            const bool popped = lane == wl;
-            const bool again = readlane(static_cast<int>(h2), wl) == 1 && readlane(static_cast<int>(h2 >> 32), wl) == 0;
-            lim = popped ? h1 : lim;
-            if (again) {
-                const uint64_t keep1 = h1, keep2 = h2;
-                rescan();
-                h1 = popped ? h1 : keep1;
-                h2 = popped ? h2 : keep2;
+            ck = writelane(ck, static_cast<int>(wv ^ 0x80000000u), r);
+            cc = writelane(cc, static_cast<int>(~wlo), r);
+            const bool won = lane == wl;
+            if ((unknown >> wl) & 1u) {
+                uint64_t n1, n2;
+                top2(true, (static_cast<uint64_t>(wv) << 32) | wlo, n1, n2);
+                h1 = won ? n1 : h1;
+                h2 = won ? n2 : h2;
+                unknown &= ~(uint64_t(1) << wl);
             } else {
-                h1 = popped ? h2 : h1;
-                h2 = popped ? uint64_t(1) : h2;
+                h1 = won ? h2 : h1;
+                unknown |= uint64_t(1) << wl;
             }
         }
         if (lane < KC) {
@@ -389,15 +405,15 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
             e.y = c.y;
             e.z = c.z;
             e.pad[0] = e.pad[1] = e.pad[2] = 0;
-            cands[wave * KC + lane] = e;
+            cands[parity][wave * KC + lane] = e;
         }
-        if (lane == 0) bounds[wave] = bound;
+        if (lane == 0) bounds[parity][wave] = bound;
         __syncthreads();
-        const WaveBest mine = cands[lane];
-        int maxb_v = bounds[0];
+        const WaveBest mine = cands[parity][lane];
+        int maxb_v = bounds[parity][0];
 #pragma unroll
-        for (int w = 1; w < NW; ++w) maxb_v = max(maxb_v, bounds[w]);
-        __syncthreads();  // every wave has read the candidates before any rewrites them
+        for (int w = 1; w < NW; ++w) maxb_v = max(maxb_v, bounds[parity][w]);
+        parity ^= 1;
         int cmd = mine.key;
         const int cidx = mine.index;
         const float ccx = mine.x, ccy = mine.y, ccz = mine.z;
@@ -429,13 +445,18 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
             const float fy = i2f(readlane(f2i(ccy), wl));
             const float fz = i2f(readlane(f2i(ccz), wl));
             cmd = f2i(running_min(i2f(cmd), sqdist3(ccx, ccy, ccz, fx, fy, fz)));
-            when = lane == wl ? taken : when;
+            when = writelane(when, taken, wl);
             // Tiles whose box may hold a point nearer to the centroid than
-            // the chosen (largest) running distance.
+            // the chosen (largest) running distance.  Per axis the gap is
+            // f minus f clamped to the box: the rounded difference to the
+            // nearer face (sign aside, which squaring drops), 0 inside.  A
+            // non-finite centroid coordinate gives an infinite or NaN gap,
+            // which selects no tile: such a centroid lowers no running
+            // distance (every point's distance to it is +inf or NaN).
             const float M = i2f(wv);
-            const float gx = fmaxf(fmaxf(blo[0] - fx, fx - bhi[0]), 0.f);
-            const float gy = fmaxf(fmaxf(blo[1] - fy, fy - bhi[1]), 0.f);
-            const float gz = fmaxf(fmaxf(blo[2] - fz, fz - bhi[2]), 0.f);
+            const float gx = fx - __builtin_amdgcn_fmed3f(fx, blo[0], bhi[0]);
+            const float gy = fy - __builtin_amdgcn_fmed3f(fy, blo[1], bhi[1]);
+            const float gz = fz - __builtin_amdgcn_fmed3f(fz, blo[2], bhi[2]);
             float lb = gx * gx;
             lb = lb + gy * gy;
             lb = lb + gz * gz;
@@ -1055,11 +1076,17 @@ constexpr int kRegsThreads = 512;  // 8 waves: two per SIMD hide each other's re
 constexpr int kRegsMaxPoints = 16 * kRegsThreads;  // 8192 points in VGPRs (P = 16)
 constexpr int kGlobalThreads = 1024;
 
+// Tiles per wave of the first half (the rest hold 2P - PO): 9 of 16 for
+// P = 8 measured 1.5 % faster at N = 4096 than an even split, 10 and 12
+// slower; other P keep the even split.
+template <int P>
+constexpr int kTilesFirstHalf = P == 8 ? 9 : P;
+
 template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream) {
-    hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads>), dim3(static_cast<uint32_t>(blocks)),
+    hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>), dim3(static_cast<uint32_t>(blocks)),
                        dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
                        start, skip);
     return hipGetLastError();

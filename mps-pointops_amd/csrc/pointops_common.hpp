@@ -52,6 +52,14 @@ __device__ __forceinline__ int readlane(int v, int lane) {
 
 __device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// `old` with lane `lane` replaced by `value` (both wave-uniform): one
+// v_writelane_b32 in place of a lane compare and a select.  The s_nop gives
+// the four wait states a lane select written by a VALU instruction needs.
+__device__ __forceinline__ int writelane(int old, int value, int lane) {
+    asm("s_nop 3\n\tv_writelane_b32 %0, %1, m0" : "+v"(old) : "s"(value), "{m0}"(lane));
+    return old;
+}
+
 __device__ __forceinline__ uint64_t ballot(bool p) { return __ballot(p); }
 
 // Lanes strictly below this lane whose bit is set in `mask`.
