@@ -309,7 +309,10 @@ __device__ __forceinline__ void lane_merge(uint32_t (&lk)[KMAX], int (&li)[KMAX]
 
 // Publish each wave's sorted list ([slot][lane] in lds[wave]) and merge the
 // NW lists of every lane in wave 0, writing K (sqrt distance, index)
-// pairs at row `row`.  Unfilled slots get (inf, empty_index).
+// pairs at row `row`.  Unfilled slots get (inf, empty_index).  The merge
+// keeps every list's head in registers as a 64-bit (key, index) value, so
+// a step is NW - 1 compares and one LDS read (the next entry of the list
+// it took from) instead of NW dependent reads.
 template <int KMAX, int NW, int CAP>
 __device__ __forceinline__ void lane_publish_and_merge(
     uint2 (&lds)[NW][KMAX > CAP ? KMAX : CAP][kWave], const uint32_t (&lk)[KMAX],
@@ -320,28 +323,38 @@ __device__ __forceinline__ void lane_publish_and_merge(
         if (s < K) lds[wave][s][lane] = make_uint2(lk[s], static_cast<uint32_t>(li[s]));
     __syncthreads();
     if (wave != 0 || !active) return;
-    int head[NW];
+    auto pack = [](uint2 v) { return (static_cast<uint64_t>(v.x) << 32) | v.y; };
+    constexpr uint64_t kPast = ~uint64_t(0);  // after a list's K-th entry
+    uint64_t head[NW];
+    int next[NW];  // slot of each list's following entry
 #pragma unroll
-    for (int w = 0; w < NW; ++w) head[w] = 0;
+    for (int w = 0; w < NW; ++w) {
+        head[w] = pack(lds[w][0][lane]);
+        next[w] = 1;
+    }
     for (int s = 0; s < K; ++s) {
-        uint2 best = make_uint2(0xFFFFFFFFu, 0xFFFFFFFFu);
+        uint64_t best = head[0];
         int from = 0;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) {
-            if (head[w] < K) {
-                const uint2 c = lds[w][head[w]][lane];
-                if (c.x < best.x || (c.x == best.x && c.y < best.y)) {
-                    best = c;
-                    from = w;
-                }
-            }
+        for (int w = 1; w < NW; ++w) {
+            const bool less = head[w] < best;  // distinct (key, index) pairs
+            best = less ? head[w] : best;
+            from = less ? w : from;
         }
+        int h = next[0];
 #pragma unroll
-        for (int w = 0; w < NW; ++w)
-            if (w == from) ++head[w];
-        const bool empty = static_cast<int>(best.y) < 0;
-        out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(best.x)));
-        out_idx[row + s] = empty ? empty_index : static_cast<int64_t>(best.y);
+        for (int w = 1; w < NW; ++w) h = from == w ? next[w] : h;
+        const uint64_t fresh = h < K ? pack(lds[from][h][lane]) : kPast;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            head[w] = from == w ? fresh : head[w];
+            next[w] = from == w ? h + 1 : next[w];
+        }
+        const uint32_t key = static_cast<uint32_t>(best >> 32);
+        const int index = static_cast<int>(static_cast<uint32_t>(best));
+        const bool empty = index < 0;
+        out_dist[row + s] = empty ? INFINITY : sqrtf(i2f(static_cast<int>(key)));
+        out_idx[row + s] = empty ? empty_index : static_cast<int64_t>(index);
     }
 }
 
@@ -354,16 +367,20 @@ __device__ __forceinline__ void lane_publish_and_merge(
 // query a "home": the middle of its cell's range in the sorted order (or where
 // the cell would start).  knn3_lane_kernel then takes, per query, the window
 // of r*K sorted references around its home (r = min(8, N/K)) in K strided
-// groups {w0 + g + j*K : j < r} and the largest of the K group minima: every
-// group holds a reference at or below it, so at least K references are, and
-// the query's K-th neighbour is no further.  Only references with keys at or
-// below it are admitted from the start, which spares most of the list merging
-// that a full list would otherwise cost before it tightens.
+// groups {w0 + g + j*K : j < r}; wave w takes the c groups g = w mod NW and
+// the c-th smallest key among their c*r references, and the limit is the
+// largest of these over the waves: every wave has c distinct references at
+// or below it, K in all, so the query's K-th neighbour is no further (the
+// c-th smallest of a union is at most the largest of its c group minima,
+// the limit taken before).  Only references with keys at or below it are
+// admitted from the start, which spares most of the list merging that a
+// full list would otherwise cost before it tightens.
 constexpr int kWindowPrepThreads = 1024;
 constexpr int kWindowMaxRefs = 8192;
 constexpr int kWindowMaxQueries = 16384;
 constexpr int kWindowCells = 4096;  // 16^3 Morton cells
 constexpr int kWindowGroups = 8;    // window references per group (r <= 8)
+constexpr int kWindowChunk = 8;     // of which loaded at once
 
 struct WindowLayout {
     float4* sorted;  // [B][N]: coordinates in Morton order (w unused)
@@ -549,9 +566,17 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float qx = qp[0], qy = qp[1], qz = qp[2];
     const float* rp = ref + 3 * b * N;
     uint2* buf = &lds[wave][0][0];
-    const int64_t span = (N + NW - 1) / NW;
-    const int64_t lo = wave * span;
-    const int64_t hi = min<int64_t>(N, lo + span);
+    // Contiguous reference ranges in wave order, the first half of the waves
+    // taking 17/16 of an even share (a multiple of 8): two waves share each
+    // SIMD and the older is issued first, so with even ranges the younger
+    // half finished its scan ~7 us later at N = 4096 and the rest waited.
+    static_assert(NW % 2 == 0, "two halves of waves");
+    constexpr int kHalf = NW / 2;
+    const int64_t a = ((N * 17 + 16 * NW - 1) / (16 * NW) + 7) / 8 * 8;
+    const int64_t split = min<int64_t>(N, a * kHalf);
+    const int64_t b_span = (N - split + kHalf - 1) / kHalf;
+    const int64_t lo = wave < kHalf ? min<int64_t>(N, wave * a) : min<int64_t>(N, split + (wave - kHalf) * b_span);
+    const int64_t hi = wave < kHalf ? min<int64_t>(split, lo + a) : min<int64_t>(N, lo + b_span);
 
     uint32_t lk[KMAX];
     int li[KMAX];
@@ -576,17 +601,42 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
         const int r = min(kWindowGroups, n / K);
         const int h = active ? home[b * M + m] : 0;
         const int w0 = min(max(h - r * K / 2, 0), n - r * K);
-        uint32_t wmax = 0;
+        // This wave's groups g = wave mod NW (c of them) hold c x r distinct
+        // references; the c-th smallest of their keys bounds c of them, so
+        // the largest over the waves bounds K distinct references.
+        constexpr int CMAX = (KMAX + NW - 1) / NW;
+        uint32_t least[CMAX];  // the wave's smallest keys, ascending
+#pragma unroll
+        for (int c = 0; c < CMAX; ++c) least[c] = 0xFFFFFFFFu;
+        int groups = 0;
         for (int g = wave; g < K; g += NW) {
-            float4 v[kWindowGroups];
+            ++groups;
 #pragma unroll
-            for (int j = 0; j < kWindowGroups; ++j) v[j] = sp[w0 + g + min(j, r - 1) * K];
-            uint32_t gmin = 0xFFFFFFFFu;
+            for (int j0 = 0; j0 < kWindowGroups; j0 += kWindowChunk) {
+                if (j0 >= r) break;
+                float vx[kWindowChunk], vy[kWindowChunk], vz[kWindowChunk];
 #pragma unroll
-            for (int j = 0; j < kWindowGroups; ++j)
-                gmin = min(gmin, static_cast<uint32_t>(f2i(sqdist3(v[j].x, v[j].y, v[j].z, qx, qy, qz))));
-            wmax = max(wmax, gmin);
+                for (int j = 0; j < kWindowChunk; ++j) {
+                    const float* f = reinterpret_cast<const float*>(sp + w0 + g + min(j0 + j, r - 1) * K);
+                    vx[j] = f[0];
+                    vy[j] = f[1];
+                    vz[j] = f[2];
+                }
+#pragma unroll
+                for (int j = 0; j < kWindowChunk; ++j) {
+                    // Clamped repeats of the last reference are not counted again.
+                    const uint32_t key = j0 + j < r
+                        ? static_cast<uint32_t>(f2i(sqdist3(vx[j], vy[j], vz[j], qx, qy, qz)))
+                        : 0xFFFFFFFFu;
+#pragma unroll
+                    for (int c = CMAX - 1; c > 0; --c) least[c] = med3_u32(key, least[c - 1], least[c]);
+                    least[0] = min(least[0], key);
+                }
+            }
         }
+        uint32_t wmax = 0;
+#pragma unroll
+        for (int c = 0; c < CMAX; ++c) wmax = groups == c + 1 ? least[c] : wmax;
         if (wmax != 0) atomicMax(&window_max[lane], wmax);
         __syncthreads();
         const uint32_t wm = window_max[lane];
