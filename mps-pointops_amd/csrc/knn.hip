@@ -400,16 +400,13 @@ __host__ __device__ inline size_t window_layout_bytes(int64_t B, int64_t M, int6
 __device__ __forceinline__ uint32_t window_cell(float x, float y, float z, const float (&lo)[3],
                                                 const float (&scale)[3]) {
     const float c3[3] = {x, y, z};
-    uint32_t key = 0;
+    uint32_t q[3];
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
         // fmaxf/fminf map NaN to cell 0 and infinities to the edge cells.
-        const float f = fminf(fmaxf((c3[a] - lo[a]) * scale[a], 0.f), 15.f);
-        const uint32_t q = static_cast<uint32_t>(f);
-#pragma unroll
-        for (int bit = 0; bit < 4; ++bit) key |= ((q >> bit) & 1u) << (3 * bit + a);
+        q[a] = static_cast<uint32_t>(fminf(fmaxf((c3[a] - lo[a]) * scale[a], 0.f), 15.f));
     }
-    return key;
+    return morton12(q[0], q[1], q[2]);
 }
 
 __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
@@ -432,8 +429,11 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     // index past the end reads the last point again), so that every load is
     // in flight before the first wait.
     float px[RPT], py[RPT], pz[RPT], qx[QPT], qy[QPT], qz[QPT];
+    // Rounds k with no point at all are skipped (a uniform branch).
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
+        px[k] = py[k] = pz[k] = 0.f;
+        if (k * kWindowPrepThreads >= N) continue;
         const int j = min(tid + k * kWindowPrepThreads, N - 1);
         px[k] = rp[3 * j];
         py[k] = rp[3 * j + 1];
@@ -441,6 +441,8 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     }
 #pragma unroll
     for (int k = 0; k < QPT; ++k) {
+        qx[k] = qy[k] = qz[k] = 0.f;
+        if (k * kWindowPrepThreads >= M) continue;
         const int m = min(tid + k * kWindowPrepThreads, M - 1);
         qx[k] = qp[3 * m];
         qy[k] = qp[3 * m + 1];
@@ -484,6 +486,8 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     int cell[RPT], rank[RPT];
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
+        cell[k] = rank[k] = 0;
+        if (k * kWindowPrepThreads >= N) continue;
         const int j = tid + k * kWindowPrepThreads;
         cell[k] = static_cast<int>(window_cell(px[k], py[k], pz[k], lo, scale));
         rank[k] = j < N ? atomicAdd(&cell_off[cell[k]], 1) : 0;

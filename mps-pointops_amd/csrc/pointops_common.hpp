@@ -14,6 +14,17 @@ namespace pointops {
 
 constexpr int kWave = 64;
 
+// 4-bit cell coordinates interleaved into a 12-bit Morton key: bit b of
+// axis a goes to bit 3b + a (each coordinate's bits spread by two
+// shift-or-mask rounds).
+__device__ __forceinline__ uint32_t morton12(uint32_t x, uint32_t y, uint32_t z) {
+    auto spread = [](uint32_t q) {
+        q = (q | (q << 4)) & 0x0C3u;     // bits 0, 1 | 6, 7
+        return (q | (q << 2)) & 0x249u;  // bits 0, 3, 6, 9
+    };
+    return spread(x) | (spread(y) << 1) | (spread(z) << 2);
+}
+
 __device__ __forceinline__ float sqdist3(float ax, float ay, float az, float bx, float by,
                                          float bz) {
     const float dx = ax - bx;
