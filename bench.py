@@ -524,16 +524,22 @@ def run_other(args) -> dict:
 def probe() -> None:
     """One pass of each config-2 kernel (the metric's FPS, ball queries and
     kNN, then three_nn and three_interpolate forward and backward of C=128
-    features) plus a 256 MiB device copy, three times, for hardware-counter
-    runs (the copy's FETCH_SIZE/WRITE_SIZE give the scale of the counters
-    against known bytes)."""
+    features, and the set-abstraction layer: the pointnet2-form ball query
+    (0.2, 32) and the grouping of C=64 features forward and backward) plus a
+    256 MiB device copy, three times, for hardware-counter runs (the copy's
+    FETCH_SIZE/WRITE_SIZE give the scale of the counters against known
+    bytes)."""
     import mps_pointops as mp
+    from mps_pointops import group as grouping
 
     xyz = make_c2().cuda()
     B, N, _ = xyz.shape
     g = torch.Generator().manual_seed(9)
     feats = torch.randn(B, 128, C2_NPOINT, generator=g).cuda().requires_grad_()
     upstream = torch.randn(B, 128, N, generator=g).cuda()
+    sa_feats = torch.randn(B, 64, N, generator=g).cuda().requires_grad_()
+    sa_up = torch.randn(B, 67, C2_NPOINT, 32, generator=g).cuda()
+    sa_layer = grouping.QueryAndGroup(0.2, 32)
     src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
     dst = torch.empty_like(src)
     for _ in range(3):
@@ -547,10 +553,12 @@ def probe() -> None:
         w = (inv / inv.sum(-1, keepdim=True)).contiguous()
         feats.grad = None
         mp.three_interpolate(feats, tn_i, w).backward(upstream)
+        sa_feats.grad = None
+        sa_layer(xyz, centres, sa_feats).backward(sa_up)
         dst.copy_(src)
     torch.cuda.synchronize()
     print("probe: 3 x (fps, 3 ball queries, knn, three_nn, three_interpolate fwd+bwd, "
-          "256 MiB copy) done", flush=True)
+          "QueryAndGroup fwd+bwd, 256 MiB copy) done", flush=True)
 
 
 def main() -> None:
