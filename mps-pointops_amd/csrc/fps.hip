@@ -28,6 +28,7 @@
 
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
@@ -563,6 +564,106 @@ __device__ __forceinline__ bool poll_give_up(uint32_t* status, uint32_t spins, u
     return false;
 }
 
+// Lazy steps over an exchange's candidates (x, y, z and key bits in xyzk,
+// the point index in idx, `count` of them), by one wave: lane l holds
+// candidates l, l + 64, ... (CS per lane).  Each step takes the largest key
+// (smallest index on ties) -- always for the first step, afterwards only
+// while it is above `bound` -- updates the candidates' keys with the
+// points' own arithmetic and calls on_step(centroid, index); at most
+// max_steps steps.  Every wave of a workgroup runs the same steps on the
+// same data.
+template <int CS, typename OnStep>
+__device__ __forceinline__ void lazy_candidate_run(const float4* xyzk, const uint32_t* idx, int count,
+                                                   int bound, int lane, int max_steps, OnStep on_step) {
+    float kx[CS], ky[CS], kz[CS];
+    int kkey[CS];
+    uint32_t knot[CS];  // ~index: larger for a smaller index
+#pragma unroll
+    for (int s = 0; s < CS; ++s) {
+        const int id = s * kWave + lane;
+        const float4 v = id < count ? xyzk[id] : make_float4(0.f, 0.f, 0.f, i2f(static_cast<int>(0x80000000u)));
+        kx[s] = v.x;
+        ky[s] = v.y;
+        kz[s] = v.z;
+        kkey[s] = f2i(v.w);
+        knot[s] = ~(id < count ? idx[id] : 0xFFFFFFFFu);
+    }
+    for (int taken = 0; taken < max_steps; ++taken) {
+        // This lane's best as one 64-bit value (key, then ~index), and its slot.
+        uint64_t bk = 0;
+        int bs = 0;
+#pragma unroll
+        for (int s = 0; s < CS; ++s) {
+            const uint64_t k64 = (static_cast<uint64_t>(static_cast<uint32_t>(kkey[s]) ^ 0x80000000u) << 32) | knot[s];
+            const bool better = k64 > bk;
+            bk = better ? k64 : bk;
+            bs = better ? s : bs;
+        }
+        const uint32_t hh = static_cast<uint32_t>(bk >> 32);
+        const uint32_t wv = wave_max_u32_l63(hh);
+        const uint64_t at = ballot(hh == wv);
+        int wl = static_cast<int>(__builtin_ctzll(at));
+        if (__popcll(at) > 1) {  // equal keys: the smallest index
+            const uint32_t wlo = wave_max_u32_l63(hh == wv ? static_cast<uint32_t>(bk) : 0u);
+            wl = static_cast<int>(__builtin_ctzll(ballot(hh == wv && static_cast<uint32_t>(bk) == wlo)));
+        }
+        const int key = static_cast<int>(wv ^ 0x80000000u);
+        if (taken > 0 && !(key > bound)) break;  // an unpublished point may tie or beat it
+        const int id = readlane(bs, wl) * kWave + wl;
+        const float4 c = xyzk[id];
+#pragma unroll
+        for (int s = 0; s < CS; ++s)
+            kkey[s] = f2i(running_min(i2f(kkey[s]), sqdist3(kx[s], ky[s], kz[s], c.x, c.y, c.z)));
+        on_step(c, idx[id]);
+    }
+}
+
+// The candidates a run can take: after the first step (which takes the
+// largest key) a candidate is taken only while its key is above every
+// bound, and keys only decrease, so those at or below `bound` that do not
+// hold the largest key are dropped.  The live ones (at most kLazyLive) are
+// copied, in candidate order, to live_xyzk / live_idx; returns their count
+// (more than kLazyLive: the run keeps all candidates).
+constexpr int kLazyLive = 2 * kWave;
+template <int CW>
+__device__ __forceinline__ int lazy_live_candidates(const float4* xyzk, const uint32_t* idx, int bound,
+                                                    int lane, float4* live_xyzk, uint32_t* live_idx) {
+    int maxkey = static_cast<int>(0x80000000u);
+#pragma unroll
+    for (int s = 0; s < CW; ++s) maxkey = max(maxkey, f2i(xyzk[s * kWave + lane].w));
+    maxkey = wave_max_i32_l63(maxkey);
+    int nlive = 0;
+#pragma unroll
+    for (int s = 0; s < CW; ++s) {
+        const float4 v = xyzk[s * kWave + lane];
+        const int key = f2i(v.w);
+        const bool live = key > bound || key == maxkey;
+        const uint64_t m = ballot(live);
+        const int pos = nlive + lanes_below(m);
+        if (live && pos < kLazyLive) {
+            live_xyzk[pos] = v;
+            live_idx[pos] = idx[s * kWave + lane];
+        }
+        nlive += __popcll(m);
+    }
+    return nlive;
+}
+
+// Runs the lazy steps over the live candidates when they fit 2 per lane,
+// else over all CW per lane.
+template <int CW, typename OnStep>
+__device__ __forceinline__ void lazy_steps(const float4* xyzk, const uint32_t* idx, int bound, int lane,
+                                           float4* live_xyzk, uint32_t* live_idx, int max_steps,
+                                           OnStep on_step) {
+    const int nlive = lazy_live_candidates<CW>(xyzk, idx, bound, lane, live_xyzk, live_idx);
+    if (nlive <= kWave)
+        lazy_candidate_run<1>(live_xyzk, live_idx, nlive, bound, lane, max_steps, on_step);
+    else if (nlive <= kLazyLive)
+        lazy_candidate_run<2>(live_xyzk, live_idx, nlive, bound, lane, max_steps, on_step);
+    else
+        lazy_candidate_run<CW>(xyzk, idx, CW * kWave, bound, lane, max_steps, on_step);
+}
+
 // fps_lazy_kernel<P,T>: the large-cloud FPS with an exchange every few steps
 // instead of every step.  At an exchange every wave publishes its kLazyCand
 // best points (running distance, index, xyz; largest distance first, smaller
@@ -601,8 +702,13 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
     static_assert(NW <= 8 && P <= 32, "shape");
     constexpr int RPT = kLazyMaxWaves / T;  // records read per thread at most
     constexpr int CPT = RPT * kLazyCand;    // candidates held per thread at most
-    __shared__ float4 pend[kLazyMaxPending];
-    __shared__ WaveBest slots[2][8];
+    constexpr int CW = kLazyMaxWaves * kLazyCand / kWave;  // candidates per lane in a run
+    // The exchange's candidates (record r's candidate c at r * kLazyCand + c):
+    // x, y, z and the key's bits; the index.
+    __shared__ float4 cand_xyzk[kLazyMaxWaves * kLazyCand];
+    __shared__ uint32_t cand_idx[kLazyMaxWaves * kLazyCand];
+    __shared__ float4 live_xyzk[NW][kLazyLive];  // per wave: the run's live candidates
+    __shared__ uint32_t live_idx[NW][kLazyLive];
     __shared__ int wave_bound[NW];
     __shared__ int abort_flag;
 
@@ -643,24 +749,18 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
     }
     if (tid == 0) {
         abort_flag = 0;
-        pend[0] = make_float4(xyz[3 * static_cast<int64_t>(start)],
-                              xyz[3 * static_cast<int64_t>(start) + 1],
-                              xyz[3 * static_cast<int64_t>(start) + 2], 0.f);
         if (g == 0) out[0] = start;
     }
-    int npend = 1;
-    int64_t step = 1;
-    int sim_par = 0;
-    for (uint32_t exch = 0; step < npoint; ++exch) {
-        __syncthreads();  // pend[] complete
-        // Apply the centroids chosen since the last exchange.
-        for (int i = 0; i < npend; ++i) {
-            const float4 c = pend[i];
+    {
+        const float sx = xyz[3 * static_cast<int64_t>(start)];
+        const float sy = xyz[3 * static_cast<int64_t>(start) + 1];
+        const float sz = xyz[3 * static_cast<int64_t>(start) + 2];
 #pragma unroll
-            for (int k = 0; k < P; ++k)
-                md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z));
-        }
-        npend = 0;
+        for (int k = 0; k < P; ++k) md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], sx, sy, sz));
+    }
+    int64_t step = 1;
+    for (uint32_t exch = 0; step < npoint; ++exch) {
+        __syncthreads();  // every wave is past the last run's reads of the candidates
 
         // This wave's kLazyCand best points and its bound, by repeated wave
         // maxima (first lane, then first slot, holding the maximum: the
@@ -759,6 +859,16 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
         }
         bmax = wave_max_i32_l63(bmax);
         if (lane == 0) wave_bound[wave] = bmax;
+#pragma unroll
+        for (int j = 0; j < RPT; ++j) {
+#pragma unroll
+            for (int c = 0; c < kLazyCand; ++c) {
+                const int id = (tid + j * T) * kLazyCand + c;
+                cand_xyzk[id] = make_float4(cx_[j * kLazyCand + c], cy_[j * kLazyCand + c],
+                                            cz_[j * kLazyCand + c], i2f(cmd[j * kLazyCand + c]));
+                cand_idx[id] = static_cast<uint32_t>(cidx[j * kLazyCand + c]);
+            }
+        }
         __syncthreads();
         if (abort_flag) {  // uniform: written before the barrier
             // Slots from `step` on were never written: mark them -1 so a
@@ -771,55 +881,17 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
 #pragma unroll
         for (int w = 1; w < NW; ++w) bound = max(bound, wave_bound[w]);
 
-        // Steps over the candidates alone.
-        for (bool first = true; step < npoint; first = false) {
-            int bv = static_cast<int>(0x80000000u), bi = 0x7FFFFFFF;
-            float bx = 0.f, by = 0.f, bz = 0.f;
+        // Steps over the candidates alone, by every wave on its own (no
+        // barrier); each is applied at once to this thread's points.
+        lazy_steps<CW>(cand_xyzk, cand_idx, bound, lane, live_xyzk[wave], live_idx[wave],
+                       static_cast<int>(min<int64_t>(npoint - step, INT32_MAX)),
+                       [&](const float4& c, uint32_t index) {
+                           if (g == 0 && tid == 0) out[step] = index;
+                           ++step;
 #pragma unroll
-            for (int j = 0; j < CPT; ++j) {
-                const bool better = cmd[j] > bv || (cmd[j] == bv && cidx[j] < bi);
-                bv = better ? cmd[j] : bv;
-                bi = better ? cidx[j] : bi;
-                bx = better ? cx_[j] : bx;
-                by = better ? cy_[j] : by;
-                bz = better ? cz_[j] : bz;
-            }
-            const int wv = wave_max_i32_l63(bv);
-            const int wneg = wave_max_i32_l63(bv == wv ? -bi : static_cast<int>(0x80000000u));
-            const int wl = static_cast<int>(__builtin_ctzll(ballot(bv == wv && -bi == wneg)));
-            WaveBest* buf = slots[sim_par];
-            sim_par ^= 1;
-            const float wx = i2f(readlane(f2i(bx), wl));
-            const float wy = i2f(readlane(f2i(by), wl));
-            const float wz = i2f(readlane(f2i(bz), wl));
-            if (lane == 0) {
-                WaveBest e;
-                e.key = wv;
-                e.index = -wneg;
-                e.x = wx;
-                e.y = wy;
-                e.z = wz;
-                e.pad[0] = e.pad[1] = e.pad[2] = 0;
-                buf[wave] = e;
-            }
-            __syncthreads();
-            WaveBest best = buf[0];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) {
-                const WaveBest e = buf[w];
-                if (e.key > best.key || (e.key == best.key && e.index < best.index)) best = e;
-            }
-            if (!first && !(best.key > bound)) break;  // an unpublished point may tie or beat it
-            if (g == 0 && tid == 0) out[step] = best.index;
-            if (tid == 0) pend[npend] = make_float4(best.x, best.y, best.z, 0.f);
-            ++npend;
-            ++step;
-#pragma unroll
-            for (int j = 0; j < CPT; ++j)
-                cmd[j] = f2i(running_min(i2f(cmd[j]),
-                                         sqdist3(cx_[j], cy_[j], cz_[j], best.x, best.y, best.z)));
-            if (npend == kLazyMaxPending) break;
-        }
+                           for (int k = 0; k < P; ++k)
+                               md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], c.x, c.y, c.z));
+                       });
     }
 }
 
@@ -847,8 +919,12 @@ __global__ __launch_bounds__(T) void fps_stream_kernel(
     constexpr int NW = T / kWave;
     static_assert(NW <= 8 && kLazyCand == 1, "shape");
     constexpr int RPT = kLazyMaxWaves / T;  // records read per thread at most
+    constexpr int CW = kLazyMaxWaves / kWave;  // candidates per lane in a run
     __shared__ float4 pend[kLazyMaxPending];
-    __shared__ WaveBest slots[2][8];
+    __shared__ float4 cand_xyzk[kLazyMaxWaves];  // the exchange's candidates: x, y, z, key bits
+    __shared__ uint32_t cand_idx[kLazyMaxWaves];
+    __shared__ float4 live_xyzk[NW][kLazyLive];  // per wave: the run's live candidates
+    __shared__ uint32_t live_idx[NW][kLazyLive];
     __shared__ int wave_bound[NW];
     __shared__ int abort_flag;
 
@@ -867,9 +943,8 @@ __global__ __launch_bounds__(T) void fps_stream_kernel(
     }
     int npend = 1;
     int64_t step = 1;
-    int sim_par = 0;
     for (uint32_t exch = 0; step < npoint; ++exch) {
-        __syncthreads();  // pend[] complete
+        __syncthreads();  // pend[] complete; every wave is past the last run's reads
         // Stream the chunk: apply the pending centroids, keep this lane's
         // best point (running distance, index, xyz) and its second value.
         int bv = static_cast<int>(0x80000000u), sv = static_cast<int>(0x80000000u);
@@ -1005,6 +1080,11 @@ __global__ __launch_bounds__(T) void fps_stream_kernel(
         }
         bmax = wave_max_i32_l63(bmax);
         if (lane == 0) wave_bound[wave] = bmax;
+#pragma unroll
+        for (int r = 0; r < RPT; ++r) {
+            cand_xyzk[tid + r * T] = make_float4(cx_[r], cy_[r], cz_[r], i2f(cmd[r]));
+            cand_idx[tid + r * T] = cidx[r];
+        }
         __syncthreads();
         if (abort_flag) {  // uniform: written before the barrier
             if (g == 0)
@@ -1015,58 +1095,16 @@ __global__ __launch_bounds__(T) void fps_stream_kernel(
 #pragma unroll
         for (int w = 1; w < NW; ++w) bound = max(bound, wave_bound[w]);
 
-        // Steps over the candidates alone (as in fps_lazy_kernel).
-        for (bool first = true; step < npoint; first = false) {
-            int sbv = static_cast<int>(0x80000000u);
-            uint32_t sbi = 0xFFFFFFFFu;
-            float sx = 0.f, sy = 0.f, sz = 0.f;
-#pragma unroll
-            for (int r = 0; r < RPT; ++r) {
-                const bool better = cmd[r] > sbv || (cmd[r] == sbv && cidx[r] < sbi);
-                sbv = better ? cmd[r] : sbv;
-                sbi = better ? cidx[r] : sbi;
-                sx = better ? cx_[r] : sx;
-                sy = better ? cy_[r] : sy;
-                sz = better ? cz_[r] : sz;
-            }
-            const int swv = wave_max_i32_l63(sbv);
-            const uint32_t sci = sbv == swv ? sbi : 0xFFFFFFFFu;
-            const uint32_t cmin = ~wave_max_u32_l63(~sci);
-            const int swl = static_cast<int>(__builtin_ctzll(ballot(sbv == swv && sci == cmin)));
-            WaveBest* buf = slots[sim_par];
-            sim_par ^= 1;
-            const float wx = i2f(readlane(f2i(sx), swl));
-            const float wy = i2f(readlane(f2i(sy), swl));
-            const float wz = i2f(readlane(f2i(sz), swl));
-            if (lane == 0) {
-                WaveBest e;
-                e.key = swv;
-                e.index = static_cast<int>(cmin);  // bit pattern of the uint32 index
-                e.x = wx;
-                e.y = wy;
-                e.z = wz;
-                e.pad[0] = e.pad[1] = e.pad[2] = 0;
-                buf[wave] = e;
-            }
-            __syncthreads();
-            WaveBest best = buf[0];
-#pragma unroll
-            for (int w = 1; w < NW; ++w) {
-                const WaveBest e = buf[w];
-                if (e.key > best.key ||
-                    (e.key == best.key && static_cast<uint32_t>(e.index) < static_cast<uint32_t>(best.index)))
-                    best = e;
-            }
-            if (!first && !(best.key > bound)) break;  // an unpublished point may tie or beat it
-            if (g == 0 && tid == 0) out[step] = static_cast<int64_t>(static_cast<uint32_t>(best.index));
-            if (tid == 0) pend[npend] = make_float4(best.x, best.y, best.z, 0.f);
-            ++npend;
-            ++step;
-#pragma unroll
-            for (int r = 0; r < RPT; ++r)
-                cmd[r] = f2i(running_min(i2f(cmd[r]), sqdist3(cx_[r], cy_[r], cz_[r], best.x, best.y, best.z)));
-            if (npend == kLazyMaxPending) break;
-        }
+        // Steps over the candidates alone, by every wave on its own (no
+        // barrier; wave 0 records the centroids for the next exchange).
+        lazy_steps<CW>(cand_xyzk, cand_idx, bound, lane, live_xyzk[wave], live_idx[wave],
+                       static_cast<int>(min<int64_t>(npoint - step, kLazyMaxPending - npend)),
+                       [&](const float4& c, uint32_t index) {
+                           if (g == 0 && tid == 0) out[step] = static_cast<int64_t>(index);
+                           if (tid == 0) pend[npend] = make_float4(c.x, c.y, c.z, 0.f);
+                           ++npend;
+                           ++step;
+                       });
     }
 }
 
