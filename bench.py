@@ -240,6 +240,72 @@ def cpu_baseline(xyz_cpu: torch.Tensor, clouds: int, warmup: int = 3, repeats: i
     }
 
 
+def cpu_baseline_other(config: str) -> dict:
+    """The reference's CPU algorithms (PyTorch-CPU port) on a bounded sample
+    of configs 1, 3, 4 and 5, scaled to the config's metric: one untimed
+    pass, then the median of 3 timed passes."""
+    import statistics
+
+    sys.path.insert(0, str(ROOT))
+    from oracle import torch_port
+
+    torch.set_num_threads(os.cpu_count() or 1)
+
+    def median_time(fn) -> float:
+        fn()
+        times = []
+        for _ in range(3):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        return statistics.median(times)
+
+    if config == "c1":
+        x = make_c1()
+        B, N, _ = x.shape
+        c = x.gather(1, torch_port.furthest_point_sample(x, 512)[..., None].expand(-1, -1, 3))
+        t_fps = median_time(lambda: torch_port.furthest_point_sample(x, 512))
+        t_ball = median_time(lambda: torch_port.ball_query(c, x, 0.2, 32))
+        t_knn = median_time(lambda: torch_port.knn(c, x, 16))
+        value, unit = B * N / (t_fps + t_ball + t_knn), "points/s"
+        sample = (f"the whole workload; medians fps {t_fps:.3f}s ball {t_ball:.3f}s "
+                  f"knn {t_knn:.3f}s")
+    elif config == "c3":
+        x = make_c3()
+        N = x.shape[1]
+        steps, queries = 256, 64
+        c = x[:, torch.randperm(N, generator=torch.Generator().manual_seed(3))[:queries]]
+        t_fps = median_time(lambda: torch_port.furthest_point_sample(x, steps)) * 16384 / steps
+        t_ball = median_time(lambda: torch_port.ball_query(c, x, 0.5, 32)) * 16384 / queries
+        value, unit = N / (t_fps + t_ball), "points/s"
+        sample = (f"FPS: the first {steps} of 16384 steps (x {16384 // steps}); ball query: "
+                  f"{queries} of the 16384 queries over all 2^20 points (x {16384 // queries}); "
+                  f"scaled fps {t_fps:.1f}s ball {t_ball:.1f}s")
+    elif config == "c4":
+        ref, query, _ = make_c4()
+        M = query.shape[1]
+        sub = 256
+        t_knn = median_time(lambda: torch_port.knn(query[:, :sub], ref, 16)) * M / sub
+        value, unit = M / t_knn, "queries/s"
+        sample = f"{sub} of the {M} queries against all 2^20 references (x {M // sub}): {t_knn:.1f}s"
+    else:
+        y1, y2 = make_c5()
+        B, P, _ = y1.shape
+        clouds = 2
+
+        def fwd_bwd():
+            a = y1[:clouds].clone().requires_grad_()
+            b = y2[:clouds].clone().requires_grad_()
+            torch_port.chamfer_l2(a, b).backward()
+
+        t = median_time(fwd_bwd) * B / clouds
+        value, unit = 2 * B * P / t, "points/s"
+        sample = f"{clouds} of the {B} clouds, forward + backward (x {B // clouds}): {t:.1f}s"
+    return {"value": value, "unit": unit, "cores": torch.get_num_threads(), "kind": "port",
+            "sample": "PyTorch-CPU port of the reference's CPU path, " + sample,
+            "cpu": cpu_info()}
+
+
 def timed_steps(step, steps: int, warmup: int) -> float:
     """Seconds per step over exactly `steps` steps after `warmup` untimed ones,
     synchronised on both sides."""
@@ -636,6 +702,8 @@ def main() -> None:
         probe()
         return
     result = run(args) if args.config == "c2" else run_other(args)
+    if args.config != "c2" and not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline_other(args.config)
     print(json.dumps(result))
 
 

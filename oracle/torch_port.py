@@ -4,7 +4,11 @@ baseline that bench.py times beside the GPU (cpu_baseline.kind = "port").
 TEST INFRASTRUCTURE ONLY: the shipped package never imports this module.
 Each function restates /root/reference/mps_pointops/reference.py:
 furthest_point_sample (:27-58), knn (:61-80, cdist + topk, the reference's
-own CPU kNN) and ball_query (:83-121, chunks of at most 2**24 pairs).
+own CPU kNN) and ball_query (:83-121, chunks of at most 2**24 pairs); and
+the squared-L2 Chamfer loss of /root/reference/mps_pointops/chamfer.py on
+CPU tensors: first nearest neighbour by tiles of coordinate differences
+(_nearest_indices, :162-230), the selected squared distance with autograd
+(_selected_squared_distance, :297-308), mean over points and batch.
 """
 
 from __future__ import annotations
@@ -58,3 +62,26 @@ def ball_query(query: Tensor, ref: Tensor, radius: float, K: int) -> tuple[Tenso
         idx[:, lo:lo + step, :kk] = torch.where(valid, first, -1)
         dist2[:, lo:lo + step, :kk] = torch.where(valid, d2.gather(-1, first.clamp(max=N - 1)), 0.0)
     return dist2, idx
+
+
+def nearest_indices(query: Tensor, ref: Tensor, tile: int = 1 << 22) -> Tensor:
+    """First minimum of the coordinate-difference squared distance (B, M)."""
+    B, M, _ = query.shape
+    N = ref.shape[1]
+    q_step = max(1, min(M, tile // max(1, B * N)))
+    out = torch.empty(B, M, dtype=torch.long)
+    for q0 in range(0, M, q_step):
+        d2 = _sqdist(query[:, q0:q0 + q_step, None, :], ref[:, None, :, :])
+        out[:, q0:q0 + q_step] = d2.argmin(-1)  # first minimum
+    return out
+
+
+def chamfer_l2(x: Tensor, y: Tensor) -> Tensor:
+    """Mean/mean squared-L2 Chamfer loss of equal-length clouds, both
+    directions, differentiable in x and y."""
+    def directed(a: Tensor, b: Tensor) -> Tensor:
+        with torch.no_grad():
+            ia = nearest_indices(a, b)
+        near = b.gather(1, ia[..., None].expand(-1, -1, 3))
+        return _sqdist(a, near).mean(dim=1)
+    return (directed(x, y) + directed(y, x)).mean()
