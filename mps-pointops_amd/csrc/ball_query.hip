@@ -187,21 +187,24 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
                 const bool h1 = (decltype(full)::value || j1 < n) && d1 < r2;
                 const uint64_t m0 = ballot(h0), m1 = ballot(h1);
                 if ((m0 | m1) == 0) continue;
-                const int s0 = found + lanes_below(m0);
-                const int s1 = found + __popcll(m0) + lanes_below(m1);
+                // Slots and indices are non-negative: unsigned, so that the
+                // 64-bit addresses and index values need no sign extension.
+                const uint32_t s0 = static_cast<uint32_t>(found + lanes_below(m0));
+                const uint32_t s1 = static_cast<uint32_t>(found + __popcll(m0) + lanes_below(m1));
+                const uint32_t uk = static_cast<uint32_t>(K);
                 if constexpr (PN2) {
                     if (found == 0)
                         first = m0 != 0 ? base + c * kWave + static_cast<int>(__builtin_ctzll(m0))
                                         : base + (c + 1) * kWave + static_cast<int>(__builtin_ctzll(m1));
-                    if (h0 && s0 < K) oi32[s0] = j0;
-                    if (h1 && s1 < K) oi32[s1] = j1;
+                    if (h0 && s0 < uk) oi32[s0] = j0;
+                    if (h1 && s1 < uk) oi32[s1] = j1;
                 } else {
-                    if (h0 && s0 < K) {
-                        oi[s0] = j0;
+                    if (h0 && s0 < uk) {
+                        oi[s0] = static_cast<int64_t>(static_cast<uint32_t>(j0));
                         od[s0] = d0;
                     }
-                    if (h1 && s1 < K) {
-                        oi[s1] = j1;
+                    if (h1 && s1 < uk) {
+                        oi[s1] = static_cast<int64_t>(static_cast<uint32_t>(j1));
                         od[s1] = d1;
                     }
                 }
