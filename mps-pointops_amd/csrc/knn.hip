@@ -533,17 +533,11 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     }
 }
 
-// With `list` set, the queries are the first list_count[b] entries of
-// list[b*M ...] (query rows of cloud b, in any order) instead of all M: the
-// workgroups of a cloud take 64 entries each and those past the count return
-// at once.  Such launches deal workgroups round-robin over the XCDs (a short
-// list then still spreads over the chip).
 template <int KMAX, int NW, int CAP>
 __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
     int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K, const float4* __restrict__ sorted,
-    const int* __restrict__ home, const int* __restrict__ list_count,
-    const int* __restrict__ list) {
+    const int* __restrict__ home) {
     // Per wave: the candidate buffer during the scan, then the final list.
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
     __shared__ uint32_t window_max[kWave];  // per lane: the Morton-window limit
@@ -554,18 +548,10 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const int lane = lane_id();
     const int wave = uniform(threadIdx.x / kWave);
     const uint32_t per_cloud = static_cast<uint32_t>((M + kWave - 1) / kWave);
-    const CloudBlock cb = list == nullptr ? cloud_block(per_cloud)
-                                          : CloudBlock{blockIdx.x % per_cloud, blockIdx.x / per_cloud};
+    const CloudBlock cb = cloud_block(per_cloud);
     const int64_t b = cb.b;
-    int64_t m = static_cast<int64_t>(cb.x) * kWave + lane;
-    bool active = m < M;
-    if (list != nullptr) {
-        const int64_t first = static_cast<int64_t>(cb.x) * kWave;
-        const int64_t count = list_count[b];
-        if (first >= count) return;  // uniform over the workgroup, before any barrier
-        active = first + lane < count;
-        m = list[b * M + (active ? first + lane : first)];
-    }
+    const int64_t m = static_cast<int64_t>(cb.x) * kWave + lane;
+    const bool active = m < M;
     const float* qp = query + 3 * (b * M + (active ? m : 0));
     const float qx = qp[0], qy = qp[1], qz = qp[2];
     const float* rp = ref + 3 * b * N;
@@ -861,8 +847,7 @@ hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, i
 template <int KMAX>
 hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                        int64_t M, int64_t N, int K, hipStream_t stream,
-                       const WindowLayout* window = nullptr, const int* list_count = nullptr,
-                       const int* list = nullptr) {
+                       const WindowLayout* window = nullptr) {
     const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave * B));  // cloud_block order
     // Small lists: 8 waves per 64 queries (more waves in flight, 16-entry
     // buffers); K up to 32: 4 waves with 32-entry buffers.
@@ -870,7 +855,7 @@ hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_
     constexpr int CAP = KMAX <= 16 ? 16 : 32;
     hipLaunchKernelGGL((knn3_lane_kernel<KMAX, NW, CAP>), grid, dim3(NW * kWave), 0, stream, query,
                        ref, dist, idx, M, N, K, window ? window->sorted : nullptr,
-                       window ? window->home : nullptr, list_count, list);
+                       window ? window->home : nullptr);
     return hipGetLastError();
 }
 
@@ -925,14 +910,6 @@ bool grid_ok(int64_t rows) { return (rows + kKnnWaves - 1) / kKnnWaves <= INT32_
 
 }  // namespace
 
-hipError_t knn3_lane_listed(const float* query, const float* ref, float* dist, int64_t* idx,
-                            int64_t B, int64_t M, int64_t N, int K, const int* list_count,
-                            const int* list, hipStream_t stream) {
-    if (K < 1 || K > 32 || (M + kWave - 1) / kWave * B > INT32_MAX) return hipErrorInvalidValue;
-    if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, K, stream, nullptr, list_count, list);
-    if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, K, stream, nullptr, list_count, list);
-    return launch_lane<32>(query, ref, dist, idx, B, M, N, K, stream, nullptr, list_count, list);
-}
 
 }  // namespace pointops
 

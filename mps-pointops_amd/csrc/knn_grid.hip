@@ -21,8 +21,13 @@
 //      less a slack for float rounding (box_bound), else grows the box by
 //      that face.  A non-finite query or a batch with non-finite
 //      references lists the wave's queries, a walk that needs more than
-//      kGridMaxGrow faces its own query, for a linear pass in the same call
-//      (knn3_lane_listed: the brute-force lane kernel over the listed rows).
+//      kGridMaxGrow faces its own query;
+//   4. grid_list_kernel: the listed queries compacted in sorted-position
+//      order, and the bounding box of every chunk of kChunkRefs sorted
+//      references;
+//   5. knn3_listed_kernel: a linear pass over the listed queries, 64 per
+//      workgroup, that skips the chunks whose box is farther from every lane
+//      than an upper bound on its K-th distance.
 #include <algorithm>
 
 #include "pointops_common.hpp"
@@ -37,12 +42,19 @@ constexpr int kGridScanTile = 8 * kGridPrepThreads;
 constexpr int kGridMaxDim = 1024;
 constexpr int kGridSearchWaves = 4;
 constexpr int kGridCap = 16;  // buffered candidates per lane
-constexpr int kGridMaxGrow = 24;  // box faces a lane may add before the wave scans everything
+constexpr int kGridMaxGrow = 8;  // box faces a quad may add before its query is listed (measured best of 4-24)
 // Nearest mode: box faces a lane may add before its query is left to the
 // fill pass (measured best of 4-24).
 constexpr int kGridNearestGrow = 6;
 constexpr int kGridQueriesPerWave = kWave / 4;  // one quad of lanes per query
 constexpr uint32_t kGridMatchLimit = 0x7F800001u;  // keys below: finite or +inf
+// Listed queries (those the search leaves to a linear pass) are compacted in
+// tiles of query positions; the linear pass prunes chunks of kChunkRefs
+// consecutive sorted references by their bounding boxes.
+constexpr int64_t kListTileMin = 2048;
+constexpr int64_t kListTilesMax = 1024;
+constexpr int kChunkRefs = 256;
+constexpr int kSuperChunks = 16;
 
 struct alignas(16) GridParams {
     float lo[3];
@@ -75,8 +87,17 @@ struct GridLayout {
     int* q_rank;     // [B][M]
     float4* sorted;  // [B][N]: x, y, z, index bits
     int* q_order;    // [B][M]
+    int* list_total; // [B]: listed queries per cloud (the search raises it to 1 first)
+    int* list_tiles; // [B][ltiles]: listed queries per tile of query positions
+    int* list;       // [B][M]: listed query rows in sorted-position order
+    float4* boxes;   // [B][chunks][2]: bounding box of each chunk of sorted references
+    float4* supers;  // [B][supers][2]: bounding box of each kSuperChunks chunks
     int64_t stride;  // cap + 2 rounded up to whole 16-byte words
     int64_t tiles;   // scan tiles per array
+    int64_t ltile;   // query positions per list tile (a multiple of kListTileMin)
+    int64_t ltiles;  // list tiles per cloud (at most kListTilesMax)
+    int64_t chunks;  // reference chunks per cloud
+    int64_t nsupers; // chunk groups per cloud
 };
 
 __host__ __device__ inline size_t align256(size_t v) { return (v + 255) & ~static_cast<size_t>(255); }
@@ -101,6 +122,14 @@ __host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_
     const size_t p_qrank = take(static_cast<size_t>(B * M) * sizeof(int));
     const size_t p_sorted = take(static_cast<size_t>(B * N) * sizeof(float4));
     const size_t p_qord = take(static_cast<size_t>(B * M) * sizeof(int));
+    const int64_t ltile = kListTileMin * ((M + kListTileMin * kListTilesMax - 1) / (kListTileMin * kListTilesMax));
+    const int64_t ltiles = (M + ltile - 1) / ltile;
+    const int64_t chunks = (N + kChunkRefs - 1) / kChunkRefs;
+    const size_t p_ltot = take(static_cast<size_t>(B + B * ltiles) * sizeof(int));
+    const size_t p_list = take(static_cast<size_t>(B * M) * sizeof(int));
+    const size_t p_box = take(static_cast<size_t>(B * chunks) * 2 * sizeof(float4));
+    const int64_t supers = (chunks + kSuperChunks - 1) / kSuperChunks;
+    const size_t p_sup = take(static_cast<size_t>(B * supers) * 2 * sizeof(float4));
     if (out != nullptr) {
         out->control = reinterpret_cast<int*>(base + p_ctrl);
         out->gate = nullptr;
@@ -113,8 +142,17 @@ __host__ __device__ inline size_t grid_layout_bytes(int64_t B, int64_t M, int64_
         out->q_rank = reinterpret_cast<int*>(base + p_qrank);
         out->sorted = reinterpret_cast<float4*>(base + p_sorted);
         out->q_order = reinterpret_cast<int*>(base + p_qord);
+        out->list_total = reinterpret_cast<int*>(base + p_ltot);
+        out->list_tiles = out->list_total + B;
+        out->list = reinterpret_cast<int*>(base + p_list);
+        out->boxes = reinterpret_cast<float4*>(base + p_box);
+        out->supers = reinterpret_cast<float4*>(base + p_sup);
         out->stride = stride;
         out->tiles = tiles;
+        out->ltile = ltile;
+        out->ltiles = ltiles;
+        out->chunks = chunks;
+        out->nsupers = supers;
     }
     return o;
 }
@@ -134,16 +172,34 @@ __device__ __forceinline__ int cell_axis(float v, float lo, float inv_h, int dim
     return static_cast<int>(fminf(fmaxf(t, 0.f), static_cast<float>(dim - 1)));
 }
 
-// Query order key: the 2 x 2 x 2 block of cells holding the point (blocks
-// in x-fastest order), so that 64 consecutive queries form a compact group;
-// non-finite queries go to block 0.  Keys stay below the cell count.
+// Query order key: the 2 x 2 x 2 block of cells holding the point, blocks in
+// Morton order (the bits of the three block coordinates interleaved from the
+// lowest, an axis dropping out once its bits are used), scaled into
+// [0, cells) -- a monotone map, so 64 consecutive queries stay a compact group
+// for the searches and the linear pass.  Non-finite queries go to key 0.
 __device__ __forceinline__ int query_key(const GridParams& P, float x, float y, float z) {
     if (!finite3(x, y, z)) return 0;
-    const int bx = cell_axis(x, P.lo[0], P.inv_h, P.dims[0]) >> 1;
-    const int by = cell_axis(y, P.lo[1], P.inv_h, P.dims[1]) >> 1;
-    const int bz = cell_axis(z, P.lo[2], P.inv_h, P.dims[2]) >> 1;
-    const int nbx = (P.dims[0] + 1) >> 1, nby = (P.dims[1] + 1) >> 1;
-    return bx + nbx * (by + nby * bz);
+    const float v[3] = {x, y, z};
+    uint32_t k = 0;
+    int o = 0;
+    int c[3], w[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        c[a] = cell_axis(v[a], P.lo[a], P.inv_h, P.dims[a]) >> 1;
+        const int nb = (P.dims[a] + 1) >> 1;
+        w[a] = nb > 1 ? 32 - __clz(nb - 1) : 0;
+    }
+#pragma unroll
+    for (int bit = 0; bit < 10; ++bit) {
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            if (bit < w[a]) {
+                k |= ((static_cast<uint32_t>(c[a]) >> bit) & 1u) << o;
+                ++o;
+            }
+        }
+    }
+    return static_cast<int>((static_cast<uint64_t>(k) * static_cast<uint64_t>(P.cells)) >> o);
 }
 
 // Cell of a point; non-finite points go to the overflow cell `cells`.
@@ -594,8 +650,7 @@ __device__ __forceinline__ float box_bound(const GridParams& P, float h, const f
 template <int S>
 __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
-    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K, int nearest,
-    int* __restrict__ miss_count, int* __restrict__ miss_list) {
+    int64_t* __restrict__ out_idx, int64_t B, int64_t M, int64_t N, int K, int nearest) {
     constexpr int KMAX = 4 * S;
     __shared__ uint2 bufs[kGridSearchWaves][kGridCap][kWave];
     const int lane = lane_id();
@@ -607,7 +662,8 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
     const int64_t gw = static_cast<int64_t>(xcd_local_block(blockIdx.x, gridDim.x)) * kGridSearchWaves + wave;
     if (gw >= B * groups) return;  // whole wave; no barriers in this kernel
     const int64_t b = gw / groups;
-    const int64_t pos = (gw - b * groups) * kGridQueriesPerWave + (lane >> 2);
+    const int64_t pos0 = (gw - b * groups) * kGridQueriesPerWave;
+    const int64_t pos = pos0 + (lane >> 2);
     const bool active = pos < M;
     const int m = active ? L.q_order[b * M + pos] : 0;
     const float* qp = query + 3 * (b * M + m);
@@ -737,18 +793,22 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void knn3_grid_kernel(
             if (has) p += 32;
         }
     }
-    // A listed query goes to its cloud's list (one atomic per query), and the
-    // linear pass of the same call writes its results.
-    if (full) {
-        if (active && qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
-        return;  // whole wave
+    // Every query's mark at its sorted position (in q_rank, dead since the
+    // scatter): its row when listed, else -1.  The wave adds its listed count
+    // to its positions' tile (a wave's 16 positions never straddle one) and
+    // raises the cloud's flag; the list pass compacts the marks in position
+    // order, so neighbours in space stay together, and the linear pass of the
+    // same call writes the listed queries' results.
+    listed = listed || full;
+    const uint64_t lm = ballot(active && listed && qi == 3);
+    if (lm != 0 && lane == 0) {
+        atomicAdd(&L.list_tiles[b * L.ltiles + pos0 / L.ltile], __popcll(lm));
+        L.list_total[b] = 1;
     }
+    if (active && qi == 3) L.q_rank[b * M + pos] = listed ? m : -1;
+    if (full) return;  // whole wave
     quad_merge<S>(slot, tau, buf, lane, cnt);
-    if (!active) return;
-    if (listed) {
-        if (qi == 3) miss_list[b * M + atomicAdd(&miss_count[b], 1)] = m;
-        return;
-    }
+    if (!active || listed) return;
     const int64_t row = (b * M + m) * K;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
@@ -788,7 +848,8 @@ __global__ __launch_bounds__(kGridSearchWaves * kWave) void ball3_grid_kernel(
     const int64_t gw = static_cast<int64_t>(xcd_local_block(blockIdx.x, gridDim.x)) * kGridSearchWaves + wave;
     if (gw >= B * groups) return;  // whole wave; no barriers in this kernel
     const int64_t b = gw / groups;
-    const int64_t pos = (gw - b * groups) * kGridQueriesPerWave + (lane >> 2);
+    const int64_t pos0 = (gw - b * groups) * kGridQueriesPerWave;
+    const int64_t pos = pos0 + (lane >> 2);
     const bool active = pos < M;
     const int m = active ? L.q_order[b * M + pos] : 0;
     const float* qp = query + 3 * (b * M + m);
@@ -1008,6 +1069,353 @@ __global__ __launch_bounds__(kFillThreads) void nearest_fill_kernel(
     idx[row] = i;
 }
 
+// After the search, per cloud with listed queries: blocks [0, ltiles)
+// compact the marks of their tile of query positions into L.list, in
+// position order after the listed queries of the tiles before (block 0 also
+// stores the cloud's total); with `boxes`, blocks from ltiles on give each
+// wave one chunk of kChunkRefs sorted references, or one group of
+// kSuperChunks chunks, and store its bounding box (lo, hi), or (-inf, +inf)
+// when it holds a non-finite coordinate.
+// Clouds with nothing listed return at once.
+constexpr int kListWaves = kGridPrepThreads / kWave;
+constexpr int kListRounds = 8;  // ballots per wave per pass: 2048 positions per block pass
+
+__global__ __launch_bounds__(kGridPrepThreads) void grid_list_kernel(GridLayout L, int64_t N,
+                                                                     int64_t M) {
+    const int64_t b = blockIdx.y;
+    if (L.list_total[b] == 0) return;  // uniform, before any barrier (1 or the total: both nonzero)
+    __shared__ int red[kListWaves];
+    __shared__ int counts[kListRounds][kListWaves];
+    const int lane = lane_id();
+    const int wave = threadIdx.x / kWave;
+    if (blockIdx.x >= L.ltiles) {
+        // Boxes: waves [0, chunks) take one chunk each, the next nsupers one
+        // group of kSuperChunks chunks each.
+        const int64_t w = (blockIdx.x - L.ltiles) * kListWaves + wave;
+        const bool group = w >= L.chunks;
+        const int64_t c = group ? w - L.chunks : w;
+        if (c >= (group ? L.nsupers : L.chunks)) return;  // whole wave; no barriers below
+        const int64_t span = group ? int64_t(kChunkRefs) * kSuperChunks : kChunkRefs;
+        const float4* srt = L.sorted + b * N + c * span;
+        const int n = static_cast<int>(min<int64_t>(span, N - c * span));
+        float lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
+        bool bad = false;
+        for (int t = lane; t < n; t += kWave) {
+            const float4 r = srt[t];
+            const float v[3] = {r.x, r.y, r.z};
+            bad = bad || !finite3(r.x, r.y, r.z);
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                lo[a] = isfinite(v[a]) ? fminf(lo[a], v[a]) : lo[a];
+                hi[a] = isfinite(v[a]) ? fmaxf(hi[a], v[a]) : hi[a];
+            }
+        }
+        const bool any_bad = ballot(bad) != 0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            lo[a] = any_bad ? -INFINITY : wave_min(lo[a]);
+            hi[a] = any_bad ? INFINITY : wave_max(hi[a]);
+        }
+        if (lane == 0) {
+            float4* box = group ? L.supers + 2 * (b * L.nsupers + c) : L.boxes + 2 * (b * L.chunks + c);
+            box[0] = make_float4(lo[0], lo[1], lo[2], 0.f);
+            box[1] = make_float4(hi[0], hi[1], hi[2], 0.f);
+        }
+        return;
+    }
+    const int64_t tile = blockIdx.x;
+    const int* tc = L.list_tiles + b * L.ltiles;
+    if (tile == 0) {
+        int t = 0;
+        for (int64_t i = threadIdx.x; i < L.ltiles; i += kGridPrepThreads) t += tc[i];
+        t = block_sum(t, red);
+        if (threadIdx.x == 0) L.list_total[b] = t;
+    }
+    if (tc[tile] == 0) return;  // uniform over the workgroup
+    int before = 0;
+    for (int64_t i = threadIdx.x; i < tile; i += kGridPrepThreads) before += tc[i];
+    before = block_sum(before, red);
+    const int* mark = L.q_rank + b * M;
+    int* out = L.list + b * M;
+    const int64_t end = min(M, (tile + 1) * L.ltile);
+    // Positions p0 + u * 256 + threadIdx.x, u < kListRounds: the list order
+    // is (u, wave, lane), which is position order.
+    for (int64_t p0 = tile * L.ltile; p0 < end; p0 += kListRounds * kGridPrepThreads) {
+        int v[kListRounds];
+        uint64_t bal[kListRounds];
+#pragma unroll
+        for (int u = 0; u < kListRounds; ++u) {
+            const int64_t p = p0 + u * kGridPrepThreads + threadIdx.x;
+            v[u] = p < end ? mark[p] : -1;
+            bal[u] = ballot(v[u] >= 0);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int u = 0; u < kListRounds; ++u) counts[u][wave] = __popcll(bal[u]);
+        }
+        __syncthreads();
+        int acc = 0;
+        int off[kListRounds];
+#pragma unroll
+        for (int u = 0; u < kListRounds; ++u) {
+            off[u] = 0;
+#pragma unroll
+            for (int w = 0; w < kListWaves; ++w) {
+                off[u] = w == wave ? acc : off[u];
+                acc += counts[u][w];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kListRounds; ++u)
+            if (v[u] >= 0) out[before + off[u] + lanes_below(bal[u])] = v[u];
+        before += acc;
+        __syncthreads();  // counts is rewritten by the next pass
+    }
+}
+
+// Insert this lane's `cnt` buffered (key, index) candidates into its list
+// of 64-bit words, ascending (KMAX - K zero words first, so the K-th entry
+// is the last slot); the wave loops while any lane has entries left.
+template <int KMAX>
+__device__ __forceinline__ void word_merge(uint64_t (&slot)[KMAX], const uint2* buf, int lane,
+                                           int cnt) {
+    for (int e = 0;; ++e) {
+        const bool has = e < cnt;
+        if (ballot(has) == 0) break;
+        const uint2 c = buf[e * kWave + lane];  // row e < max(cnt): inside the buffer
+        const uint64_t w = has ? grid_word(c.x, c.y) : ~0ull;
+        bool here = w < slot[KMAX - 1];
+        if (ballot(here) == 0) continue;
+#pragma unroll
+        for (int s = KMAX - 1; s > 0; --s) {
+            const bool prev = w < slot[s - 1];
+            slot[s] = prev ? slot[s - 1] : (here ? w : slot[s]);
+            here = prev;
+        }
+        slot[0] = here ? w : slot[0];
+    }
+}
+
+// The linear pass over the listed queries (64 consecutive entries of a
+// cloud's list per workgroup, neighbours in space), pruned by the chunk
+// boxes of grid_list_kernel.  The chunks c = wave (mod kListedWaves) belong to
+// wave `wave`.  First every wave bounds each lane's K-th key from above:
+// all references of a chunk of at least K lie within the distance to the
+// box's far corner, and the smallest such bound over the chunks is shared
+// in LDS.  Then a wave scans a chunk unless, for every lane, the distance
+// to the box exceeds both that bound and the smallest K-th key of the
+// waves' lists.  Both bounds are computed with the distance arithmetic on
+// the per-axis gaps fl(lo - q), fl(q - hi) (float subtraction and the sum of
+// squares are monotone, so every reference in the box has a key at or above
+// the near bound and at or below the far one), then widened by 2^-20 to
+// cover fused or unfused products.  Each lane keeps an ascending list of
+// (key, index) words, so the chunks' order does not matter, and the waves'
+// lists are merged at the end.  A non-finite query scans every chunk.
+constexpr int kListedWaves = 4;
+constexpr int kListedCap = 16;  // buffered candidates per lane
+constexpr int kListedBatch = 8;
+
+template <int KMAX>
+__global__ __launch_bounds__(kListedWaves * kWave) void knn3_listed_kernel(
+    const float* __restrict__ query, GridLayout L, float* __restrict__ out_dist,
+    int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K) {
+    constexpr int NW = kListedWaves;
+    constexpr int ROWS = KMAX > kListedCap ? KMAX : kListedCap;
+    __shared__ uint2 lds[NW][ROWS][kWave];
+    __shared__ uint32_t far_bits[kWave];
+    __shared__ uint4 taus[kWave];  // per lane: the K-th key of each wave's list
+    static_assert(NW == 4, "one 16-byte word of K-th keys per lane");
+    const int lane = lane_id();
+    const int wave = uniform(threadIdx.x / kWave);
+    const int64_t per_cloud = (M + kWave - 1) / kWave;
+    const int64_t b = blockIdx.x / per_cloud;
+    const int64_t first = (blockIdx.x - b * per_cloud) * kWave;
+    const int64_t count = L.list_total[b];
+    if (first >= count) return;  // uniform over the workgroup, before any barrier
+    const bool active = first + lane < count;
+    const int m = L.list[b * M + (active ? first + lane : first)];
+    const float* qp = query + 3 * (b * M + m);
+    const float qx = qp[0], qy = qp[1], qz = qp[2];
+    const bool qfin = finite3(qx, qy, qz);
+    const float4* box = L.boxes + 2 * b * L.chunks;
+    const float4* srt = L.sorted + b * N;
+    uint2* buf = &lds[wave][0][0];
+    uint32_t* my_tau = reinterpret_cast<uint32_t*>(&taus[lane]) + wave;
+    if (wave == 0) far_bits[lane] = 0x7F800000u;
+    *my_tau = 0xFFFFFFFFu;
+    __syncthreads();
+    // This wave's groups g = wave + NW i, i < mine (kSuperChunks chunks
+    // each), visited 64 at a time: lane l loads the box of the l-th, and the
+    // wave reads them in turn with readlane; a group some lane still needs
+    // has its chunk boxes loaded the same way (lane u: chunk u).
+    const float4* gbox = L.supers + 2 * b * L.nsupers;
+    const int64_t mine = L.nsupers > wave ? (L.nsupers - wave + NW - 1) / NW : 0;
+    auto rl = [](float v, int t) { return i2f(readlane(f2i(v), t)); };
+    // Squared distance from the query to box t of (lo, hi), computed as the
+    // references' keys are on the per-axis gaps, then lowered by 2^-20.
+    auto near_key = [&](const float4& lo, const float4& hi, int t) {
+        const float gx = qx - __builtin_amdgcn_fmed3f(qx, rl(lo.x, t), rl(hi.x, t));
+        const float gy = qy - __builtin_amdgcn_fmed3f(qy, rl(lo.y, t), rl(hi.y, t));
+        const float gz = qz - __builtin_amdgcn_fmed3f(qz, rl(lo.z, t), rl(hi.z, t));
+        return __float_as_uint(sqdist3(gx, gy, gz, 0.f, 0.f, 0.f) * (1.f - 0x1p-20f));
+    };
+
+    // Upper bound: the nearest far corner over the chunks of at least K.  A
+    // group nearer to no lane than its current bound cannot lower it (every
+    // chunk's far corner is at least the group's near distance).
+    {
+        float far = INFINITY;
+        for (int64_t i0 = 0; i0 < mine; i0 += kWave) {
+            const int64_t g = wave + NW * min<int64_t>(i0 + lane, mine - 1);
+            const float4 glo = gbox[2 * g], ghi = gbox[2 * g + 1];
+            const int nb = static_cast<int>(min<int64_t>(kWave, mine - i0));
+            for (int t = 0; t < nb; ++t) {
+                const uint32_t gn = near_key(glo, ghi, t);
+                if (ballot(active && qfin && __uint_as_float(gn) < far) == 0) continue;
+                const int64_t c0 = (wave + NW * (i0 + t)) * kSuperChunks;
+                const int nc = static_cast<int>(min<int64_t>(kSuperChunks, L.chunks - c0));
+                const int64_t cl = c0 + min(lane, nc - 1);
+                const float4 lo = box[2 * cl], hi = box[2 * cl + 1];
+                for (int u = 0; u < nc; ++u) {
+                    // Chunk u's box: the larger of |fl(lo - q)|, |fl(hi - q)| per axis.
+                    const float ax = fmaxf(fabsf(rl(lo.x, u) - qx), fabsf(rl(hi.x, u) - qx));
+                    const float ay = fmaxf(fabsf(rl(lo.y, u) - qy), fabsf(rl(hi.y, u) - qy));
+                    const float az = fmaxf(fabsf(rl(lo.z, u) - qz), fabsf(rl(hi.z, u) - qz));
+                    const float d = sqdist3(ax, ay, az, 0.f, 0.f, 0.f);
+                    if (N - (c0 + u) * kChunkRefs >= K) far = fminf(far, d);
+                }
+            }
+        }
+        far *= 1.f + 0x1p-20f;
+        if (active && qfin && far < INFINITY) atomicMin(&far_bits[lane], __float_as_uint(far));
+    }
+    __syncthreads();
+    const uint32_t farkey = qfin ? min(far_bits[lane], 0x7F800000u) : 0x7F800000u;
+
+    uint64_t slot[KMAX];
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s) slot[s] = (active && s >= KMAX - K) ? ~0ull : 0ull;
+    // Exclusive admission limit on keys: at or below the far bound and every
+    // wave's K-th key (a key above another wave's K-th cannot be among the
+    // K; an equal key can, with a smaller index).  Inactive lanes admit
+    // nothing.  Other waves' keys are read without synchronisation: they only
+    // decrease, so a stale one is a looser but valid limit.
+    auto limit = [&]() -> uint32_t {
+        const uint4 t = taus[lane];
+        const uint32_t k = min(min(farkey, min(t.x, t.y)), min(t.z, t.w));
+        return active ? k + 1u : 0u;
+    };
+    int cnt = 0;
+    uint32_t lim = limit();
+    auto drain = [&]() {
+        if (ballot(cnt > kListedCap - kListedBatch) != 0) {
+            word_merge<KMAX>(slot, buf, lane, cnt);
+            cnt = 0;
+            *my_tau = static_cast<uint32_t>(slot[KMAX - 1] >> 32);
+        }
+    };
+    // One chunk's references through uniform (scalar) loads, a batch ahead;
+    // a batch whose keys are all at or above every lane's limit costs no
+    // buffer traffic.
+    auto scan_chunk = [&](int64_t j0) {
+        const int n = static_cast<int>(min<int64_t>(kChunkRefs, N - j0));
+        const float4* cp = srt + j0;
+        float4 cur[kListedBatch];
+#pragma unroll
+        for (int u = 0; u < kListedBatch; ++u) cur[u] = cp[min(u, n - 1)];
+        for (int r0 = 0; r0 < n; r0 += kListedBatch) {
+            const int rn = r0 + kListedBatch < n ? r0 + kListedBatch : r0;
+            float4 nxt[kListedBatch];
+#pragma unroll
+            for (int u = 0; u < kListedBatch; ++u) nxt[u] = cp[min(rn + u, n - 1)];
+            uint32_t key[kListedBatch];
+            uint32_t least = 0xFFFFFFFFu;
+#pragma unroll
+            for (int u = 0; u < kListedBatch; ++u) {
+                key[u] = r0 + u < n
+                    ? static_cast<uint32_t>(f2i(sqdist3(cur[u].x, cur[u].y, cur[u].z, qx, qy, qz)))
+                    : 0xFFFFFFFFu;
+                least = min(least, key[u]);
+            }
+            if (ballot(least < lim) != 0) {
+#pragma unroll
+                for (int u = 0; u < kListedBatch; ++u) {
+                    if (key[u] < lim) {
+                        buf[cnt * kWave + lane] = make_uint2(key[u], static_cast<uint32_t>(f2i(cur[u].w)));
+                        ++cnt;
+                    }
+                }
+                drain();
+                lim = limit();
+            }
+#pragma unroll
+            for (int u = 0; u < kListedBatch; ++u) cur[u] = nxt[u];
+        }
+    };
+    // Scan every chunk of a needed group that some lane needs: its box nearer
+    // than the lane's limit (or a non-finite query).
+    auto needed = [&](uint32_t nk) { return ballot(active && (!qfin || nk < lim)) != 0; };
+    for (int64_t i0 = 0; i0 < mine; i0 += kWave) {
+        const int64_t g = wave + NW * min<int64_t>(i0 + lane, mine - 1);
+        const float4 glo = gbox[2 * g], ghi = gbox[2 * g + 1];
+        const int nb = static_cast<int>(min<int64_t>(kWave, mine - i0));
+        for (int t = 0; t < nb; ++t) {
+            lim = limit();
+            if (!needed(near_key(glo, ghi, t))) continue;
+            const int64_t c0 = (wave + NW * (i0 + t)) * kSuperChunks;
+            const int nc = static_cast<int>(min<int64_t>(kSuperChunks, L.chunks - c0));
+            const int64_t cl = c0 + min(lane, nc - 1);
+            const float4 lo = box[2 * cl], hi = box[2 * cl + 1];
+            for (int k = 0; k < nc; ++k)
+                if (needed(near_key(lo, hi, k))) scan_chunk((c0 + k) * kChunkRefs);
+        }
+    }
+    word_merge<KMAX>(slot, buf, lane, cnt);
+
+    // Merge the waves' lists: wave 0 keeps every list's head in registers.
+#pragma unroll
+    for (int s = 0; s < KMAX; ++s)
+        if (s >= KMAX - K)
+            lds[wave][s - (KMAX - K)][lane] =
+                make_uint2(static_cast<uint32_t>(slot[s] >> 32), static_cast<uint32_t>(slot[s]));
+    __syncthreads();
+    if (wave != 0 || !active) return;
+    auto word_at = [&](int w, int s) {
+        const uint2 v = lds[w][s][lane];
+        return grid_word(v.x, v.y);
+    };
+    uint64_t head[NW];
+    int next[NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+        head[w] = word_at(w, 0);
+        next[w] = 1;
+    }
+    const int64_t row = (b * M + m) * K;
+    for (int s = 0; s < K; ++s) {
+        uint64_t best = head[0];
+        int from = 0;
+#pragma unroll
+        for (int w = 1; w < NW; ++w) {
+            const bool less = head[w] < best;
+            best = less ? head[w] : best;
+            from = less ? w : from;
+        }
+        int h = next[0];
+#pragma unroll
+        for (int w = 1; w < NW; ++w) h = from == w ? next[w] : h;
+        const uint64_t fresh = h < K ? word_at(from, h) : ~0ull;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            head[w] = from == w ? fresh : head[w];
+            next[w] = from == w ? h + 1 : next[w];
+        }
+        const float d2 = i2f(static_cast<int>(static_cast<uint32_t>(best >> 32)));
+        out_dist[row + s] = best == ~0ull ? INFINITY : sqrtf(d2);
+        out_idx[row + s] = static_cast<int64_t>(static_cast<uint32_t>(best));
+    }
+}
+
 }  // namespace
 }  // namespace pointops
 
@@ -1045,6 +1453,22 @@ void grid_build(const float* query, const float* ref, const GridLayout& L, int64
     hipLaunchKernelGGL(grid_scatter_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks);
 }
 
+// Listed-query counts and flags to zero before the search.
+void grid_list_zero(const GridLayout& L, int64_t B, hipStream_t stream) {
+    const int64_t n = B + B * L.ltiles;
+    hipLaunchKernelGGL(grid_zero_kernel, dim3(static_cast<uint32_t>((n + 255) / 256)), dim3(256), 0,
+                       stream, L.list_total, n);
+}
+
+// The list pass after the search: compaction, and the chunk boxes when the
+// linear pass prunes by them.
+void grid_list(const GridLayout& L, int64_t B, int64_t M, int64_t N, bool boxes, hipStream_t stream) {
+    const int64_t box_blocks = boxes ? (L.chunks + L.nsupers + kListWaves - 1) / kListWaves : 0;
+    hipLaunchKernelGGL(grid_list_kernel, dim3(static_cast<uint32_t>(L.ltiles + box_blocks),
+                                              static_cast<uint32_t>(B)),
+                       dim3(kGridPrepThreads), 0, stream, L, N, M);
+}
+
 // Search launch shape: 16 queries per wave, kGridSearchWaves waves per
 // workgroup, a multiple of 8 workgroups for the XCD-local deal.
 bool grid_search_grid(int64_t B, int64_t M, dim3& grid) {
@@ -1077,25 +1501,27 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     grid_build(query, ref, L, B, M, N, static_cast<int>(K), 0.f, stream);
-    // The build's scan totals and query ranks are dead once the queries are
-    // placed: they hold the per-cloud counts and lists of listed queries.
-    int* miss_count = L.tile_sum;  // B * 2 * tiles >= B ints
-    int* miss_list = L.q_rank;     // B * M ints
-    hipLaunchKernelGGL(grid_zero_kernel, dim3(static_cast<uint32_t>((B + 255) / 256)), dim3(256), 0,
-                       stream, miss_count, B);
+    grid_list_zero(L, B, stream);
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
     if (K <= 4)
-        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
+        hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else if (K <= 8)
-        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
+        hipLaunchKernelGGL((knn3_grid_kernel<2>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else if (K <= 16)
-        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
+        hipLaunchKernelGGL((knn3_grid_kernel<4>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
     else
-        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0, miss_count, miss_list);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
-    return knn3_lane_listed(query, ref, dist, idx, B, M, N, k, miss_count, miss_list, stream);
+        hipLaunchKernelGGL((knn3_grid_kernel<8>), grid, block, 0, stream, query, L, dist, idx, B, M, N, k, 0);
+    grid_list(L, B, M, N, true, stream);
+    const dim3 listed(static_cast<uint32_t>(B * ((M + kWave - 1) / kWave)));
+    const dim3 lblock(kListedWaves * kWave);
+    if (K <= 8)
+        hipLaunchKernelGGL((knn3_listed_kernel<8>), listed, lblock, 0, stream, query, L, dist, idx, M, N, k);
+    else if (K <= 16)
+        hipLaunchKernelGGL((knn3_listed_kernel<16>), listed, lblock, 0, stream, query, L, dist, idx, M, N, k);
+    else
+        hipLaunchKernelGGL((knn3_listed_kernel<32>), listed, lblock, 0, stream, query, L, dist, idx, M, N, k);
+    return hipGetLastError();
 }
 
 hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* dist2,
@@ -1111,17 +1537,13 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     grid_build(query, ref, L, B, M, N, 1, 0.f, stream);
-    // The build's scan totals and query ranks are dead once the queries are
-    // placed: they hold the per-cloud counts and lists of far queries.
-    int* miss_count = L.tile_sum;  // B * 2 * tiles >= B ints
-    int* miss_list = L.q_rank;     // B * M ints
-    hipLaunchKernelGGL(grid_zero_kernel, dim3(static_cast<uint32_t>((B + 255) / 256)), dim3(256), 0,
-                       stream, miss_count, B);
+    grid_list_zero(L, B, stream);
     hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, dim3(kGridSearchWaves * kWave), 0, stream, query,
-                       L, dist2, idx, B, M, N, 1, 1, miss_count, miss_list);
+                       L, dist2, idx, B, M, N, 1, 1);
+    grid_list(L, B, M, N, false, stream);
     const int64_t fill_blocks = B * ((M + kWave - 1) / kWave);
     hipLaunchKernelGGL(nearest_fill_kernel, dim3(static_cast<uint32_t>(fill_blocks)),
-                       dim3(kFillThreads), 0, stream, query, ref, miss_count, miss_list, dist2, idx,
+                       dim3(kFillThreads), 0, stream, query, ref, L.list_total, L.list, dist2, idx,
                        M, N);
     return hipGetLastError();
 }

@@ -228,10 +228,4 @@ hipError_t ball_query_f32_unless(const float* queries, const float* points, int6
                                  float* dist2, int64_t B, int64_t Q, int64_t P, int64_t K,
                                  float radius_sq, const int* skip, hipStream_t stream);
 
-// knn.hip: the brute-force 3-D kNN (K <= 32, results of pointops_knn3) for the
-// listed query rows only: cloud b's rows are list[b*M .. b*M + list_count[b]).
-hipError_t knn3_lane_listed(const float* query, const float* ref, float* dist, int64_t* idx,
-                            int64_t B, int64_t M, int64_t N, int K, const int* list_count,
-                            const int* list, hipStream_t stream);
-
 }  // namespace pointops

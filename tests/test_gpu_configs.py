@@ -66,6 +66,28 @@ def test_c4_knn_at_scale_rows(cuda_device):
     same_bits(host(d)[:, rows.numpy()], want_d)
 
 
+def test_c4_clustered_knn_rows(cuda_device):
+    """Config 4's sizes on clustered references queried uniformly (almost
+    every query goes to the pruned linear pass): every 64th row against the
+    oracle, and every row against the brute-force kernel of the same
+    launch sizes."""
+    import mps_pointops as mp
+    from mps_pointops import _native
+
+    ref, query = bench.make_c4_clustered()
+    qd, rd = query.cuda(), ref.cuda()
+    d, i = mp.knn(qd, rd, 16)
+    rows = torch.arange(0, query.shape[1], 64)
+    want_d, want_i = O.knn3(query[:, rows].contiguous(), ref, 16)
+    np.testing.assert_array_equal(host(i)[:, rows.numpy()], want_i)
+    same_bits(host(d)[:, rows.numpy()], want_d)
+    bd, bi = torch.empty_like(d), torch.empty_like(i)
+    _native.call("pointops_knn3", qd.data_ptr(), rd.data_ptr(), bd.data_ptr(), bi.data_ptr(),
+                 1, query.shape[1], ref.shape[1], 16, _native.stream(qd.device))
+    assert torch.equal(i, bi)
+    same_bits(host(d), host(bd))
+
+
 def test_c4_dgcnn_feature_knn_full(cuda_device):
     """DGCNN feature-space kNN: (8, 2048, 64), query is ref (self included)."""
     import mps_pointops as mp

@@ -584,6 +584,53 @@ def test_knn3_grid_listed_far_queries(cuda_device, k):
     same_bits(d, want_d)
 
 
+def _listed_case(case: str):
+    g = torch.Generator().manual_seed(sum(map(ord, case)))
+    if case == "clusters":  # 40965 references: the last chunk of 256 holds 5
+        centres = torch.rand(30, 3, generator=g) * 100
+        ref = centres.repeat_interleave(1366, 0)[:40_965] + torch.randn(40_965, 3, generator=g) * 0.1
+        query = torch.rand(5000, 3, generator=g) * 100
+        return query[None].contiguous(), ref[None].contiguous()
+    if case == "lattice_ties":  # integer points repeated: equal keys across chunks and waves
+        centres = torch.randint(0, 60, (20, 1, 3), generator=g)
+        offs = torch.stack(torch.meshgrid(*[torch.arange(-1, 2)] * 3, indexing="ij"), -1).reshape(1, 27, 3)
+        ref = (centres + offs).reshape(-1, 3).repeat(30, 1).float()
+        ref = ref[torch.randperm(ref.shape[0], generator=g)]
+        query = torch.randint(-10, 70, (3000, 3), generator=g).float()
+        return query[None].contiguous(), ref[None].contiguous()
+    # non_finite: cloud 0 holds NaN and inf references (every query listed,
+    # chunks with (-inf, +inf) boxes next to pruned ones); cloud 1 non-finite queries.
+    refs, queries = [], []
+    for b in range(2):
+        centres = torch.rand(12, 3, generator=g) * 50
+        ref = centres.repeat_interleave(1000, 0) + torch.randn(12_000, 3, generator=g) * 0.2
+        query = torch.rand(2500, 3, generator=g) * 50
+        if b == 0:
+            ref[17] = float("nan")
+            ref[5000, 2] = float("inf")
+            ref[9000, 0] = -float("inf")
+        else:
+            query[3] = float("nan")
+            query[1000, 1] = float("inf")
+        refs.append(ref)
+        queries.append(query)
+    return torch.stack(queries).contiguous(), torch.stack(refs).contiguous()
+
+
+@pytest.mark.parametrize("case", ["clusters", "lattice_ties", "non_finite"])
+@pytest.mark.parametrize("k", [1, 7, 16, 32])
+def test_knn3_grid_listed_pruned(cuda_device, case, k):
+    """Queries far from tight clusters go to the pruned linear pass (more than
+    one list tile, chunk boxes that skip whole clusters, a last chunk shorter
+    than K, equal keys at the K-th place, non-finite chunks and queries): the
+    result equals brute force bit for bit."""
+    query, ref = _listed_case(case)
+    want_d, want_i = O.knn3(query, ref, k)
+    d, i = _knn3_grid(query, ref, k)
+    np.testing.assert_array_equal(i, want_i)
+    same_bits(d, want_d)
+
+
 def test_knn3_grid_public_path(cuda_device):
     """ops.knn uses the grid search for large clouds; results match the
     brute-force kernel on the same inputs."""
