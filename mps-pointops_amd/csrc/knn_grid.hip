@@ -55,6 +55,7 @@ constexpr int64_t kListTileMin = 2048;
 constexpr int64_t kListTilesMax = 1024;
 constexpr int kChunkRefs = 256;
 constexpr int kSuperChunks = 16;
+constexpr int kCountSortMin = 4;  // equal-cell neighbour pairs that make a count wave sort
 
 struct alignas(16) GridParams {
     float lo[3];
@@ -62,7 +63,8 @@ struct alignas(16) GridParams {
     int dims[3];
     int cells;
     int nonfinite;
-    int pad[7];
+    int morton;  // query order: Morton blocks (1) or x-fastest blocks (0)
+    int pad[6];
 };
 static_assert(sizeof(GridParams) == 64, "workspace layout");
 
@@ -172,11 +174,13 @@ __device__ __forceinline__ int cell_axis(float v, float lo, float inv_h, int dim
     return static_cast<int>(fminf(fmaxf(t, 0.f), static_cast<float>(dim - 1)));
 }
 
-// Query order key: the 2 x 2 x 2 block of cells holding the point, blocks in
-// Morton order (the bits of the three block coordinates interleaved from the
-// lowest, an axis dropping out once its bits are used), scaled into
-// [0, cells) -- a monotone map, so 64 consecutive queries stay a compact group
-// for the searches and the linear pass.  Non-finite queries go to key 0.
+// Query order key: the 2 x 2 x 2 block of cells holding the point, so that
+// 64 consecutive queries form a compact group.  With P.morton the blocks go
+// in Morton order (the bits of the three block coordinates interleaved from
+// the lowest, an axis dropping out once its bits are used) scaled into
+// [0, cells) by a monotone map -- the tighter groups the kNN linear pass
+// prunes with; otherwise in x-fastest order, whose strips share the x-rows
+// of cells the ball search reads.  Non-finite queries go to key 0.
 __device__ __forceinline__ int query_key(const GridParams& P, float x, float y, float z) {
     if (!finite3(x, y, z)) return 0;
     const float v[3] = {x, y, z};
@@ -188,6 +192,10 @@ __device__ __forceinline__ int query_key(const GridParams& P, float x, float y, 
         c[a] = cell_axis(v[a], P.lo[a], P.inv_h, P.dims[a]) >> 1;
         const int nb = (P.dims[a] + 1) >> 1;
         w[a] = nb > 1 ? 32 - __clz(nb - 1) : 0;
+    }
+    if (!P.morton) {
+        const int nbx = (P.dims[0] + 1) >> 1, nby = (P.dims[1] + 1) >> 1;
+        return c[0] + nbx * (c[1] + nby * c[2]);
     }
 #pragma unroll
     for (int bit = 0; bit < 10; ++bit) {
@@ -339,7 +347,8 @@ __device__ void grid_params(const GridLayout& L, int64_t b, int64_t N, int parts
     P.inv_h = 1.f / hside;
     P.cells = dims[0] * dims[1] * dims[2];
     P.nonfinite = nonfinite;
-    for (int i = 0; i < 7; ++i) P.pad[i] = 0;
+    P.morton = 0;
+    for (int i = 0; i < 6; ++i) P.pad[i] = 0;
     *out = P;
 }
 
@@ -365,20 +374,69 @@ __global__ __launch_bounds__(kGridPrepThreads) void grid_count_kernel(const floa
                                                                       const float* __restrict__ query,
                                                                       GridLayout L, int64_t N, int64_t M,
                                                                       uint32_t ref_blocks, int parts,
-                                                                      int K, float hmin) {
+                                                                      int K, float hmin, int morton) {
     if (grid_gated_off(L)) return;  // uniform, before any barrier
     __shared__ GridParams shared_params;
     const int64_t b = blockIdx.y;
     if (threadIdx.x < kWave) grid_params(L, b, N, parts, K, hmin, &shared_params);
+    if (threadIdx.x == 0) shared_params.morton = morton;
     __syncthreads();
     const GridParams P = shared_params;
     if (blockIdx.x == 0 && threadIdx.x == 0) L.params[b] = P;
     const PrepItem it = prep_item(ref, query, N, M, ref_blocks);
-    if (it.j >= it.n) return;
-    const float* p = it.pts + 3 * (b * it.n + it.j);
-    const int c = it.queries ? query_key(P, p[0], p[1], p[2]) : cell_of(P, p[0], p[1], p[2]);
-    const int rank = atomicAdd((it.queries ? L.q_off : L.ref_off) + b * L.stride + c, 1);
-    (it.queries ? L.q_rank : L.ref_rank)[b * it.n + it.j] = rank;
+    const bool valid = it.j < it.n;
+    int c = -1;
+    if (valid) {
+        const float* p = it.pts + 3 * (b * it.n + it.j);
+        c = it.queries ? query_key(P, p[0], p[1], p[2]) : cell_of(P, p[0], p[1], p[2]);
+    }
+    // A wave whose neighbouring lanes often share a cell (at least
+    // kCountSortMin pairs: clustered or spatially ordered input) sorts its
+    // (cell, lane) pairs (bitonic network over the 64 lanes; absent points
+    // last), so that each run of equal cells takes one atomic for its length
+    // and every lane of the run its offset in it -- such points otherwise
+    // queue thousands of atomics on a few cells.  Other waves take one atomic
+    // per point.
+    const int lane = lane_id();
+    int* counts = (it.queries ? L.q_off : L.ref_off) + b * L.stride;
+    const int before = __shfl_up(c, 1);
+    if (__popcll(ballot(valid && lane > 0 && before == c)) < kCountSortMin) {
+        if (valid) (it.queries ? L.q_rank : L.ref_rank)[b * it.n + it.j] = atomicAdd(counts + c, 1);
+        return;
+    }
+    uint32_t key = valid ? static_cast<uint32_t>(c) : 0xFFFFFFFFu;
+    int from = lane;
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t ok = static_cast<uint32_t>(__shfl_xor(static_cast<int>(key), stride));
+            const int of = __shfl_xor(from, stride);
+            const bool up = (lane & size) == 0;
+            const bool low = (lane & stride) == 0;
+            // (key, from) pairs are distinct, so the order is strict.
+            const bool less = ok < key || (ok == key && of < from);
+            const bool take = low == up ? less : !less;
+            key = take ? ok : key;
+            from = take ? of : from;
+        }
+    }
+    const bool real = key != 0xFFFFFFFFu;
+    const uint32_t prev = static_cast<uint32_t>(__shfl_up(static_cast<int>(key), 1));
+    const uint64_t heads = ballot(real && (lane == 0 || prev != key));
+    const uint64_t reals = ballot(real);
+    int base = 0;
+    if (real && ((heads >> lane) & 1)) {
+        const uint64_t above = heads & ~((2ull << lane) - 1);  // heads after this one
+        const int end = above != 0 ? __builtin_ctzll(above) : __popcll(reals);
+        base = atomicAdd(counts + key, end - lane);
+    }
+    const uint64_t upto = heads & ((2ull << lane) - 1);  // 2 << 63 wraps to 0: all lanes
+    const int head = upto != 0 ? 63 - __builtin_clzll(upto) : 0;
+    const int rank = __shfl(base, head) + (lane - head);
+    // Back to the lane that holds the point.
+    const int mine = __builtin_amdgcn_ds_permute(from * 4, rank);
+    if (valid) (it.queries ? L.q_rank : L.ref_rank)[b * it.n + it.j] = mine;
 }
 
 // Sum of `v` over a workgroup of kGridPrepThreads threads (every thread gets
@@ -1432,8 +1490,8 @@ int grid_partial_count(int64_t N) {
 // `choice` (ball query only) the device-side choice runs after the bounds and
 // L.gate must point at it.
 void grid_build(const float* query, const float* ref, const GridLayout& L, int64_t B, int64_t M,
-                int64_t N, int K, float hmin, hipStream_t stream, int* choice = nullptr,
-                float radius_sq = 0.f) {
+                int64_t N, int K, float hmin, int morton, hipStream_t stream,
+                int* choice = nullptr, float radius_sq = 0.f) {
     const uint32_t nb = static_cast<uint32_t>(B);
     const uint32_t ref_blocks = static_cast<uint32_t>((N + kGridPrepThreads - 1) / kGridPrepThreads);
     const uint32_t q_blocks = static_cast<uint32_t>((M + kGridPrepThreads - 1) / kGridPrepThreads);
@@ -1447,7 +1505,7 @@ void grid_build(const float* query, const float* ref, const GridLayout& L, int64
         hipLaunchKernelGGL(ball_grid_choice_kernel, dim3(1), dim3(kGateThreads), 0, stream, L, B, N,
                            parts, K, radius_sq, choice);
     hipLaunchKernelGGL(grid_count_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks,
-                       parts, K, hmin);
+                       parts, K, hmin, morton);
     hipLaunchKernelGGL(grid_tile_sum_kernel, scan_grid, prep, 0, stream, L);
     hipLaunchKernelGGL(grid_tile_scan_kernel, scan_grid, prep, 0, stream, L);
     hipLaunchKernelGGL(grid_scatter_kernel, point_grid, prep, 0, stream, ref, query, L, N, M, ref_blocks);
@@ -1500,7 +1558,7 @@ hipError_t pointops_knn3_grid(const float* query, const float* ref, float* dist,
     if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
-    grid_build(query, ref, L, B, M, N, static_cast<int>(K), 0.f, stream);
+    grid_build(query, ref, L, B, M, N, static_cast<int>(K), 0.f, 1, stream);
     grid_list_zero(L, B, stream);
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
@@ -1536,7 +1594,7 @@ hipError_t pointops_nearest3_grid(const float* query, const float* ref, float* d
     if (!grid_search_grid(B, M, grid)) return hipErrorInvalidValue;
     GridLayout L;
     grid_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
-    grid_build(query, ref, L, B, M, N, 1, 0.f, stream);
+    grid_build(query, ref, L, B, M, N, 1, 0.f, 1, stream);
     grid_list_zero(L, B, stream);
     hipLaunchKernelGGL((knn3_grid_kernel<1>), grid, dim3(kGridSearchWaves * kWave), 0, stream, query,
                        L, dist2, idx, B, M, N, 1, 1);
@@ -1573,7 +1631,7 @@ hipError_t ball_query_grid(const float* queries, const float* points, int64_t* i
     grid_layout_bytes(B, Q, P, &L, static_cast<char*>(workspace));
     if (choose) L.gate = L.control;
     const float hmin = (radius_sq > 0.f && radius_sq < INFINITY) ? sqrtf(radius_sq) : 0.f;
-    grid_build(queries, points, L, B, Q, P, static_cast<int>(K), hmin, stream,
+    grid_build(queries, points, L, B, Q, P, static_cast<int>(K), hmin, 0, stream,
                choose ? L.control : nullptr, radius_sq);
     const dim3 block(kGridSearchWaves * kWave);
     const int k = static_cast<int>(K);
