@@ -100,7 +100,9 @@ hipError_t pointops_knn3(const float *query, const float *ref, float *dist, int6
  * into `workspace` (pointops_knn3_grid_workspace_bytes(B, M, N) bytes, no
  * initialisation needed; B <= 65535) and each query scans the box of cells
  * around it, grown face by face until no unscanned reference can be nearer
- * than its K-th neighbour.  Replaces ops.py:195-199
+ * than its K-th neighbour; queries still unfinished after a few faces are
+ * finished inside the call by a scan that skips chunks of the sorted
+ * references whose bounding box is too far.  Replaces ops.py:195-199
  * (kernels/knn.metal:32-140), like pointops_knn3. */
 size_t pointops_knn3_grid_workspace_bytes(int64_t B, int64_t M, int64_t N);
 hipError_t pointops_knn3_grid(const float *query, const float *ref, float *dist, int64_t *idx,
