@@ -391,7 +391,20 @@ def run(args) -> dict:
         balls()
         knn()
 
-    wall = timed_steps(step, args.steps, args.warmup)
+    wall_sequential = timed_steps(step, args.steps, args.warmup)
+
+    # The same batch's FPS, centre gather, ball queries and kNN in one call
+    # (mps_pointops.fps_ball_knn): the ball queries of each 256-centre chunk
+    # run as soon as FPS has sampled it, on the CUs FPS leaves free, and kNN
+    # once after the last chunk.  Same outputs,
+    # bit for bit (tests/test_gpu_pipeline.py); this is the timed step.
+    radii = [r for r, _ in C2_RADII]
+    ks = [k for _, k in C2_RADII]
+
+    def fused_step():
+        mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
+
+    wall = timed_steps(fused_step, args.steps, args.warmup)
 
     # Per-op kernel time on the launch stream (HIP events).
     reps = max(5, args.steps)
@@ -504,6 +517,15 @@ def run(args) -> dict:
         },
         "ops": {"fps": op(t_fps, fps_ops), "ball_query_x3": op(t_ball, ball_ops),
                 "knn": op(t_knn, knn_ops)},
+        "step": "mps_pointops.fps_ball_knn: FPS, centre gather, 3 ball queries and kNN of one "
+                "batch, the ball queries of each 256-centre chunk overlapped with the rest of FPS, "
+                "kNN once after the last chunk",
+        "sequential_not_in_value": {
+            "what": "the same batch as separate calls on one stream (FPS, then the ball queries "
+                    "and kNN on centres gathered beforehand, outside the timed region)",
+            "ms_per_step": wall_sequential * 1e3,
+            "points_per_s": B * N / wall_sequential,
+        },
         "propagation_not_in_value": propagation,
         "two_streams_not_in_value": {
             "what": "the same K steps software-pipelined over two default-priority streams: "

@@ -323,6 +323,34 @@ hipError_t pointops_chamfer_backward_f64(const double *query, const double *ref,
                                          int64_t Q, int64_t R, int64_t D, int32_t norm,
                                          hipStream_t stream);
 
+/* A set-abstraction front end in one call, with the queries overlapped with
+ * sampling: furthest_point_sample (ops.py:53-141; dense, 1 <= npoint <= N <=
+ * 8192, B <= 65535), the centres gathered from the samples (the caller's
+ * xyz.gather of the reference's tests/test_pointnet2_e2e.py:36-45), then for
+ * every centre `nball` first-K ball queries (ops.py:208-227; radius_sq[r] as
+ * pointops_ball_query_f32 takes it, ball_k[r] slots, no lengths) and an
+ * exact kNN of knn_k <= 32 neighbours (ops.py:144-205; Euclidean distances),
+ * each output (B, npoint, K) as the separate entry points write it, bit for
+ * bit.  FPS runs on `fps_stream` and publishes its progress every `chunk`
+ * samples; the ball queries of each chunk of centres run on `query_stream` as
+ * soon as every cloud has sampled it, and kNN once after the last chunk
+ * (`workspace` sized for all npoint centres).  The caller orders both streams after
+ * the producer of xyz and joins `query_stream` back before using the
+ * outputs.  `workspace` holds pointops_fps_query_pipeline_workspace_bytes
+ * bytes whose first 8*B bytes are zero before the first call that uses it
+ * (the library keeps them afterwards); calls sharing a workspace must not
+ * overlap.  `status` (one zeroed word) becomes non-zero if a chunk's wait
+ * gave up (then the outputs are not valid).  No counterpart in the
+ * reference, which runs these steps one after another. */
+size_t pointops_fps_query_pipeline_workspace_bytes(int64_t B, int64_t N, int64_t npoint,
+                                                   int64_t chunk);
+hipError_t pointops_fps_query_pipeline_f32(
+    const float *xyz, int64_t *samples, float *centres, int64_t nball, const float *radii_sq,
+    const int64_t *ball_k, int64_t *const *ball_idx, float *const *ball_dist2, int64_t knn_k,
+    float *knn_dist, int64_t *knn_idx, void *workspace, uint32_t *status, int64_t B, int64_t N,
+    int64_t npoint, int64_t start_idx, int32_t skip_near_origin, int64_t chunk,
+    hipStream_t fps_stream, hipStream_t query_stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -126,7 +126,7 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     const S* __restrict__ queries, const S* __restrict__ points,
     const int64_t* __restrict__ query_lengths, const int64_t* __restrict__ point_lengths,
     void* __restrict__ out_idx, float* __restrict__ out_dist, int64_t Q, int64_t P, int K,
-    float r2, const int* __restrict__ skip) {
+    float r2, const int* __restrict__ skip, int64_t QS) {
     if (skip != nullptr && *skip != 0) return;  // uniform, before any barrier
     constexpr int kTile = kBqLdsDepth * kWave;
     constexpr int kPer = kTile / (NWQ * kWave);  // points each thread stages per tile
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     const int64_t plen = point_lengths != nullptr ? point_lengths[b] : P;
     const int n = static_cast<int>(plen < P ? plen : P);
     const bool live = qi < Q && qi < qlen;
-    const int64_t row = b * Q + (qi < Q ? qi : 0);
+    const int64_t row = b * QS + (qi < Q ? qi : 0);  // QS: rows between clouds (>= Q)
     float qx = 0.f, qy = 0.f, qz = 0.f;
     if (live) {
         const S* qp = queries + 3 * row;
@@ -307,7 +307,7 @@ hipError_t launch_ball(const S* q, const S* p, const int64_t* ql, const int64_t*
         hipLaunchKernelGGL((ball_query_lds_kernel<S, NWQ, false>),
                            dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
                            dim3(NWQ * kWave), 0, stream, q, p, ql, pl, idx, dist2, Q, P,
-                           static_cast<int>(K), r2, skip);
+                           static_cast<int>(K), r2, skip, Q);
         return hipGetLastError();
     }
     if (skip != nullptr) return hipErrorInvalidValue;
@@ -345,7 +345,7 @@ hipError_t ball_query_pn2(const float* queries, const float* points, int32_t* id
     hipLaunchKernelGGL((ball_query_lds_kernel<float, NWQ, true>),
                        dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
                        dim3(NWQ * kWave), 0, stream, queries, points, nullptr, nullptr, idx, nullptr,
-                       Q, P, static_cast<int>(K), r2, nullptr);
+                       Q, P, static_cast<int>(K), r2, nullptr, Q);
     return hipGetLastError();
 }
 
@@ -354,6 +354,28 @@ hipError_t ball_query_f32_unless(const float* queries, const float* points, int6
                                  float radius_sq, const int* skip, hipStream_t stream) {
     return launch_ball<float>(queries, points, nullptr, nullptr, idx, dist2, B, Q, P, K, radius_sq,
                               skip, stream);
+}
+
+}  // namespace pointops
+
+namespace pointops {
+
+// Ball query (float32, no lengths, LDS-staged kernel) over Q query rows per
+// cloud whose rows -- queries and both outputs -- lie QS rows apart: Q
+// consecutive centres of a (B, QS, 3) tensor and of its (B, QS, K) outputs.
+hipError_t ball_query_rows_f32(const float* q, const float* p, int64_t* idx, float* dist2,
+                               int64_t B, int64_t Q, int64_t QS, int64_t P, int64_t K, float r2,
+                               hipStream_t stream) {
+    constexpr int NWQ = kBqLdsQueries;
+    const int64_t qblocks = (Q + NWQ - 1) / NWQ;
+    if (B < 1 || B > 65535 || Q < 1 || QS < Q || P < 0 || K < 1 || K > INT32_MAX ||
+        P > INT32_MAX - kBqDepth * kWave || qblocks > INT32_MAX)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((ball_query_lds_kernel<float, NWQ, false>),
+                       dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
+                       dim3(NWQ * kWave), 0, stream, q, p, nullptr, nullptr, idx, dist2, Q, P,
+                       static_cast<int>(K), r2, nullptr, QS);
+    return hipGetLastError();
 }
 
 }  // namespace pointops

@@ -137,7 +137,8 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
                                                       const int64_t* __restrict__ out_ptr,
                                                       const int64_t* __restrict__ starts,
                                                       int64_t* __restrict__ out, int64_t N,
-                                                      int64_t npoint, int64_t start, int skip) {
+                                                      int64_t npoint, int64_t start, int skip,
+    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk) {
     constexpr int NW = T / kWave;
     constexpr int KC = kWave / NW;  // candidates per wave
     constexpr int CAP = P * T;      // points per cloud at most
@@ -172,7 +173,25 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     const int lane = tid % kWave;
     const int far0 = static_cast<int>(seg.start);
     if (tid == 0) o[0] = seg.base + far0;
-    if (seg.cnt == 1 || n <= 0) return;
+    // With `progress` set, wave 0 publishes, once the samples [0, done) are
+    // stored, tag + the number of whole `chunk`s among them (all of them once
+    // done == seg.cnt) in word blockIdx.x: an agent-scope release fence over
+    // the wave's stores, then one lane's store, so that a workgroup on any
+    // XCD that reads the word with acquire ordering sees those samples.
+    auto publish = [&](int64_t before, int64_t done) {
+        if (progress == nullptr || wave != 0) return;
+        const int64_t whole = (seg.cnt + chunk - 1) / chunk;
+        const int64_t now = done >= seg.cnt ? whole : done / chunk;
+        if (before >= 0 && now == (before >= seg.cnt ? whole : before / chunk)) return;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        if (lane == 0)
+            __hip_atomic_store(progress + blockIdx.x, tag + static_cast<uint64_t>(now),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (seg.cnt == 1 || n <= 0) {
+        publish(-1, seg.cnt);
+        return;
+    }
 
     // ---- setup: bounding box, cells, counting sort
     for (int c = tid; c < kCells; c += T) cell_count[c] = 0;
@@ -477,6 +496,7 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
         if (pend) apply_pending();
         if (wave == 0 && when >= 0) o[step + when] = seg.base + cidx;
         step += taken;
+        publish(step - taken, step);
     }
 }
 
@@ -1123,10 +1143,12 @@ constexpr int kTilesFirstHalf = P == 8 ? 9 : P;
 template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
-                       int64_t npoint, int64_t start, int skip, hipStream_t stream) {
+                       int64_t npoint, int64_t start, int skip, hipStream_t stream,
+                       uint64_t* progress = nullptr, uint64_t tag = 0, int64_t chunk = 1,
+                       size_t reserve = 0) {
     hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>), dim3(static_cast<uint32_t>(blocks)),
-                       dim3(kRegsThreads), 0, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                       start, skip);
+                       dim3(kRegsThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                       start, skip, progress, tag, chunk);
     return hipGetLastError();
 }
 
@@ -1249,6 +1271,59 @@ int large_capacity(int device) {
 }
 
 }  // namespace
+}  // namespace pointops
+
+namespace pointops {
+
+// Dense FPS of B clouds of N <= 8192 points (the tiled kernel) that publishes
+// per-cloud progress words: progress[b] = tag + the whole `chunk`s of samples
+// of cloud b stored so far (all ceil(npoint / chunk) of them at the end).
+// Dynamic LDS that, added to fps_tiled_kernel<P>'s own, takes all of a CU's
+// LDS: no workgroup that uses LDS (every kernel queued beside a pipelined
+// FPS does) can then share a CU with an FPS workgroup and take issue slots
+// from its latency-bound steps.  0 if the attributes cannot be read.
+template <int P>
+size_t fps_reserve_lds() {
+    static const size_t bytes = [] {
+        hipFuncAttributes a{};
+        int dev = 0, per_block = 0, per_cu = 0;
+        const void* k = reinterpret_cast<const void*>(&fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>);
+        if (hipFuncGetAttributes(&a, k) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
+            hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
+            return size_t(0);
+        const size_t cap = static_cast<size_t>(per_block < per_cu ? per_block : per_cu);
+        const size_t mine = a.sharedSizeBytes;
+        if (cap <= mine) return size_t(0);
+        if (hipFuncSetAttribute(k, hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(cap - mine)) != hipSuccess)
+            return size_t(0);
+        return cap - mine;
+    }();
+    return bytes;
+}
+
+hipError_t fps_dense_progress(const float* xyz, int64_t* out, int64_t B, int64_t N,
+                              int64_t npoint, int64_t start, int skip, uint64_t* progress,
+                              uint64_t tag, int64_t chunk, hipStream_t stream) {
+    if (B < 1 || B > INT32_MAX || N < 1 || N > kRegsMaxPoints || npoint < 1 || npoint > N ||
+        start < 0 || start >= N || chunk < 1 || progress == nullptr)
+        return hipErrorInvalidValue;
+    if (N <= 1 * kRegsThreads)
+        return launch_regs<1>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
+                               fps_reserve_lds<1>());
+    if (N <= 2 * kRegsThreads)
+        return launch_regs<2>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
+                               fps_reserve_lds<2>());
+    if (N <= 4 * kRegsThreads)
+        return launch_regs<4>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
+                               fps_reserve_lds<4>());
+    if (N <= 8 * kRegsThreads)
+        return launch_regs<8>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
+                               fps_reserve_lds<8>());
+    return launch_regs<16>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
+                               fps_reserve_lds<16>());
+}
+
 }  // namespace pointops
 
 using namespace pointops;

@@ -410,7 +410,8 @@ __device__ __forceinline__ uint32_t window_cell(float x, float y, float z, const
 }
 
 __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
-    const float* __restrict__ query, const float* __restrict__ ref, WindowLayout L, int M, int N) {
+    const float* __restrict__ query, const float* __restrict__ ref, WindowLayout L, int M, int N,
+    int64_t QS) {
     constexpr int RPT = kWindowMaxRefs / kWindowPrepThreads;
     constexpr int QPT = kWindowMaxQueries / kWindowPrepThreads;
     constexpr int CPT = kWindowCells / kWindowPrepThreads;  // cells per thread in the scan
@@ -422,7 +423,7 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     const int lane = tid % kWave, wave = tid / kWave;
     const int64_t b = blockIdx.x;
     const float* rp = ref + 3 * b * N;
-    const float* qp = query + 3 * b * M;
+    const float* qp = query + 3 * b * QS;  // QS: query rows between clouds
 
     for (int c = tid; c <= kWindowCells; c += kWindowPrepThreads) cell_off[c] = 0;
     // References and queries are requested together, without branches (an
@@ -537,7 +538,7 @@ template <int KMAX, int NW, int CAP>
 __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
     int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K, const float4* __restrict__ sorted,
-    const int* __restrict__ home) {
+    const int* __restrict__ home, int64_t QS) {
     // Per wave: the candidate buffer during the scan, then the final list.
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
     __shared__ uint32_t window_max[kWave];  // per lane: the Morton-window limit
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const int64_t b = cb.b;
     const int64_t m = static_cast<int64_t>(cb.x) * kWave + lane;
     const bool active = m < M;
-    const float* qp = query + 3 * (b * M + (active ? m : 0));
+    const float* qp = query + 3 * (b * QS + (active ? m : 0));  // QS: rows between clouds
     const float qx = qp[0], qy = qp[1], qz = qp[2];
     const float* rp = ref + 3 * b * N;
     uint2* buf = &lds[wave][0][0];
@@ -704,7 +705,7 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     }
     lane_merge<KMAX>(lk, li, tau, K, buf, lane, cnt);
 
-    lane_publish_and_merge<KMAX, NW, CAP>(lds, lk, li, K, wave, lane, active, (b * M + m) * K, out_dist,
+    lane_publish_and_merge<KMAX, NW, CAP>(lds, lk, li, K, wave, lane, active, (b * QS + m) * K, out_dist,
                                  out_idx, static_cast<int64_t>(0xFFFFFFFFu));
 }
 
@@ -847,7 +848,7 @@ hipError_t launch_feat_lane(const float* query, const float* ref, float* dist, i
 template <int KMAX>
 hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_t* idx, int64_t B,
                        int64_t M, int64_t N, int K, hipStream_t stream,
-                       const WindowLayout* window = nullptr) {
+                       const WindowLayout* window = nullptr, int64_t QS = 0) {
     const dim3 grid(static_cast<uint32_t>((M + kWave - 1) / kWave * B));  // cloud_block order
     // Small lists: 8 waves per 64 queries (more waves in flight, 16-entry
     // buffers); K up to 32: 4 waves with 32-entry buffers.
@@ -855,7 +856,7 @@ hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_
     constexpr int CAP = KMAX <= 16 ? 16 : 32;
     hipLaunchKernelGGL((knn3_lane_kernel<KMAX, NW, CAP>), grid, dim3(NW * kWave), 0, stream, query,
                        ref, dist, idx, M, N, K, window ? window->sorted : nullptr,
-                       window ? window->home : nullptr);
+                       window ? window->home : nullptr, QS > 0 ? QS : M);
     return hipGetLastError();
 }
 
@@ -913,6 +914,34 @@ bool grid_ok(int64_t rows) { return (rows + kKnnWaves - 1) / kKnnWaves <= INT32_
 
 }  // namespace pointops
 
+namespace pointops {
+
+// The windowed kNN (D = 3, K <= 32) over M query rows per cloud whose rows --
+// queries and both outputs -- lie QS rows apart (M consecutive centres of a
+// (B, QS, 3) tensor and of its (B, QS, K) outputs).  `workspace` holds
+// pointops_knn3_windowed_workspace_bytes(B, M, N) bytes.
+hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist, int64_t* idx,
+                              void* workspace, int64_t B, int64_t M, int64_t QS, int64_t N,
+                              int64_t K, hipStream_t stream) {
+    if (B < 1 || B > INT32_MAX || M < 1 || QS < M || K < 1 || K > 32 || K > N ||
+        N > kWindowMaxRefs || M > kWindowMaxQueries || workspace == nullptr ||
+        (M + kWave - 1) / kWave * B > INT32_MAX)
+        return hipErrorInvalidValue;
+    WindowLayout L;
+    window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
+    hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
+                       dim3(kWindowPrepThreads), 0, stream, query, ref, L, static_cast<int>(M),
+                       static_cast<int>(N), QS);
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+    const int k = static_cast<int>(K);
+    if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, k, stream, &L, QS);
+    if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, k, stream, &L, QS);
+    return launch_lane<32>(query, ref, dist, idx, B, M, N, k, stream, &L, QS);
+}
+
+}  // namespace pointops
+
 using namespace pointops;
 
 extern "C" {
@@ -942,7 +971,7 @@ hipError_t pointops_knn3_windowed(const float* query, const float* ref, float* d
     window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
     hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
                        dim3(kWindowPrepThreads), 0, stream, query, ref, L, static_cast<int>(M),
-                       static_cast<int>(N));
+                       static_cast<int>(N), M);
     const hipError_t err = hipGetLastError();
     if (err != hipSuccess) return err;
     const int k = static_cast<int>(K);

@@ -58,9 +58,12 @@ _SIGNATURES: dict[str, list] = {
     "pointops_chamfer_nearest_f64": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "pointops_chamfer_backward_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
     "pointops_chamfer_backward_f64": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i32, _vp],
+    "pointops_fps_query_pipeline_f32": [_vp, _vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _vp, _vp,
+                                        _vp, _vp, _i64, _i64, _i64, _i64, _i32, _i64, _vp, _vp],
 }
 _SIZE_QUERIES: dict[str, list] = {
     "pointops_fps_dense_scratch_bytes": [_i64, _i64],
+    "pointops_fps_query_pipeline_workspace_bytes": [_i64, _i64, _i64, _i64],
     "pointops_fps_large_workspace_bytes": [_i64, _i64],
     "pointops_fps_flat_scratch_bytes": [_i64, _i64],
     "pointops_knn3_grid_workspace_bytes": [_i64, _i64, _i64],
