@@ -402,9 +402,20 @@ def run(args) -> dict:
     ks = [k for _, k in C2_RADII]
 
     def fused_step():
-        mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
+        state["fused"] = mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
 
     wall = timed_steps(fused_step, args.steps, args.warmup)
+    # The last timed call's outputs against the separate calls, bit for bit
+    # (outside the timed region): a chunk whose wait gave up would show here.
+    samples, fused_centres, fused_balls, fused_knn = state["fused"]
+    same = torch.equal(samples, state["idx"]) and torch.equal(fused_centres, centres)
+    for (radius, k), (d, i) in zip(C2_RADII, fused_balls):
+        rd, ri = mp.ball_query(centres, xyz, radius, k)
+        same = same and torch.equal(i, ri) and torch.equal(d, rd)
+    kd, ki = mp.knn(centres, xyz, C2_KNN_K)
+    same = same and torch.equal(fused_knn[1], ki) and torch.equal(fused_knn[0], kd)
+    if not same:
+        raise SystemExit("bench: fps_ball_knn's last timed call differs from the separate calls")
 
     # Per-op kernel time on the launch stream (HIP events).
     reps = max(5, args.steps)
@@ -525,6 +536,12 @@ def run(args) -> dict:
                     "and kNN on centres gathered beforehand, outside the timed region)",
             "ms_per_step": wall_sequential * 1e3,
             "points_per_s": B * N / wall_sequential,
+        },
+        "sum_of_ops_not_in_value": {
+            "what": "B*N / (t_FPS + sum of the 3 ball-query times + t_kNN), each the kernel time "
+                    "of its separate call (HIP events on the launch stream)",
+            "ms": (t_fps + t_ball + t_knn) * 1e3,
+            "points_per_s": B * N / (t_fps + t_ball + t_knn),
         },
         "propagation_not_in_value": propagation,
         "two_streams_not_in_value": {

@@ -334,13 +334,21 @@ hipError_t pointops_chamfer_backward_f64(const double *query, const double *ref,
  * bit.  FPS runs on `fps_stream` and publishes its progress every `chunk`
  * samples; the ball queries of each chunk of centres run on `query_stream` as
  * soon as every cloud has sampled it, and kNN once after the last chunk
- * (`workspace` sized for all npoint centres).  The caller orders both streams after
- * the producer of xyz and joins `query_stream` back before using the
- * outputs.  `workspace` holds pointops_fps_query_pipeline_workspace_bytes
- * bytes whose first 8*B bytes are zero before the first call that uses it
- * (the library keeps them afterwards); calls sharing a workspace must not
- * overlap.  `status` (one zeroed word) becomes non-zero if a chunk's wait
- * gave up (then the outputs are not valid).  No counterpart in the
+ * (`workspace` sized for all npoint centres).  The caller orders fps_stream
+ * after the producer of xyz; the call orders query_stream after its own
+ * clear of the workspace's progress words and of `status` (a kernel on
+ * fps_stream, then an event), and fps_stream after its last query (an
+ * event), so work queued on fps_stream afterwards sees every output.  Two
+ * events per host thread and device are created on first use and kept.
+ * `workspace` (pointops_fps_query_pipeline_workspace_bytes bytes, no
+ * initialisation needed) and `status` (one word) belong to one call until
+ * fps_stream has passed it: calls that overlap need distinct ones.  The
+ * gates read the progress words at most 2^24 times per thread (or
+ * POINTOPS_PIPELINE_SPIN_LIMIT times, read per call; 0 makes them give up at
+ * once).  A gate that gives up sets `status` non-zero and writes NaN centres
+ * for its chunk and every later chunk, whose queries then return the
+ * results for a NaN query (ball query (0, -1), kNN (inf, 2^32 - 1)); the
+ * samples stay exact.  No counterpart in the
  * reference, which runs these steps one after another. */
 size_t pointops_fps_query_pipeline_workspace_bytes(int64_t B, int64_t N, int64_t npoint,
                                                    int64_t chunk);

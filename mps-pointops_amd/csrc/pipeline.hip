@@ -19,10 +19,19 @@
 // The only waiting is the gate's bounded poll of the progress words; FPS
 // waits on nothing, and its workgroups are resident before any chunk can be
 // published, so the query kernels queued behind a gate cannot keep FPS from
-// running.  A gate that gives up (kGateSpinLimit polls) sets *status and
-// lets its chunk run on whatever the samples hold (indices clamped in
-// bounds), so every launch ends.
-#include <atomic>
+// running.
+//
+// Every call owns its progress words and status word: a clear kernel on
+// `fps_stream` zeroes them, and `query_stream` waits (through an event) for
+// that clear before its first gate, so a gate can only be satisfied by its
+// own call's FPS.  Overlapping calls (on other streams, or queued back to
+// back) need distinct workspaces; the Python wrapper allocates one per call.
+// A gate that gives up (its poll budget spent, or an earlier gate of the call
+// gave up) sets *status and writes NaN centres for its chunk, so the chunk's
+// queries run on NaN centres: ball-query rows (0, -1) and kNN rows
+// (inf, 2^32 - 1), the reference's results for a NaN query.  Every launch
+// ends.
+#include <cstdlib>
 
 #include "pointops_common.hpp"
 #include "pointops_hip.h"
@@ -42,50 +51,115 @@ hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist,
 namespace {
 
 constexpr int kGateThreads = 256;
-// Polls of one progress word before a gate gives up, each after a sleep of
-// about 0.5 us: several seconds, against a few milliseconds for the longest
-// FPS this path takes (8192 points).
+// Reads of the progress words per gate thread (over all of its clouds)
+// before the gate gives up, each after a sleep of about 0.5 us: several
+// seconds, against well under a second for the longest FPS this path takes
+// (65535 clouds of 8192 points).
 constexpr uint32_t kGateSpinLimit = 1u << 24;
-// Tags advance by 2^20 per call, above any chunk count (at most 8192).
-constexpr int kTagShift = 20;
 constexpr size_t kAlign = 256;
-
-std::atomic<uint64_t> g_epoch{0};
+constexpr int kMaxDevices = 64;
 
 size_t align_up(size_t x) { return (x + kAlign - 1) / kAlign * kAlign; }
 
+// kGateSpinLimit, or POINTOPS_PIPELINE_SPIN_LIMIT when set, read per call
+// (0 makes every gate give up without reading a progress word: the host's
+// way to exercise the give-up path while every kernel still ends).
+uint32_t gate_spin_limit() {
+    const char* env = std::getenv("POINTOPS_PIPELINE_SPIN_LIMIT");
+    if (env == nullptr || *env == '\0') return kGateSpinLimit;
+    return static_cast<uint32_t>(std::strtoul(env, nullptr, 10));
+}
+
+// Two events per host thread and device: `cleared` orders the query stream
+// after the clear of the call's words, `done` orders the FPS stream after
+// the call's last query.  An event may be recorded again once the waits on
+// its previous record are enqueued, which happens before this call returns,
+// so one pair per thread suffices.  They are never destroyed (no exit-time
+// HIP calls).
+struct CallEvents {
+    hipEvent_t cleared = nullptr;
+    hipEvent_t done = nullptr;
+};
+thread_local CallEvents tl_events[kMaxDevices];
+
+hipError_t call_events(hipStream_t stream, CallEvents** out) {
+    int device = 0;
+    hipError_t err = hipGetDevice(&device);
+    if (err != hipSuccess) return err;
+    int stream_device = device;
+    err = hipStreamGetDevice(stream, &stream_device);
+    if (err != hipSuccess) return err;
+    if (stream_device != device || device < 0 || device >= kMaxDevices)
+        return hipErrorInvalidDevice;
+    CallEvents& ev = tl_events[device];
+    if (ev.cleared == nullptr) {
+        err = hipEventCreateWithFlags(&ev.cleared, hipEventDisableTiming);
+        if (err != hipSuccess) return err;
+    }
+    if (ev.done == nullptr) {
+        err = hipEventCreateWithFlags(&ev.done, hipEventDisableTiming);
+        if (err != hipSuccess) return err;
+    }
+    *out = &ev;
+    return hipSuccess;
+}
+
+// Zeroes the B progress words and the status word of one call.
+__global__ __launch_bounds__(kGateThreads) void pipeline_clear_kernel(
+    uint64_t* __restrict__ progress, uint32_t* __restrict__ status, int64_t B) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kGateThreads + threadIdx.x;
+    if (i < B) progress[i] = 0;
+    if (i == 0) status[0] = 0;
+}
+
 // Waits until progress[b] >= target for every cloud b, then writes the
 // centres of samples [m0, m1) of every cloud: centres[b, m] = xyz[b, samples[b, m]].
+// A thread reads the words at most `spin_limit` times in all; once any
+// thread gives up (or an earlier gate has: *status set), every thread stops
+// waiting and the chunk's centres are NaN.
 __global__ __launch_bounds__(kGateThreads) void pipeline_gate_kernel(
     const uint64_t* __restrict__ progress, uint64_t target, const float* __restrict__ xyz,
     const int64_t* samples, float* __restrict__ centres, uint32_t* __restrict__ status,
-    int64_t B, int64_t N, int64_t npoint, int64_t m0, int64_t m1) {
+    int64_t B, int64_t N, int64_t npoint, int64_t m0, int64_t m1, uint32_t spin_limit) {
     __shared__ int gave_up;
-    if (threadIdx.x == 0) gave_up = 0;
+    if (threadIdx.x == 0)
+        gave_up = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
     __syncthreads();
+    volatile int* const flag = &gave_up;
+    uint32_t polls = 0;
     for (int64_t b = threadIdx.x; b < B; b += kGateThreads) {
-        uint32_t polls = 0;
-        while (__hip_atomic_load(progress + b, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) < target) {
-            if (++polls > kGateSpinLimit) {
-                gave_up = 1;
+        for (;;) {
+            if (*flag) break;
+            if (polls >= spin_limit) {
+                *flag = 1;
                 break;
             }
+            ++polls;
+            if (__hip_atomic_load(progress + b, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= target)
+                break;
             __builtin_amdgcn_s_sleep(16);
         }
+        if (*flag) break;
     }
     __syncthreads();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    if (gave_up && threadIdx.x == 0) status[0] = 1u;
+    const bool poisoned = gave_up != 0;
+    if (poisoned && threadIdx.x == 0)
+        __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     const int64_t mc = m1 - m0;
     for (int64_t i = threadIdx.x; i < B * mc; i += kGateThreads) {
         const int64_t b = i / mc, m = m0 + i % mc;
+        float* dst = centres + (b * npoint + m) * 3;
+        if (poisoned) {
+            dst[0] = dst[1] = dst[2] = __builtin_nanf("");
+            continue;
+        }
         // Samples are read with agent-scope atomic loads: they were stored by
         // workgroups still running on other XCDs.
         int64_t j = __hip_atomic_load(samples + b * npoint + m, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
         j = j < 0 ? 0 : (j >= N ? N - 1 : j);
         const float* src = xyz + (b * N + j) * 3;
-        float* dst = centres + (b * npoint + m) * 3;
         dst[0] = src[0];
         dst[1] = src[1];
         dst[2] = src[2];
@@ -123,24 +197,29 @@ hipError_t pointops_fps_query_pipeline_f32(
         if (ball_k[r] < 1 || ball_idx[r] == nullptr || ball_dist2[r] == nullptr)
             return hipErrorInvalidValue;
     const int64_t chunks = (npoint + chunk - 1) / chunk;
-    if (chunks >= (int64_t(1) << kTagShift)) return hipErrorInvalidValue;
     uint64_t* progress = static_cast<uint64_t*>(workspace);
     char* knn_ws = static_cast<char*>(workspace) + align_up(static_cast<size_t>(B) * sizeof(uint64_t));
-    // Progress words hold an earlier call's tag (smaller) or zero: every
-    // target of this call lies above them.
-    const uint64_t tag = (g_epoch.fetch_add(1) + 1) << kTagShift;
-    hipError_t err = fps_dense_progress(xyz, samples, B, N, npoint, start_idx,
-                                        skip_near_origin != 0, progress, tag, chunk, fps_stream);
+    CallEvents* ev = nullptr;
+    hipError_t err = call_events(fps_stream, &ev);
+    if (err != hipSuccess) return err;
+    const uint32_t limit = gate_spin_limit();
+    // This call's words start at zero, after everything already on fps_stream.
+    hipLaunchKernelGGL(pipeline_clear_kernel, dim3(static_cast<uint32_t>((B + kGateThreads - 1) / kGateThreads)),
+                       dim3(kGateThreads), 0, fps_stream, progress, status, B);
+    if ((err = hipGetLastError()) != hipSuccess) return err;
+    if ((err = hipEventRecord(ev->cleared, fps_stream)) != hipSuccess) return err;
+    if ((err = hipStreamWaitEvent(query_stream, ev->cleared, 0)) != hipSuccess) return err;
+    err = fps_dense_progress(xyz, samples, B, N, npoint, start_idx, skip_near_origin != 0,
+                             progress, 0, chunk, fps_stream);
     if (err != hipSuccess) return err;
     for (int64_t c = 0; c < chunks; ++c) {
         const int64_t m0 = c * chunk;
         const int64_t m1 = m0 + chunk < npoint ? m0 + chunk : npoint;
         const int64_t mc = m1 - m0;
         hipLaunchKernelGGL(pipeline_gate_kernel, dim3(1), dim3(kGateThreads), 0, query_stream,
-                           progress, tag + static_cast<uint64_t>(c + 1), xyz, samples, centres,
-                           status, B, N, npoint, m0, m1);
-        err = hipGetLastError();
-        if (err != hipSuccess) return err;
+                           progress, static_cast<uint64_t>(c + 1), xyz, samples, centres,
+                           status, B, N, npoint, m0, m1, limit);
+        if ((err = hipGetLastError()) != hipSuccess) return err;
         for (int64_t r = 0; r < nball; ++r) {
             err = ball_query_rows_f32(centres + 3 * m0, xyz, ball_idx[r] + m0 * ball_k[r],
                                       ball_dist2[r] + m0 * ball_k[r], B, mc, npoint, N, ball_k[r],
@@ -148,10 +227,14 @@ hipError_t pointops_fps_query_pipeline_f32(
             if (err != hipSuccess) return err;
         }
     }
-    if (knn_k > 0)  // after the last gate: every centre is in place
-        return knn3_windowed_rows(centres, xyz, knn_dist, knn_idx, knn_ws, B, npoint, npoint, N,
-                                  knn_k, query_stream);
-    return hipSuccess;
+    if (knn_k > 0) {  // after the last gate: every centre is in place
+        err = knn3_windowed_rows(centres, xyz, knn_dist, knn_idx, knn_ws, B, npoint, npoint, N,
+                                 knn_k, query_stream);
+        if (err != hipSuccess) return err;
+    }
+    // Work queued on fps_stream after this call sees every output.
+    if ((err = hipEventRecord(ev->done, query_stream)) != hipSuccess) return err;
+    return hipStreamWaitEvent(fps_stream, ev->done, 0);
 }
 
 }  // extern "C"

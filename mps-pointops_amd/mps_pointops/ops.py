@@ -17,9 +17,9 @@ from torch import Tensor
 from . import _native
 from ._ball_query import _checked_radius_and_k, ball_query as _native_ball_query
 
-# Largest cloud the single-launch large-cloud FPS path addresses (21-bit index
-# in its per-step records).
-# The persistent kernel's index range (ops.py:108-109): fewer than 2**32 points.
+# Largest cloud the large-cloud FPS path takes, the reference's index range
+# (ops.py:108-109): fewer than 2**32 points (clouds above 2**21 points use the
+# streaming persistent kernel).
 _FPS_LARGE_MAX_N = (1 << 32) - 1
 # One cloud with at least this many points uses the all-CU persistent kernel
 # under strategy="auto"; smaller clouds fit one workgroup's registers and LDS.
@@ -196,13 +196,10 @@ def ball_query(query: Tensor, ref: Tensor, radius: float, K: int) -> tuple[Tenso
     return result.distances, result.indices
 
 
-# Streams beside torch's current stream for fps_ball_knn, one per device
-# (default priority).
-_SIDE_STREAMS: dict[int, torch.cuda.Stream] = {}
-# Workspaces of fps_ball_knn: their first 8*B bytes (progress words) are
-# zeroed once and then kept by the library, so they are reused per device and
-# shape.  Calls on one device from several host threads must not overlap.
-_PIPELINE_WORKSPACES: dict[tuple, Tensor] = {}
+# Streams beside the caller's stream for fps_ball_knn, one per (device,
+# caller stream), default priority: calls issued from different streams keep
+# independent query queues.
+_SIDE_STREAMS: dict[tuple[int, int], torch.cuda.Stream] = {}
 _PIPELINE_MAX_N = 8192
 
 
@@ -227,13 +224,21 @@ def fps_ball_knn(
 
     The ball queries of each ``chunk`` of centres start as soon as FPS has
     sampled it in every cloud, on the CUs FPS leaves free (FPS uses one per
-    cloud), and kNN runs once after the last chunk, on a side stream joined
-    back to the current one before returning (256: 0.560 ms at B=32, N=4096,
-    npoint 1024, three radii and kNN16, against 0.600 ms for the separate
-    calls; 128: 0.590, 512: 0.606).
-    ``check=True`` reads the status word (one host synchronisation) and
-    raises if a chunk's wait gave up.  float32 (B, N, 3) clouds with
-    ``1 <= npoint <= N <= 8192``, ``knn_k <= 32``, at most 8 radii.
+    cloud), and kNN runs once after the last chunk, on a side stream that
+    the library joins back to the current one before returning (256:
+    0.560 ms at B=32, N=4096, npoint 1024, three radii and kNN16, against
+    0.600 ms for the separate calls; 128: 0.590, 512: 0.606).  Each call has
+    its own workspace, so calls may overlap (queued back to back, or issued
+    from several streams or host threads).
+
+    A chunk whose wait for its samples gives up (a bounded poll, several
+    seconds; ``POINTOPS_PIPELINE_SPIN_LIMIT`` sets the number of polls) and
+    every later chunk of the call get NaN centres, so their ball-query rows
+    are (0, -1) and their kNN rows (inf, 2**32 - 1); ``samples`` stay
+    exact.  ``check=True`` reads the call's status word (one host
+    synchronisation) and raises RuntimeError in that case.  float32
+    (B, N, 3) clouds with ``1 <= npoint <= N <= 8192``, ``knn_k <= 32``, at
+    most 8 radii.
 
     Returns ``(samples, centres, [(ball_dists, ball_idx) per radius],
     (knn_dists, knn_idx))``.
@@ -263,30 +268,31 @@ def fps_ball_knn(
               torch.empty(B, npoint, k, dtype=torch.long, device=dev)) for k in nsamples]
     knn_out = (torch.empty(B, npoint, knn_k, dtype=torch.float32, device=dev),
                torch.empty(B, npoint, knn_k, dtype=torch.long, device=dev))
-    key = (device, B, N, npoint, chunk)
-    workspace = _PIPELINE_WORKSPACES.get(key)
-    if workspace is None:
-        size = _native.size_query("pointops_fps_query_pipeline_workspace_bytes", B, N, npoint, chunk)
-        workspace = torch.zeros(size + 4, dtype=torch.uint8, device=dev)  # + the status word
-        _PIPELINE_WORKSPACES[key] = workspace
+    size = _native.size_query("pointops_fps_query_pipeline_workspace_bytes", B, N, npoint, chunk)
+    # The call's progress words, kNN workspace and (last 4 bytes) status
+    # word; the library clears what must start at zero on the current stream.
+    workspace = torch.empty(size + 4, dtype=torch.uint8, device=dev)
     status = workspace[-4:]
     current = torch.cuda.current_stream(dev)
-    side = _SIDE_STREAMS.get(device)
+    side = _SIDE_STREAMS.get((device, current.cuda_stream))
     if side is None:
-        side = _SIDE_STREAMS[device] = torch.cuda.Stream(dev)
-    side.wait_stream(current)
+        side = torch.cuda.Stream(dev)
+        if side.cuda_stream == current.cuda_stream:  # the pool handed back the caller's stream
+            side = torch.cuda.Stream(dev)
+        _SIDE_STREAMS[(device, current.cuda_stream)] = side
     n = len(radii)
     c_radii = (ctypes.c_float * max(n, 1))(*radii_sq)
     c_ks = (ctypes.c_int64 * max(n, 1))(*nsamples)
     c_idx = (ctypes.c_void_p * max(n, 1))(*[i.data_ptr() for _, i in balls])
     c_d2 = (ctypes.c_void_p * max(n, 1))(*[d.data_ptr() for d, _ in balls])
-    _native.call("pointops_fps_query_pipeline_f32", xyz.data_ptr(), samples.data_ptr(),
-                 centres.data_ptr(), n, c_radii, c_ks, c_idx, c_d2, knn_k,
-                 knn_out[0].data_ptr(), knn_out[1].data_ptr(), workspace.data_ptr(),
-                 status.data_ptr(), B, N, npoint, start_idx, int(skip_near_origin), chunk,
-                 current.cuda_stream, side.cuda_stream)
-    current.wait_stream(side)
+    with torch.cuda.device(dev):
+        _native.call("pointops_fps_query_pipeline_f32", xyz.data_ptr(), samples.data_ptr(),
+                     centres.data_ptr(), n, c_radii, c_ks, c_idx, c_d2, knn_k,
+                     knn_out[0].data_ptr(), knn_out[1].data_ptr(), workspace.data_ptr(),
+                     status.data_ptr(), B, N, npoint, start_idx, int(skip_near_origin), chunk,
+                     current.cuda_stream, side.cuda_stream)
+    # The library has joined the side stream back to `current`, so every
+    # tensor above (allocated on `current`) is safe to free or reuse there.
     if check and int(status.view(torch.int32).item()) != 0:
-        status.zero_()
         raise RuntimeError("fps_ball_knn: a chunk's wait for its samples gave up")
     return samples, centres, balls, knn_out
