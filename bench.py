@@ -492,6 +492,24 @@ def run(args) -> dict:
     t_gfb = timer.time(group_fwd_bwd, reps)
     t_gl = timer.time(group_layer, reps)
     group_bytes = 4 * (B * 67 * C2_NPOINT * 32 + B * C2_NPOINT * 32 + B * 64 * N + B * N * 3)
+    # Ball query with gradients (r=0.4, K=128, the largest of the three): the
+    # forward alone and forward + backward (both coordinate gradients).
+    bq_q = centres.clone().requires_grad_()
+    bq_p = xyz.clone().requires_grad_()
+    bq_g = torch.randn(B, C2_NPOINT, 128, generator=g).to(device)
+
+    def ball_fwd():
+        return mp.ball_query(bq_q, bq_p, 0.4, 128)
+
+    def ball_fwd_bwd():
+        bq_q.grad = None
+        bq_p.grad = None
+        mp.ball_query(bq_q, bq_p, 0.4, 128)[0].backward(bq_g)
+
+    ball_fwd_bwd()
+    torch.cuda.synchronize()
+    t_bf = timer.time(ball_fwd, reps)
+    t_bfb = timer.time(ball_fwd_bwd, reps)
     propagation = {
         "three_nn": {"ms": t_tn * 1e3, "tops": PAIR_OPS * B * N * C2_NPOINT / t_tn / 1e12},
         "three_interpolate": {"ms": t_ti * 1e3, "gbps": interp_bytes / t_ti / 1e9},
@@ -499,6 +517,8 @@ def run(args) -> dict:
         "query_and_group_C64_S32": {"ms": t_gf * 1e3, "gbps": group_bytes / t_gf / 1e9},
         "query_and_group_fwd_bwd": {"ms": t_gfb * 1e3},
         "QueryAndGroup_layer_ball_query_plus_group": {"ms": t_gl * 1e3},
+        "ball_query_r04_K128_fwd": {"ms": t_bf * 1e3},
+        "ball_query_r04_K128_fwd_bwd": {"ms": t_bfb * 1e3},
     }
 
     overlapped = pipelined_steps(mp, xyz, args.steps, args.warmup)

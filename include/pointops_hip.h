@@ -4,9 +4,11 @@
  *
  * Conventions (every entry point):
  *   - All pointers are DEVICE pointers to contiguous row-major arrays owned by
- *     the caller.  The library never allocates, frees or synchronises; scratch
- *     and workspace buffers are passed in (their size comes from the
- *     matching *_bytes query).
+ *     the caller.  The library never allocates device memory, frees or
+ *     synchronises; scratch and workspace buffers are passed in (their size
+ *     comes from the matching *_bytes query).  The one exception to "holds no
+ *     state" is pointops_fps_query_pipeline_f32, which keeps two events per
+ *     host thread and device to order its two streams.
  *   - Sizes are int64_t element counts; float arithmetic is IEEE binary32
  *     (binary64 for the *_f64 entries) with no contraction and no fast-math.
  *   - Work is enqueued on `stream`; the return value is hipSuccess or the
@@ -199,6 +201,32 @@ size_t pointops_ball_query_auto_workspace_bytes(int64_t B, int64_t Q, int64_t P)
 hipError_t pointops_ball_query_auto_f32(const float *queries, const float *points, int64_t *idx,
                                         float *dist2, void *workspace, int64_t B, int64_t Q,
                                         int64_t P, int64_t K, float radius_sq, hipStream_t stream);
+
+/* Backward of the dense ball query: the gradients of dist2 (B,Q,K) with
+ * respect to queries (B,Q,3) and points (B,P,3), float32, from the forward's
+ * idx.  Replaces _ball_query_mps.py:168-203 (gather, masking and scatter_add
+ * in PyTorch).  A slot with idx in [0, P) contributes c = (2 g) (q - p) per
+ * axis; padded slots contribute nothing.  grad_queries[b,q] = the row's c
+ * summed as ((s0 + s1) + s2) + s3, s_l the sum in order of the slots
+ * k = l (mod 4); grad_points[b,j] = -(the c of the slots holding j),
+ * summed in row order within 8 contiguous row segments, then over the
+ * segments in order: the same bits on every run.  Either gradient pointer
+ * may be NULL (not computed); every element of a non-NULL one is written.
+ * `workspace`: pointops_ball_query_backward_workspace_bytes(B, Q) bytes (per
+ * row its smallest and largest index), no initialisation needed.  The _f16
+ * entry takes IEEE half coordinates (uint16 bit patterns), widened exactly;
+ * the gradients stay float32. */
+size_t pointops_ball_query_backward_workspace_bytes(int64_t B, int64_t Q);
+hipError_t pointops_ball_query_backward_f32(const float *queries, const float *points,
+                                            const int64_t *idx, const float *grad_dist2,
+                                            float *grad_queries, float *grad_points,
+                                            void *workspace, int64_t B, int64_t Q, int64_t P,
+                                            int64_t K, hipStream_t stream);
+hipError_t pointops_ball_query_backward_f16(const uint16_t *queries, const uint16_t *points,
+                                            const int64_t *idx, const float *grad_dist2,
+                                            float *grad_queries, float *grad_points,
+                                            void *workspace, int64_t B, int64_t Q, int64_t P,
+                                            int64_t K, hipStream_t stream);
 
 /* Flat radius search (torch_cluster convention): first K global x indices
  * with squared distance < radius_sq, padded with -1, (Q,K); optional

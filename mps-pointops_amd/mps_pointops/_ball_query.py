@@ -118,7 +118,10 @@ def _launch(queries, points, query_lengths, point_lengths, radius_sq, k):
 
 
 class _BallQuery(torch.autograd.Function):
-    """Native forward; PyTorch gather/scatter backward (_ball_query_mps.py:122-203)."""
+    """Native forward and backward (_ball_query_mps.py:122-203 defines the
+    gradients).  The backward (pointops_ball_query_backward_*) sums each
+    query's slot contributions 2 g (q - p) in slot order and each point's in
+    row order with a fixed grouping, so its bits do not vary between runs."""
 
     @staticmethod
     def forward(ctx, queries, points, query_lengths, point_lengths, radius_sq, k):
@@ -129,34 +132,30 @@ class _BallQuery(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, grad_distances, grad_indices):
-        if grad_distances is None:
+        want_q, want_p = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+        if grad_distances is None or not (want_q or want_p):
             return None, None, None, None, None, None
         queries, points, indices = ctx.saved_tensors
         batch, query_count, k = indices.shape
-        if not indices.numel() or points.shape[1] == 0:
-            return torch.zeros_like(queries), torch.zeros_like(points), None, None, None, None
-        valid = indices >= 0
-        safe_indices = indices.clamp_min(0)
-        gathered = points.float().gather(
-            1, safe_indices.reshape(batch, -1, 1).expand(-1, -1, 3)
-        ).reshape(batch, query_count, k, 3)
-        delta = queries.float().unsqueeze(2) - gathered
-        # Mask before multiplying: 0 * NaN is NaN.
-        delta = torch.where(valid.unsqueeze(-1), delta, torch.zeros_like(delta))
-        valid_grad = torch.where(valid, grad_distances, torch.zeros_like(grad_distances))
-        contributions = (2.0 * valid_grad).unsqueeze(-1) * delta
-        grad_queries = (
-            contributions.sum(dim=2).to(queries.dtype) if ctx.needs_input_grad[0] else None
-        )
-        grad_points = None
-        if ctx.needs_input_grad[1]:
-            grad_points = torch.zeros_like(points, dtype=torch.float32)
-            grad_points.scatter_add_(
-                1, safe_indices.reshape(batch, -1, 1).expand(-1, -1, 3),
-                -contributions.reshape(batch, -1, 3),
-            )
-            grad_points = grad_points.to(points.dtype)
-        return grad_queries, grad_points, None, None, None, None
+        device = queries.device
+        grad_q = (torch.empty((batch, query_count, 3), dtype=torch.float32, device=device)
+                  if want_q else None)
+        grad_p = (torch.empty(points.shape, dtype=torch.float32, device=device)
+                  if want_p else None)
+        size = _native.size_query("pointops_ball_query_backward_workspace_bytes", batch,
+                                  query_count)
+        workspace = torch.empty(size, dtype=torch.uint8, device=device) if size else None
+        name = ("pointops_ball_query_backward_f32" if queries.dtype == torch.float32
+                else "pointops_ball_query_backward_f16")
+        _native.call(name, queries.data_ptr(), points.data_ptr(), indices.data_ptr(),
+                     grad_distances.float().contiguous().data_ptr(), _native.ptr(grad_q),
+                     _native.ptr(grad_p), _native.ptr(workspace), batch, query_count,
+                     points.shape[1], k, _native.stream(device))
+        if grad_q is not None:
+            grad_q = grad_q.to(queries.dtype)
+        if grad_p is not None:
+            grad_p = grad_p.to(points.dtype)
+        return grad_q, grad_p, None, None, None, None
 
 
 def ball_query(

@@ -42,6 +42,10 @@ _SIGNATURES: dict[str, list] = {
     "pointops_ball_query_f16": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_radius_flat_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "pointops_radius_flat_f16": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
+    "pointops_ball_query_backward_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                         _i64, _vp],
+    "pointops_ball_query_backward_f16": [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64,
+                                         _i64, _vp],
     "pointops_three_nn": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
@@ -70,6 +74,7 @@ _SIZE_QUERIES: dict[str, list] = {
     "pointops_knn3_windowed_workspace_bytes": [_i64, _i64, _i64],
     "pointops_three_interpolate_backward_workspace_bytes": [_i64, _i64, _i64],
     "pointops_ball_query_grid_workspace_bytes": [_i64, _i64, _i64],
+    "pointops_ball_query_backward_workspace_bytes": [_i64, _i64],
     "pointops_ball_query_auto_workspace_bytes": [_i64, _i64, _i64],
     "pointops_group_points_backward_workspace_bytes": [_i64, _i64, _i64, _i64],
 }
