@@ -500,6 +500,582 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     }
 }
 
+// fps_lead_kernel<P>: the tiled FPS above with the step chain taken by one
+// wave instead of all of them.
+//
+// Nine waves: eight followers (waves 0-7) hold the cloud's 64-point tiles
+// (the setup, tiles and exchanges of fps_tiled_kernel with an even split, P
+// tiles each) and the leader, wave 8, holds none.  After an exchange (every
+// follower publishes its kLeadCand best points and its bound, the next
+// largest running distance) the leader takes the exact steps of the run on
+// its own over the 64 candidates: largest key, ties to the smallest index,
+// the candidates updated with the points' own arithmetic, until the chosen
+// key is no longer above every bound.  Its step loop is hand-scheduled
+// gfx950 code (the chain is one wave's latency: wave maximum, ballot,
+// readlanes, update), at raised priority.  Per step it publishes only the
+// lane of the chosen candidate: four lanes are packed into a word, written
+// into an LDS ring every 4 steps (and at the end of the run) with the chosen
+// key of the block's first step, then the count of steps published.
+//
+// The followers follow the ring as it fills, a block of 4 steps at a time:
+// lane l fetches the centroid of step l / 16 (this wave's copy of the
+// candidates, by a lane permute) and tests tile l % 16's box against the
+// block's first chosen key (keys only decrease, so it bounds the largest
+// running distance of the block's later steps, and a tile it selects
+// without need only takes a no-op minimum), so one ballot gives the tile
+// masks of all four steps; then the masked tile updates.  Updates may be
+// applied in any order before the next exchange, since running distances
+// are minima.  At the end of a run follower 0 turns the ring's lanes into
+// sample indices (64 per lane permute) and stores them, then publishes the
+// progress words.  A run also ends after kLeadRing steps (the ring's size;
+// the ring is rewritten only after the next exchange's barrier, which every
+// follower reaches after reading it).  LDS ordering: one wave's LDS
+// operations complete in issue order, so a follower that reads a published
+// count (or the run's end) and then the ring sees the words the leader wrote
+// before that count.
+constexpr int kLeadWaves = 9;
+constexpr int kLeadThreads = kLeadWaves * kWave;
+constexpr int kLeadFollowers = 8;
+constexpr int kLeadCand = 8;  // candidates per follower: the leader's 64 lanes
+constexpr int kLeadRing = 256;
+
+template <int P>
+__global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
+    const float* __restrict__ xyz, const int64_t* __restrict__ ptr,
+    const int64_t* __restrict__ out_ptr, const int64_t* __restrict__ starts,
+    int64_t* __restrict__ out, int64_t N, int64_t npoint, int64_t start, int skip,
+    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk) {
+    constexpr int NS = kLeadFollowers;  // followers; they also run the setup's sort
+    constexpr int TS = NS * kWave;      // threads of the sort
+    constexpr int NF = kLeadFollowers;
+    constexpr int KC = kLeadCand;
+    constexpr int CAP = P * TS;         // points per cloud at most
+    constexpr int PO = P;               // tiles per follower
+    constexpr int kCells = 4096;
+    static_assert(KC * NF == kWave && KC + 1 <= kWave && P <= 16 && CAP <= 8192, "shape");
+    static_assert(kCells % TS == 0, "cells per thread");
+    constexpr int kSortInts = kCells + CAP;
+    constexpr int kBufVec = (kSortInts * 4 > CAP * 16 ? kSortInts * 4 : CAP * 16) / 16;
+    __shared__ float4 buf[kBufVec];
+    int* const cell_count = reinterpret_cast<int*>(buf);
+    int* const sorted_index = cell_count + kCells;
+    float4* const spts = buf;
+    __shared__ float red[6][NS];
+    __shared__ int wave_sum[NS];
+    // The candidates: coordinates with the point index in w, and keys;
+    // double-buffered by run parity, since followers read the table during
+    // a run while followers that have finished it already extract the next.
+    __shared__ float4 cand_pos[2][kWave];
+    __shared__ int cand_key[2][kWave];
+    __shared__ int bounds[NF];
+    // Per 4 steps, a row of 64 words written by one conflict-free store of
+    // the leader (lane l writes word l): the chosen candidate lanes (8 bits
+    // per step, word 0) and the chosen key of the first of them (word 1);
+    // the other words are padding.
+    __shared__ uint32_t ring[kLeadRing / 4][kWave];
+    // Word 0: steps published; word 1: the step at which the current run
+    // ended (read together as one 8-byte value); words 2-63: padding that
+    // the leader's other lanes write, so that its stores hit distinct
+    // addresses.  Accessed with relaxed workgroup-scope atomics (plain LDS
+    // reads and writes); compiler fences keep each wave's ring and mark
+    // accesses in program order, which the LDS then keeps.
+    __shared__ __align__(8) uint32_t marks[kWave];
+    // Set by the leader at the end of a run when every sample is taken, in
+    // the slot of the next iteration's parity: every wave reads it after the
+    // next barrier, and the leader writes that slot again only two barriers
+    // later.
+    __shared__ int done[2];
+
+    const Segment seg = segment_of(blockIdx.x, ptr, out_ptr, starts, N, npoint, start);
+    if (seg.cnt <= 0) return;  // uniform over the workgroup, before any barrier
+    const float* p = xyz + 3 * seg.in_lo;
+    int64_t* o = out + seg.out_lo;
+    const int n = static_cast<int>(seg.n);
+    const int tid = threadIdx.x;
+    const int wave = uniform(tid / kWave);  // known wave-uniform: scalar branches on it
+    const int lane = tid % kWave;
+    const bool leader = wave == NS;
+    const bool sorter = wave < NS;
+    const int fi = wave;  // follower number
+    const bool follower = !leader;
+    constexpr int kOutWave = 0;  // the first follower stores the samples
+    const int far0 = static_cast<int>(seg.start);
+    if (wave == kOutWave && lane == 0) o[0] = seg.base + far0;
+    auto publish = [&](int64_t before, int64_t done_steps) {
+        if (progress == nullptr || wave != kOutWave) return;
+        const int64_t whole = (seg.cnt + chunk - 1) / chunk;
+        const int64_t now = done_steps >= seg.cnt ? whole : done_steps / chunk;
+        if (before >= 0 && now == (before >= seg.cnt ? whole : before / chunk)) return;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        if (lane == 0)
+            __hip_atomic_store(progress + blockIdx.x, tag + static_cast<uint64_t>(now),
+                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    };
+    if (seg.cnt == 1 || n <= 0) {
+        publish(-1, seg.cnt);
+        return;
+    }
+
+    // ---- setup: the sort by waves 0-7
+    if (sorter)
+        for (int c = tid; c < kCells; c += TS) cell_count[c] = 0;
+    float lx[P], ly[P], lz[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = min(tid * P + k, n - 1);
+        lx[k] = sorter ? p[3 * j] : 0.f;
+        ly[k] = sorter ? p[3 * j + 1] : 0.f;
+        lz[k] = sorter ? p[3 * j + 2] : 0.f;
+    }
+    if (sorter) {
+        float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            mn[0] = fminf(mn[0], lx[k]); mx[0] = fmaxf(mx[0], lx[k]);
+            mn[1] = fminf(mn[1], ly[k]); mx[1] = fmaxf(mx[1], ly[k]);
+            mn[2] = fminf(mn[2], lz[k]); mx[2] = fmaxf(mx[2], lz[k]);
+        }
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            mn[a] = wave_min(mn[a]);
+            mx[a] = wave_max(mx[a]);
+        }
+        if (lane == 0) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) {
+                red[a][wave] = mn[a];
+                red[3 + a][wave] = mx[a];
+            }
+        }
+    }
+    if (tid == 0) {
+        marks[0] = marks[1] = 1u;
+        done[0] = done[1] = 0;
+    }
+    __syncthreads();  // box partials, cleared counters, marks
+    float lo[3], scale[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        float mn = red[a][0], mx = red[3 + a][0];
+#pragma unroll
+        for (int w = 1; w < NS; ++w) {
+            mn = fminf(mn, red[a][w]);
+            mx = fmaxf(mx, red[3 + a][w]);
+        }
+        lo[a] = mn;
+        const float ext = mx - mn;
+        scale[a] = (ext > 0.f && ext < INFINITY) ? 16.f / ext : 0.f;
+    }
+    int cell[P], rank[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const float c3[3] = {lx[k], ly[k], lz[k]};
+        uint32_t key = 0;
+#pragma unroll
+        for (int a = 0; a < 3; ++a) {
+            const float f = fminf(fmaxf((c3[a] - lo[a]) * scale[a], 0.f), 15.f);
+            const uint32_t q = static_cast<uint32_t>(f);
+#pragma unroll
+            for (int b = 0; b < 4; ++b) key |= ((q >> b) & 1u) << (3 * b + a);
+        }
+        cell[k] = static_cast<int>(key);
+        rank[k] = (sorter && tid * P + k < n) ? atomicAdd(&cell_count[key], 1) : 0;
+    }
+    __syncthreads();  // counts complete
+    {
+        constexpr int CPT = kCells / TS;
+        int run = 0;
+        if (sorter) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) {
+                const int v = cell_count[tid * CPT + c];
+                cell_count[tid * CPT + c] = run;
+                run += v;
+            }
+        }
+        int incl = run;
+#pragma unroll
+        for (int d = 1; d < kWave; d <<= 1) {
+            const int up = __shfl_up(incl, d, kWave);
+            if (lane >= d) incl += up;
+        }
+        if (sorter && lane == kWave - 1) wave_sum[wave] = incl;
+        __syncthreads();  // wave totals
+        int before = incl - run;
+        for (int w = 0; w < wave && w < NS; ++w) before += wave_sum[w];
+        if (sorter) {
+#pragma unroll
+            for (int c = 0; c < CPT; ++c) cell_count[tid * CPT + c] += before;
+        }
+    }
+    __syncthreads();  // offsets complete
+    if (sorter) {
+#pragma unroll
+        for (int k = 0; k < P; ++k)
+            if (tid * P + k < n) sorted_index[cell_count[cell[k]] + rank[k]] = tid * P + k;
+    }
+    __syncthreads();  // permutation complete
+
+    // ---- followers: their points, indices, running distances and boxes
+    const int my_tiles = follower ? PO : 0;
+    const int tile0 = fi * PO;
+    float px[PO], py[PO], pz[PO], md[PO];
+    int pcode[PO];
+#pragma unroll
+    for (int k = 0; k < PO; ++k) {
+        px[k] = py[k] = pz[k] = 0.f;
+        pcode[k] = 0x7FFFFFFF;
+        md[k] = -INFINITY;
+    }
+    float blo[3] = {INFINITY, INFINITY, INFINITY}, bhi[3] = {INFINITY, INFINITY, INFINITY};
+    if (follower) {
+        float cx, cy, cz;
+        {
+            const int f = min(max(far0, 0), n - 1);
+            cx = p[3 * f];
+            cy = p[3 * f + 1];
+            cz = p[3 * f + 2];
+        }
+#pragma unroll
+        for (int k = 0; k < PO; ++k) {
+            const int q = (tile0 + k) * kWave + lane;
+            const bool valid = k < my_tiles && q < n;
+            const int j = valid ? sorted_index[q] : 0;
+            px[k] = valid ? p[3 * j] : 0.f;
+            py[k] = valid ? p[3 * j + 1] : 0.f;
+            pz[k] = valid ? p[3 * j + 2] : 0.f;
+            pcode[k] = valid ? (j << 13) | q : 0x7FFFFFFF;
+            md[k] = !valid ? -INFINITY
+                           : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
+            const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
+            const float tly = wave_min(valid ? py[k] : INFINITY), thy = wave_max(valid ? py[k] : -INFINITY);
+            const float tlz = wave_min(valid ? pz[k] : INFINITY), thz = wave_max(valid ? pz[k] : -INFINITY);
+            if (lane == k && tlx <= thx && tly <= thy && tlz <= thz) {
+                blo[0] = tlx; bhi[0] = thx;
+                blo[1] = tly; bhi[1] = thy;
+                blo[2] = tlz; bhi[2] = thz;
+            }
+        }
+    }
+    // Per lane, the box of tile lane % 16 (the follower's tile boxes sit in
+    // lanes 0..PO-1; lanes without a tile hold [+inf, +inf], which no test
+    // selects), and the shift of step lane / 16's byte in a block's lanes.
+    static_assert(PO <= 16, "a follower holds at most 16 tiles");
+    float tlo[3], thi[3];
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        tlo[a] = __shfl(blo[a], lane & 15, kWave);
+        thi[a] = __shfl(bhi[a], lane & 15, kWave);
+    }
+    const uint32_t lane_shift = 8u * static_cast<uint32_t>(lane >> 4);
+    __syncthreads();  // every sorted index has been read
+    if (follower) {
+#pragma unroll
+        for (int k = 0; k < PO; ++k) {
+            const int q = (tile0 + k) * kWave + lane;
+            if (k < my_tiles && q < n) spts[q] = make_float4(px[k], py[k], pz[k], 0.f);
+        }
+    }
+    __syncthreads();  // coordinates by sorted position
+
+    if (leader) __builtin_amdgcn_s_setprio(3);
+    int64_t step = 1;
+    int parity = 0;
+    for (;;) {
+        if (follower) {
+            // Exchange: this follower's KC best points and its bound (the
+            // (KC+1)-th), as in fps_tiled_kernel.
+            auto top2 = [&](bool limited, uint64_t lim, uint64_t& a1, uint64_t& a2) {
+                a1 = 0;
+                a2 = 0;
+#pragma unroll
+                for (int k = 0; k < PO; ++k) {
+                    if (k >= my_tiles) break;  // wave-uniform
+                    const uint64_t key =
+                        (static_cast<uint64_t>(static_cast<uint32_t>(f2i(md[k])) ^ 0x80000000u) << 32) |
+                        static_cast<uint32_t>(~pcode[k]);
+                    const bool below = !limited || key < lim;
+                    const bool first = below && key > a1;
+                    const bool second = below && !first && key > a2;
+                    a2 = first ? a1 : (second ? key : a2);
+                    a1 = first ? key : a1;
+                }
+            };
+            uint64_t h1, h2;
+            top2(false, 0, h1, h2);
+            uint64_t unknown = 0;
+            int ck = 0, cc = 0x7FFFFFFF;
+            int bound = 0;
+#pragma unroll
+            for (int r = 0; r <= KC; ++r) {
+                const uint32_t hh = static_cast<uint32_t>(h1 >> 32);
+                const uint32_t wv = wave_max_u32_l63(hh);
+                const uint64_t at = ballot(hh == wv);
+                int wl = static_cast<int>(__builtin_ctzll(at));
+                uint32_t wlo;
+                if (__popcll(at) > 1) {
+                    wlo = wave_max_u32_l63(hh == wv ? static_cast<uint32_t>(h1) : 0u);
+                    wl = static_cast<int>(__builtin_ctzll(ballot(hh == wv && static_cast<uint32_t>(h1) == wlo)));
+                } else {
+                    wlo = static_cast<uint32_t>(readlane(static_cast<int>(h1), wl));
+                }
+                if (r == KC) {
+                    bound = static_cast<int>(wv ^ 0x80000000u);
+                    break;
+                }
+                ck = writelane(ck, static_cast<int>(wv ^ 0x80000000u), r);
+                cc = writelane(cc, static_cast<int>(~wlo), r);
+                const bool won = lane == wl;
+                if ((unknown >> wl) & 1u) {
+                    uint64_t n1, n2;
+                    top2(true, (static_cast<uint64_t>(wv) << 32) | wlo, n1, n2);
+                    h1 = won ? n1 : h1;
+                    h2 = won ? n2 : h2;
+                    unknown &= ~(uint64_t(1) << wl);
+                } else {
+                    h1 = won ? h2 : h1;
+                    unknown |= uint64_t(1) << wl;
+                }
+            }
+            if (lane < KC) {
+                // Padding codes 0x7FFFFFFF: a published padding key never wins a
+                // step, so any in-range position serves.
+                const float4 c = spts[min(cc & 0x1FFF, CAP - 1)];
+                cand_pos[parity][fi * KC + lane] = make_float4(c.x, c.y, c.z, i2f(cc >> 13));
+                cand_key[parity][fi * KC + lane] = ck;
+            }
+            if (lane == 0) bounds[fi] = bound;
+        }
+        __syncthreads();  // candidates and bounds published; the last run applied
+        if (done[parity]) break;  // uniform: written by the leader before this barrier
+        const int64_t run_start = step;
+        const float4 mine = cand_pos[parity][lane];  // w: the point index
+        if (leader) {
+            int maxb_v = bounds[0];
+#pragma unroll
+            for (int w = 1; w < NF; ++w) maxb_v = max(maxb_v, bounds[w]);
+            int cmd = cand_key[parity][lane];
+            const int cidx = f2i(mine.w);
+            const float ccx = mine.x, ccy = mine.y, ccz = mine.z;
+            // A later step of the run needs a key above every bound and
+            // above 0.  A taken candidate's key becomes its distance to
+            // itself, 0 -- or stays +inf/-inf when a coordinate is not
+            // finite (the distance is NaN) -- so with finite candidates none
+            // is taken twice in one run; a non-finite candidate limits runs
+            // to one step.
+            const bool odd = !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
+            const int maxb = ballot(odd) ? INT_MAX : max(uniform(maxb_v), 0);
+            const int64_t rest = seg.cnt - step;
+            int rem = uniform(static_cast<int>(rest < kLeadRing ? rest : kLeadRing));  // steps left
+            const uint32_t base = static_cast<uint32_t>(run_start);
+            int taken = 0;
+            // The candidates' LDS loads complete here, so that the loop's
+            // waits never cover its own ring stores.
+            __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+            int wv = wave_max_i32_l63(cmd);  // the first step after an exchange is exact
+            int block_key = wv;              // chosen key of the block's first step
+            const int nidx = -cidx;
+            const int imin = INT_MIN;
+            uint32_t packed = 0, sh = 0;
+            for (;;) {
+                // Up to 4 steps (one block), as hand-scheduled gfx950 code:
+                // the chosen candidate (the lowest lane holding the largest
+                // key wv; on a tie, the smallest index by a second wave
+                // maximum of -index), its coordinates by readlane, every
+                // candidate's key lowered to its distance to them, the lane
+                // packed into `packed`, then the next step's largest key by
+                // the DPP reduction of wave_max_i32_l63.  It stops after 4
+                // steps (st = 0, wv the next step's key), or when the run
+                // ends (st = 1): no steps left, or the next key is not above
+                // every bound.  The s_nop's give the wait states a DPP read
+                // of a VALU result (2), a readlane of a DPP result (1) and a
+                // VALU read of a readlane's SGPR (2) need.
+                int st, wl, t, fx, fy, fz;
+                uint64_t tt;
+                float t0, t1, t2;
+                int m;
+                asm volatile(
+                    "s_nop 1\n\t"
+                    "s_mov_b32 %[sh], 0\n\t"
+                    "s_mov_b32 %[pk], 0\n"
+                    "1:\n\t"
+                    "v_cmp_eq_u32_e32 vcc, %[wv], %[cmd]\n\t"
+                    "s_ff1_i32_b64 %[wl], vcc\n\t"
+                    "s_bcnt1_i32_b64 %[t], vcc\n\t"
+                    "s_cmp_gt_u32 %[t], 1\n\t"
+                    "s_cbranch_scc1 5f\n"
+                    "2:\n\t"
+                    "v_readlane_b32 %[fx], %[cx], %[wl]\n\t"
+                    "v_readlane_b32 %[fy], %[cy], %[wl]\n\t"
+                    "v_readlane_b32 %[fz], %[cz], %[wl]\n\t"
+                    "s_lshl_b32 %[t], %[wl], %[sh]\n\t"
+                    "v_subrev_f32_e32 %[t0], %[fx], %[cx]\n\t"
+                    "v_subrev_f32_e32 %[t1], %[fy], %[cy]\n\t"
+                    "v_subrev_f32_e32 %[t2], %[fz], %[cz]\n\t"
+                    "s_or_b32 %[pk], %[pk], %[t]\n\t"
+                    "v_mul_f32_e32 %[t0], %[t0], %[t0]\n\t"
+                    "v_mul_f32_e32 %[t1], %[t1], %[t1]\n\t"
+                    "v_mul_f32_e32 %[t2], %[t2], %[t2]\n\t"
+                    "v_add_f32_e32 %[t0], %[t0], %[t1]\n\t"
+                    "s_add_u32 %[sh], %[sh], 8\n\t"
+                    "v_add_f32_e32 %[t0], %[t0], %[t2]\n\t"
+                    "s_sub_u32 %[rem], %[rem], 1\n\t"
+                    "v_min_f32_e32 %[cmd], %[cmd], %[t0]\n\t"
+                    "s_cmp_eq_u32 %[rem], 0\n\t"
+                    "s_cbranch_scc1 8f\n\t"
+                    "v_max_i32_dpp %[m], %[cmd], %[cmd] quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_mirror row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+                    "s_nop 0\n\t"
+                    "v_readlane_b32 %[wv], %[m], 63\n\t"
+                    "s_cmp_le_i32 %[wv], %[maxb]\n\t"
+                    "s_cbranch_scc1 8f\n\t"
+                    "s_cmp_lt_u32 %[sh], 32\n\t"
+                    "s_cbranch_scc1 1b\n\t"
+                    "s_mov_b32 %[st], 0\n\t"
+                    "s_branch 9f\n"
+                    "5:\n\t"
+                    "v_cndmask_b32_e32 %[m], %[imin], %[nidx], vcc\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] quad_perm:[1,0,3,2] row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] quad_perm:[2,3,0,1] row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_half_mirror row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_mirror row_mask:0xf bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_bcast:15 row_mask:0xa bank_mask:0xf\n\t"
+                    "s_nop 1\n\t"
+                    "v_max_i32_dpp %[m], %[m], %[m] row_bcast:31 row_mask:0xc bank_mask:0xf\n\t"
+                    "s_nop 0\n\t"
+                    "v_readlane_b32 %[t], %[m], 63\n\t"
+                    "s_nop 1\n\t"
+                    "v_cmp_eq_u32_e64 %[tt], %[t], %[nidx]\n\t"
+                    "s_and_b64 vcc, vcc, %[tt]\n\t"
+                    "s_ff1_i32_b64 %[wl], vcc\n\t"
+                    "s_branch 2b\n"
+                    "8:\n\t"
+                    "s_mov_b32 %[st], 1\n"
+                    "9:\n\t"
+                    "s_nop 1"
+                    : [cmd] "+v"(cmd), [wv] "+s"(wv), [rem] "+s"(rem), [pk] "=&s"(packed),
+                      [sh] "=&s"(sh), [st] "=&s"(st), [wl] "=&s"(wl), [t] "=&s"(t),
+                      [fx] "=&s"(fx), [fy] "=&s"(fy), [fz] "=&s"(fz), [tt] "=&s"(tt),
+                      [t0] "=&v"(t0), [t1] "=&v"(t1), [t2] "=&v"(t2), [m] "=&v"(m)
+                    : [cx] "v"(ccx), [cy] "v"(ccy), [cz] "v"(ccz), [nidx] "v"(nidx),
+                      [imin] "v"(imin), [maxb] "s"(maxb)
+                    : "vcc", "scc");
+                taken += static_cast<int>(sh >> 3);
+                if (st != 0) break;
+                // A full block: its row, then the count.  Lane l writes word l
+                // (distinct addresses, no conflicts).
+                ring[(taken >> 2) - 1][lane] = lane == 0 ? packed : static_cast<uint32_t>(block_key);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // the row is issued before the count
+                __hip_atomic_store(&marks[lane == 0 ? 0 : lane + (lane == 1)], base + taken,
+                                   __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+                block_key = wv;
+            }
+            // The last block's row (full or partial).
+            ring[(taken - 1) >> 2][lane] = lane == 0 ? packed : static_cast<uint32_t>(block_key);
+            step += taken;
+            done[parity ^ 1] = step >= seg.cnt ? 1 : 0;  // read by every wave after the next barrier
+            __atomic_signal_fence(__ATOMIC_SEQ_CST);
+            // Count and end of the run (lanes 0 and 1 of one store: a follower
+            // never sees an end beyond the count it reads with it).
+            __hip_atomic_store(&marks[lane], lane < 2 ? base + taken : 0u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_WORKGROUP);
+        } else if (follower) {
+            // A block of up to 4 published steps, all box tests at once: lane
+            // l takes tile l % 16 (a follower holds at most 16) and step
+            // l / 16 of the block, whose centroid it fetches from this wave's
+            // copy of the candidates by a lane permute; one ballot gives the
+            // tile masks of the four steps (16 bits each), tested against
+            // the block's first chosen key.  Then the masked updates (minima,
+            // so their order does not matter), the centroid of step j read
+            // from lane 16 j.
+            auto block = [&](uint32_t lanes4, float M1, int cnt) {
+                const int wl = static_cast<int>((lanes4 >> lane_shift) & 63u);
+                const float cx = i2f(__builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.x)));
+                const float cy = i2f(__builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.y)));
+                const float cz = i2f(__builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.z)));
+                const float gx = cx - __builtin_amdgcn_fmed3f(cx, tlo[0], thi[0]);
+                const float gy = cy - __builtin_amdgcn_fmed3f(cy, tlo[1], thi[1]);
+                const float gz = cz - __builtin_amdgcn_fmed3f(cz, tlo[2], thi[2]);
+                float lb = gx * gx;
+                lb = lb + gy * gy;
+                lb = lb + gz * gz;
+                uint64_t pend = ballot(lb < M1);
+                if (cnt < 4) pend &= (uint64_t(1) << (16 * cnt)) - 1;
+                if (pend == 0) return;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t pj = static_cast<uint32_t>(pend >> (16 * j)) & 0xFFFFu;
+                    if (pj == 0) continue;
+                    const float fx = i2f(readlane(f2i(cx), 16 * j));
+                    const float fy = i2f(readlane(f2i(cy), 16 * j));
+                    const float fz = i2f(readlane(f2i(cz), 16 * j));
+#pragma unroll
+                    for (int k = 0; k < PO; ++k)
+                        if ((pj >> k) & 1u)
+                            md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], fx, fy, fz));
+                }
+            };
+            int a = 0;  // steps of this run applied (a multiple of 4 until the run ends)
+            for (;;) {
+                const uint64_t m = __hip_atomic_load(reinterpret_cast<uint64_t*>(marks), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_WORKGROUP);
+                __atomic_signal_fence(__ATOMIC_SEQ_CST);  // ring reads after the mark
+                const int pub = uniform(static_cast<int>(m)) - static_cast<int>(run_start);
+                const int end = uniform(static_cast<int>(m >> 32)) - static_cast<int>(run_start);
+                // Whole blocks (counts published during a run are multiples of 4).
+                while (a + 4 <= pub) {
+                    const uint32_t* row = ring[a >> 2];
+                    const uint32_t lanes4 = static_cast<uint32_t>(uniform(static_cast<int>(row[0])));
+                    const float M1 = i2f(uniform(static_cast<int>(row[1])));
+                    block(lanes4, M1, 4);
+                    a += 4;
+                }
+                if (end > 0 && pub >= end) {
+                    // The run's last, partial block.
+                    if (a < end) {
+                        const uint32_t* row = ring[a >> 2];
+                        const uint32_t lanes4 = static_cast<uint32_t>(uniform(static_cast<int>(row[0])));
+                        const float M1 = i2f(uniform(static_cast<int>(row[1])));
+                        block(lanes4, M1, end - a);
+                        a = end;
+                    }
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(1);
+            }
+            if (wave == kOutWave) {
+                // The run's samples: lane i of a batch takes step c0 + i, its
+                // chosen lane from the ring's bytes and that candidate's index
+                // by a lane permute (all lanes take part).
+                for (int c0 = 0; c0 < a; c0 += kWave) {
+                    const int si = min(c0 + lane, a - 1);
+                    const int wl = reinterpret_cast<const uint8_t*>(ring[si >> 2])[si & 3];
+                    const int idx = __builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.w));
+                    if (c0 + lane < a) o[run_start + c0 + lane] = seg.base + idx;
+                }
+            }
+            step = run_start + a;
+            publish(run_start, step);
+        }
+        parity ^= 1;
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__ xyz,
                                                        const int64_t* __restrict__ ptr,
@@ -1140,15 +1716,30 @@ constexpr int kGlobalThreads = 1024;
 template <int P>
 constexpr int kTilesFirstHalf = P == 8 ? 9 : P;
 
+// The single-cloud kernel that runs P points per sorting thread: the
+// leader/follower kernel up to 4096 points, the tiled kernel above (its
+// follower tiles would not fit the registers of nine waves).
+template <int P>
+const void* dense_fps_kernel() {
+    if constexpr (P <= 8) return reinterpret_cast<const void*>(&fps_lead_kernel<P>);
+    else return reinterpret_cast<const void*>(&fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>);
+}
+
 template <int P>
 hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_ptr,
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream,
                        uint64_t* progress = nullptr, uint64_t tag = 0, int64_t chunk = 1,
                        size_t reserve = 0) {
-    hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>), dim3(static_cast<uint32_t>(blocks)),
-                       dim3(kRegsThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                       start, skip, progress, tag, chunk);
+    if constexpr (P > 8) {
+        hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>), dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kRegsThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                           start, skip, progress, tag, chunk);
+    } else {
+        hipLaunchKernelGGL((fps_lead_kernel<P>), dim3(static_cast<uint32_t>(blocks)),
+                           dim3(kLeadThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
+                           start, skip, progress, tag, chunk);
+    }
     return hipGetLastError();
 }
 
@@ -1287,7 +1878,7 @@ size_t fps_reserve_lds() {
     static const size_t bytes = [] {
         hipFuncAttributes a{};
         int dev = 0, per_block = 0, per_cu = 0;
-        const void* k = reinterpret_cast<const void*>(&fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>);
+        const void* k = dense_fps_kernel<P>();
         if (hipFuncGetAttributes(&a, k) != hipSuccess || hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&per_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess ||
             hipDeviceGetAttribute(&per_cu, hipDeviceAttributeMaxSharedMemoryPerMultiprocessor, dev) != hipSuccess)
