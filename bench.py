@@ -657,6 +657,13 @@ def run_other(args) -> dict:
         r = max(1, reps // 5)
         t_knn = timer.time(lambda: mp.knn(query, ref, 16), r)
         t_feat = timer.time(lambda: mp.knn(feat, feat, 20), reps)
+        # DGCNN's deeper EdgeConv width (D=128) at the same sizes, and the
+        # reference's own feature-kNN sizes (Q = N = 1024, k = 20, D = 64/128).
+        g = torch.Generator().manual_seed(44)
+        feat128 = torch.randn(8, 2048, 128, generator=g).to(dev)
+        small = {d: torch.randn(1, 1024, d, generator=g).to(dev) for d in (64, 128)}
+        t_feat128 = timer.time(lambda: mp.knn(feat128, feat128, 20), reps)
+        t_small = {d: timer.time(lambda x=x: mp.knn(x, x, 20), reps) for d, x in small.items()}
         M, N = query.shape[1], ref.shape[1]
         Bf, Nf, D = feat.shape
         # The same sizes on clustered references with uniform queries, through
@@ -673,12 +680,16 @@ def run_other(args) -> dict:
                    value=M / t_knn, unit="queries/s",
                    config={"workload": "c4 kNN at scale + DGCNN feature kNN (8,2048,64) K=20"},
                    ops_ms={"knn": t_knn * 1e3, "dgcnn_feature_knn": t_feat * 1e3,
+                           "dgcnn_feature_knn_d128": t_feat128 * 1e3,
+                           "feature_knn_q1024_d64": t_small[64] * 1e3,
+                           "feature_knn_q1024_d128": t_small[128] * 1e3,
                            "knn_clustered_uniform_queries": t_clustered * 1e3,
                            "knn_clustered_brute_force_kernel": t_brute * 1e3},
                    knn_path="grid search (knn_grid.hip): examines the cells around each query, "
                             "not all M x N pairs",
                    tops={"knn_brute_force_equivalent": PAIR_OPS * M * N / t_knn / 1e12,
-                         "dgcnn_feature_knn": (3 * D - 1) * Bf * Nf * Nf / t_feat / 1e12})
+                         "dgcnn_feature_knn": (3 * D - 1) * Bf * Nf * Nf / t_feat / 1e12,
+                         "dgcnn_feature_knn_d128": (3 * 128 - 1) * Bf * Nf * Nf / t_feat128 / 1e12})
     elif args.config == "c5":
         y1, y2 = (t.to(dev) for t in make_c5())
         B, P, _ = y1.shape

@@ -5,10 +5,16 @@
 // to the sampled set is largest, ties to the smaller index; points with
 // ((x*x + y*y) + z*z) < fl32(1e-3) are never picked when skip_near_origin is
 // set (their running distance is -inf); if no point can be picked the step
-// takes index 0.
-//
+// takes index 0.  A point with a NaN coordinate is never picked either: its
+// running distance starts at -inf, as a NaN running distance never wins
+// `m > best` in kernels/fps.metal:77-83 (reference.py:56-57's torch.minimum
+// and argmax would instead let NaN win).
 //
 // Kernels:
+//   fps_lead_kernel<P>      one workgroup per cloud of up to 4096 points:
+//                           the tiled scheme below with the step chain taken
+//                           by one leader wave and the tile updates applied
+//                           by eight follower waves.
 //   fps_tiled_kernel<P,T,PO> one workgroup per cloud of up to 8192 points
 //                           (batched or ragged), its points and running
 //                           distances in VGPRs, sorted into spatially compact
@@ -24,6 +30,8 @@
 //                           and a bound, after which every workgroup takes
 //                           exact steps over the candidates alone until the
 //                           bound could be reached.
+//   fps_stream_kernel<T>    the same exchange for clouds too large for the
+//                           CUs' registers, the cloud streamed from HBM.
 #include <hip/hip_cooperative_groups.h>
 
 #include <cstdlib>
@@ -43,6 +51,17 @@ __device__ __forceinline__ bool near_origin(float x, float y, float z) {
     mag = mag + y * y;
     mag = mag + z * z;
     return mag < kSkipThreshold;
+}
+
+// Initial running distance of a point: -inf for one that is never sampled
+// (a NaN coordinate, as in kernels/fps.metal:77-83, where a NaN running
+// distance never wins `m > best`; or near the origin when skip is set),
+// +inf otherwise.  Every step's minimum keeps -inf, so such a point is
+// never taken while another point of its cloud has a larger running
+// distance (a taken point keeps 0).
+__device__ __forceinline__ float initial_running(int skip, float x, float y, float z) {
+    const bool nan = __builtin_isnan(x) || __builtin_isnan(y) || __builtin_isnan(z);
+    return (nan || (skip && near_origin(x, y, z))) ? -INFINITY : INFINITY;
 }
 
 // Segment of workgroup b: dense clouds (ptr == nullptr) or ragged ones.
@@ -314,8 +333,7 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
         py[k] = valid ? p[3 * j + 1] : 0.f;
         pz[k] = valid ? p[3 * j + 2] : 0.f;
         pcode[k] = valid ? (j << 13) | q : 0x7FFFFFFF;
-        md[k] = !valid ? -INFINITY
-                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+        md[k] = !valid ? -INFINITY : initial_running(skip, px[k], py[k], pz[k]);
         md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
         // Box of tile k (padding excluded), kept in lane k.
         const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
@@ -441,8 +459,10 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
         // A taken candidate's key becomes its distance to itself, 0 -- or
         // stays +inf/-inf when a coordinate is not finite (the distance is
         // NaN) -- so with finite candidates none is taken twice in one run;
-        // a non-finite candidate limits runs to one step.
-        const bool odd = !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
+        // a non-finite candidate limits runs to one step.  One at -inf (a
+        // NaN point, never sampled) does not: it can only be a run's first
+        // step, after which no key is above 0.
+        const bool odd = cmd >= 0 && !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
         const int maxb = ballot(odd) ? INT_MAX : max(uniform(maxb_v), 0);
         // Steps of this run: at most `left`, counted in 32 bits.
         const int left = static_cast<int>(min<int64_t>(seg.cnt - step, int64_t(1) << 30));
@@ -745,8 +765,7 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
             py[k] = valid ? p[3 * j + 1] : 0.f;
             pz[k] = valid ? p[3 * j + 2] : 0.f;
             pcode[k] = valid ? (j << 13) | q : 0x7FFFFFFF;
-            md[k] = !valid ? -INFINITY
-                           : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+            md[k] = !valid ? -INFINITY : initial_running(skip, px[k], py[k], pz[k]);
             md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
             const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
             const float tly = wave_min(valid ? py[k] : INFINITY), thy = wave_max(valid ? py[k] : -INFINITY);
@@ -863,8 +882,10 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
             // itself, 0 -- or stays +inf/-inf when a coordinate is not
             // finite (the distance is NaN) -- so with finite candidates none
             // is taken twice in one run; a non-finite candidate limits runs
-            // to one step.
-            const bool odd = !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
+            // to one step.  One at -inf (a NaN point, never sampled) does
+            // not: it can only be a run's first step, after which no key is
+            // above 0.
+            const bool odd = cmd >= 0 && !(isfinite(ccx) && isfinite(ccy) && isfinite(ccz));
             const int maxb = ballot(odd) ? INT_MAX : max(uniform(maxb_v), 0);
             const int64_t rest = seg.cnt - step;
             int rem = uniform(static_cast<int>(rest < kLeadRing ? rest : kLeadRing));  // steps left
@@ -1097,7 +1118,7 @@ __global__ __launch_bounds__(T) void fps_global_kernel(const float* __restrict__
     const int lane = tid % kWave;
 
     for (int64_t j = tid; j < n; j += T) {
-        md[j] = (skip && near_origin(p[3 * j], p[3 * j + 1], p[3 * j + 2])) ? -INFINITY : INFINITY;
+        md[j] = initial_running(skip, p[3 * j], p[3 * j + 1], p[3 * j + 2]);
     }
     int64_t far = seg.start;
     for (int64_t step = 0; step < seg.cnt; ++step) {
@@ -1340,8 +1361,7 @@ __global__ __launch_bounds__(T) void fps_lazy_kernel(
         px[k] = valid ? px[k] : 0.f;
         py[k] = valid ? py[k] : 0.f;
         pz[k] = valid ? pz[k] : 0.f;
-        md[k] = !valid ? -INFINITY
-                       : ((skip && near_origin(px[k], py[k], pz[k])) ? -INFINITY : INFINITY);
+        md[k] = !valid ? -INFINITY : initial_running(skip, px[k], py[k], pz[k]);
     }
     if (tid == 0) {
         abort_flag = 0;
@@ -1568,8 +1588,7 @@ __global__ __launch_bounds__(T) void fps_stream_kernel(
             float v[kStreamUnroll];
 #pragma unroll
             for (int u = 0; u < kStreamUnroll; ++u)
-                v[u] = exch != 0 ? m[u]
-                                 : ((skip && near_origin(x[u], y[u], z[u])) ? -INFINITY : INFINITY);
+                v[u] = exch != 0 ? m[u] : initial_running(skip, x[u], y[u], z[u]);
             for (int i = 0; i < npend; ++i) {  // each centroid read once per batch
                 const float4 c = pend[i];
 #pragma unroll

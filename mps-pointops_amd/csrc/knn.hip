@@ -875,6 +875,11 @@ hipError_t launch_dense(const float* query, const float* ref, float* dist, int64
         if (K <= 16) return launch_feat_lane<16, 64>(query, ref, dist, idx, B, M, N, K, stream);
         return launch_feat_lane<32, 64>(query, ref, dist, idx, B, M, N, K, stream);
     }
+    if (!DIM3 && D == 128 && K <= 32 && aligned && lane_grid_ok) {
+        if (K <= 8) return launch_feat_lane<8, 128>(query, ref, dist, idx, B, M, N, K, stream);
+        if (K <= 16) return launch_feat_lane<16, 128>(query, ref, dist, idx, B, M, N, K, stream);
+        return launch_feat_lane<32, 128>(query, ref, dist, idx, B, M, N, K, stream);
+    }
     const int64_t rows = B * M;
     const dim3 grid(static_cast<uint32_t>((rows + kKnnWaves - 1) / kKnnWaves));
     const dim3 block(kKnnThreads);

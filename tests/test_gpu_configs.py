@@ -99,6 +99,17 @@ def test_c4_dgcnn_feature_knn_full(cuda_device):
     same_bits(host(d), want_d)
 
 
+def test_dgcnn_feature_knn_d128(cuda_device):
+    """DGCNN's deeper layer width: (2, 2048, 128), K = 20, query is ref."""
+    import mps_pointops as mp
+
+    feat = torch.randn(2, 2048, 128, generator=torch.Generator().manual_seed(44))
+    d, i = mp.knn(feat.cuda(), feat.cuda(), 20)
+    want_d, want_i = O.knn_feat(feat, feat, 20)
+    np.testing.assert_array_equal(host(i), want_i)
+    same_bits(host(d), want_d)
+
+
 def test_c5_chamfer_forward_backward_full(cuda_device):
     """B=32, P1=P2=8192, mean/mean: loss and both gradients against the
     closed form on the oracle's nearest pairs."""

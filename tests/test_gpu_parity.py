@@ -396,6 +396,42 @@ def test_fps_skip_near_origin_boundary(cuda_device):
     assert picked.isdisjoint(range(1, 41)) and 41 in picked
 
 
+@pytest.mark.parametrize("B,n,npoint,frac,strategy,skip", [
+    (2, 1000, 300, 0.05, "single", False),        # one workgroup, leader/follower kernel
+    (1, 40, 25, 0.75, "single", False),           # fewer finite points than samples
+    (2, 6000, 300, 0.05, "single", True),         # 8192-point tiled kernel
+    (2, 9000, 200, 0.05, "single", False),        # running distances in scratch
+    (1, 70_000, 200, 0.02, "multigroup", False),  # cooperative lazy kernel
+    (1, (1 << 21) + 5, 100, 0.02, "auto", False), # streaming kernel
+])
+def test_fps_nan_points_never_sampled(cuda_device, B, n, npoint, frac, strategy, skip):
+    """A point with a NaN coordinate is never sampled, and the others are
+    sampled as if it were absent: in kernels/fps.metal:77-83 its NaN running
+    distance never wins `m > best`.  (reference.py:56-57, torch.minimum then
+    argmax, would pick the first NaN point instead.)  Expected: the oracle's
+    FPS of each cloud without its NaN points, mapped back to the full
+    cloud's indices; the start point is finite."""
+    import mps_pointops as mp
+
+    print(f"fps nan B={B} n={n} npoint={npoint} strategy={strategy}", flush=True)
+    xyz = rand_cloud(B, n, 31 + n)
+    g = np.random.default_rng(n)
+    start = n // 3
+    bad = g.random((B, n)) < frac
+    bad[:, start] = False
+    axis = g.integers(0, 3, (B, n))
+    for b in range(B):
+        rows = np.nonzero(bad[b])[0]
+        xyz[b, rows, axis[b, rows]] = float("nan")
+    got = host(mp.furthest_point_sample(xyz.cuda(), npoint, start, skip, strategy=strategy))
+    for b in range(B):
+        keep = np.nonzero(~bad[b])[0]
+        sub = xyz[b:b + 1, keep].contiguous()
+        want = keep[O.fps(sub, npoint, int(np.searchsorted(keep, start)), skip)[0]]
+        np.testing.assert_array_equal(got[b], want)
+        assert not bad[b, got[b]].any()
+
+
 def _fps_shape_case(case: str) -> tuple[torch.Tensor, int, int, bool]:
     seeds = {"uniform_exhausted": 1, "blobs_skip": 2, "plane": 3, "duplicates": 4,
              "mixed_scale": 5, "infinite": 6}
@@ -679,19 +715,21 @@ def test_knn_feat_matches_oracle(cuda_device, dim, k):
     same_bits(host(d), want_d)
 
 
+@pytest.mark.parametrize("dim", [64, 128])
 @pytest.mark.parametrize("m,n,k", [(1, 1, 1), (63, 15, 8), (65, 17, 9), (130, 100, 16),
                                    (70, 1000, 17), (64, 2049, 32), (3, 40, 33)])
-def test_knn_feat_dim64_lane_path(cuda_device, m, n, k):
-    """D=64, K<=32 runs one lane per query with LDS reference tiles: ragged
-    tiles and wave ranges, duplicate references (ties), non-finite queries
-    and references, and K=33 (wave-per-query path) against the oracle."""
+def test_knn_feat_lane_path(cuda_device, m, n, k, dim):
+    """D=64 and D=128 with K<=32 run one lane per query with LDS reference
+    tiles: ragged tiles and wave ranges, duplicate references (ties),
+    non-finite queries and references, and K=33 (wave-per-query path)
+    against the oracle."""
     import mps_pointops as mp
 
     if k > n:
         k = n
-    g = torch.Generator().manual_seed(1000 * m + n + k)
-    ref = torch.randn(2, n, 64, generator=g)
-    query = torch.randn(2, m, 64, generator=g)
+    g = torch.Generator().manual_seed(1000 * m + n + k + dim)
+    ref = torch.randn(2, n, dim, generator=g)
+    query = torch.randn(2, m, dim, generator=g)
     if n > 4:
         ref[:, n - 1] = ref[:, 1]
         ref[:, n // 2] = ref[:, 1]
@@ -700,7 +738,7 @@ def test_knn_feat_dim64_lane_path(cuda_device, m, n, k):
     query[:, 0] = ref[:, min(1, n - 1)]
     if m > 2:
         query[0, 2, 5] = float("inf")
-        query[1, 1, 63] = float("nan")
+        query[1, 1, dim - 1] = float("nan")
     want_d, want_i = O.knn_feat(query, ref, k)
     d, i = mp.knn(query.cuda(), ref.cuda(), k)
     np.testing.assert_array_equal(host(i), want_i)
