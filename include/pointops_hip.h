@@ -280,6 +280,22 @@ hipError_t pointops_three_interpolate_backward_csr(const float *grad_out, const 
                                                    const float *weights, float *grad_features,
                                                    void *workspace, int64_t B, int64_t C,
                                                    int64_t M, int64_t N, hipStream_t stream);
+/* The two halves of pointops_three_interpolate_backward_csr, so that the CSR
+ * can be built when the forward runs (the indices and weights are known
+ * then) and the backward only gathers: _csr_build writes the CSR of
+ * (idx, weights) into `workspace` (as above); _backward_from_csr reads it
+ * and writes grad_features, the same bits as the combined call.  The
+ * workspace must hold a CSR built with the same B, M and N on the same
+ * stream (or one ordered before it).  Same limits as the combined call.
+ * Replace the same reference code (pointnet2.py:179-186). */
+hipError_t pointops_three_interpolate_csr_build(const int32_t *idx, const float *weights,
+                                               void *workspace, int64_t B, int64_t M, int64_t N,
+                                               hipStream_t stream);
+hipError_t pointops_three_interpolate_backward_from_csr(const float *grad_out,
+                                                        const void *workspace,
+                                                        float *grad_features, int64_t B,
+                                                        int64_t C, int64_t M, int64_t N,
+                                                        hipStream_t stream);
 
 /* --------------------------------------------------- PointNet++ grouping */
 
@@ -293,9 +309,14 @@ hipError_t pointops_group_points(const float *features, const void *idx, int idx
 
 /* The gradient of that gather (compat.py:62-73, torch.gather's scatter-add):
  * grad_features[b,c,n] = the float sum of grad_out[b,c,p] over the p with
- * idx[b,p] = n, added in increasing p for a point gathered at most 256 times
- * (deterministic), in an unspecified order for one gathered more often; 0
- * for a point never gathered; every element is written.  grad_out channel c of batch b starts
+ * idx[b,p] = n; 0 for a point never gathered; every element is written.
+ * For a point gathered at most 256 times the sum is deterministic: with
+ * P <= 32768 and N <= 4096 the batch's entries sorted by (n, p) are cut
+ * into pieces at every 32nd position, each piece is summed from +0 in
+ * increasing p and a point's pieces are added in order (so that every lane
+ * of the kernel sums 32 entries however long the lists are); otherwise
+ * the terms are added in increasing p.  A point gathered more often sums
+ * in an unspecified order.  grad_out channel c of batch b starts
  * at grad_out + b*grad_batch_stride + c*P (grad_batch_stride >= C*P, so a
  * channel slice of a larger tensor can be passed).  `workspace` holds
  * pointops_group_points_backward_workspace_bytes(B, C, N, P) bytes (the

@@ -15,7 +15,8 @@
 // A bucket of more than OMAX entries keeps the scatter's order instead (the
 // count costs O(L^2)).  Entries go from their final place straight to
 // memory.  Keys outside [0, num_keys) are dropped, or clamped into it with
-// CLAMP; with W the entries' weights travel with their ids.
+// CLAMP; with W the entries' weights travel with their ids; with key_out
+// non-null each list position also gets its key (num_keys <= 65536).
 #pragma once
 
 #include "pointops_common.hpp"
@@ -47,7 +48,8 @@ __device__ __forceinline__ void csr_sort_class(const I* __restrict__ keys,
                                                int num_entries, int num_keys, int r, int R,
                                                int* __restrict__ start,
                                                uint16_t* __restrict__ list_out,
-                                               float* __restrict__ weight_out) {
+                                               float* __restrict__ weight_out,
+                                               uint16_t* __restrict__ key_out = nullptr) {
     constexpr int EPT = MAXE / T;  // entries per thread
     constexpr int KPT = MAXK / T;  // keys per thread in the scan
     constexpr int NW = T / kWave;
@@ -143,6 +145,7 @@ __device__ __forceinline__ void csr_sort_class(const I* __restrict__ keys,
         if (p1 - p0 > kCsrSmall && p1 - p0 <= OMAX) continue;
         const int at = p1 - p0 <= kCsrSmall ? p0 + csr_rank(list, p0, p1, e) : (em[k] & 0xFFFF);
         list_out[at] = static_cast<uint16_t>(e);
+        if (key_out != nullptr) key_out[at] = static_cast<uint16_t>(m);
         if constexpr (W) weight_out[at] = ew[k];
     }
     __syncthreads();  // the long-bucket list is complete
@@ -156,6 +159,7 @@ __device__ __forceinline__ void csr_sort_class(const I* __restrict__ keys,
                 const int e = list[q];
                 const int at = p0 + csr_rank(list, p0, p1, e);
                 list_out[at] = static_cast<uint16_t>(e);
+                if (key_out != nullptr) key_out[at] = static_cast<uint16_t>(m);
                 if constexpr (W) weight_out[at] = weights[e];
             }
         }

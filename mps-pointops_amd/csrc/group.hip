@@ -262,22 +262,32 @@ __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
 // workgroups, each owning the points of one residue class) sorts the
 // entries p by their point idx[b,p] (csr_sort_class: ascending p within a
 // point's list of up to 256, the scatter's order beyond);
-// group_csr_grad_kernel (one workgroup per (channel, batch)) stages the
-// channel's grad_out row of P floats in LDS with coalesced loads, and
-// thread n sums row[p] over its point's list in order (ids from L2, the
-// first kGroupCsrFirst requested with the row), writing each element of
-// grad_features once.  No transpose, no
-// atomics on the gradients.
+// group_csr_grad_kernel (a few workgroups per batch, each taking every
+// J-th channel): thread t owns positions [32 t, 32 t + 32) of the batch's
+// CSR list -- the same amount of work in every lane, however long the
+// lists are -- with their ids and point indices in registers for all
+// channels.  A channel's grad_out row of P floats is staged in LDS (the
+// next row requested into registers meanwhile); each thread sums the
+// pieces of lists inside its range in list order, and a list that crosses
+// ranges is summed piece by piece: its first piece by the thread where it
+// starts, which then adds the following threads' pieces in order.  So a
+// point's gradient is the sum of its entries in ascending p, cut into
+// pieces at every 32nd list position of the batch, each piece summed from
+// +0 in order and the pieces added in order.  The results go through LDS
+// to coalesced stores; every element of grad_features is written once.
+// No transpose, no atomics on the gradients.
 constexpr int kGroupCsrThreads = 1024;
 constexpr int kGroupCsrMaxP = 32768;
 constexpr int kGroupCsrMaxN = 4096;
-constexpr int kGroupCsrRanges = 8;  // build workgroups per batch at most
-constexpr int kGroupCsrFirst = 8;   // list entries per point requested ahead
-constexpr int kGroupCsrTail = 8;    // further entries requested at once (32: slower)
+constexpr int kGroupCsrRanges = 8;       // build workgroups per batch at most
+constexpr int kGroupCsrSorted = 256;     // lists up to this long are in ascending p
+constexpr int kGroupGradThreads = 1024;  // the gather's workgroup
+constexpr int kGroupCsrPiece = kGroupCsrMaxP / kGroupGradThreads;  // list positions per thread
 
 struct GroupCsr {
     int* start;      // [B][sstride]: list starts, N + 1 used
     uint16_t* list;  // [B][lstride]: entries p by point
+    uint16_t* key;   // [B][lstride]: the point of each list position
     int64_t sstride, lstride;
 };
 
@@ -285,13 +295,15 @@ __host__ __device__ inline size_t group_csr_bytes(int64_t B, int64_t N, int64_t 
                                                   char* base) {
     const int64_t ss = (N + 1 + 63) & ~int64_t(63), ls = (P + 63) & ~int64_t(63);
     const size_t start_bytes = group_align(static_cast<size_t>(B * ss) * sizeof(int));
+    const size_t list_bytes = group_align(static_cast<size_t>(B * ls) * sizeof(uint16_t));
     if (out != nullptr) {
         out->start = reinterpret_cast<int*>(base);
         out->list = reinterpret_cast<uint16_t*>(base + start_bytes);
+        out->key = reinterpret_cast<uint16_t*>(base + start_bytes + list_bytes);
         out->sstride = ss;
         out->lstride = ls;
     }
-    return start_bytes + group_align(static_cast<size_t>(B * ls) * sizeof(uint16_t));
+    return start_bytes + 2 * list_bytes;
 }
 
 __host__ __device__ inline bool group_csr_fits(int64_t N, int64_t P) {
@@ -303,70 +315,177 @@ __global__ __launch_bounds__(kGroupCsrThreads) void group_csr_kernel(const I* __
                                                                      GroupCsr csr, int N, int P) {
     const int64_t b = blockIdx.x;
     // Indices outside [0, N) are clamped, as the forward gathers them.
-    csr_sort_class<kGroupCsrThreads, kGroupCsrMaxP, kGroupCsrMaxN, 256, I, false, true>(
+    csr_sort_class<kGroupCsrThreads, kGroupCsrMaxP, kGroupCsrMaxN, kGroupCsrSorted, I, false, true>(
         idx + b * P, nullptr, P, N, static_cast<int>(blockIdx.y), static_cast<int>(gridDim.y),
-        csr.start + b * csr.sstride, csr.list + b * csr.lstride, nullptr);
+        csr.start + b * csr.sstride, csr.list + b * csr.lstride, nullptr,
+        csr.key + b * csr.lstride);
 }
 
-__global__ __launch_bounds__(kGroupCsrThreads) void group_csr_grad_kernel(
+template <bool VEC>
+__global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
     const float* __restrict__ g, int64_t g_batch, GroupCsr csr, float* __restrict__ gf, int64_t C,
-    int N, int P) {
-    constexpr int T = kGroupCsrThreads;
-    constexpr int NPT = kGroupCsrMaxN / T;  // points per thread
-    constexpr int F = kGroupCsrFirst;
-    constexpr int TB = kGroupCsrTail;
-    extern __shared__ float row[];  // [P]
-    const int64_t c = blockIdx.x, b = blockIdx.y;
+    int N, int P, uint32_t J) {
+    constexpr int T = kGroupGradThreads;
+    constexpr int E = kGroupCsrPiece;       // list positions per thread
+    constexpr int NPT = kGroupCsrMaxN / T;  // output points per thread
+    constexpr int V = kGroupCsrMaxP / T;    // row floats per thread
+    static_assert(E % 8 == 0 && V % 4 == 0 && E <= 64, "whole 16-byte loads, one mask");
+    extern __shared__ __align__(16) unsigned char group_lds[];
+    // LDS: the row [kGroupCsrMaxP], then the result slots: a channel's
+    // results [N], continuation pieces [T], head pieces [T], and a discard
+    // slot per thread [T].
+    float* const row = reinterpret_cast<float*>(group_lds);
+    float* const slots = row + kGroupCsrMaxP;
+    const int kCont = kGroupCsrMaxN, kHead = kCont + T, kTrash = kHead + T;
+    const CloudBlock cb = cloud_block(J);  // a 1-D launch of B J workgroups
+    const int64_t b = cb.b;
+    const int64_t j = cb.x;
     const int tid = threadIdx.x;
-    const int* st = csr.start + b * csr.sstride;
-    const uint16_t* ls = csr.list + b * csr.lstride;
-    // This thread's points n = tid + i*T: list bounds, then the first F
-    // entries of each (an empty list reads entry 0, not added), all in
-    // flight with the row's loads.
-    int pb[NPT], pe[NPT];
+    const int64_t own = j < C ? (C - 1 - j) / J + 1 : 0;  // channels j, j + J, ...
+    const float* gb = g + b * g_batch;
+    // A channel's row, read from inside it (chunks past P read the last
+    // one again: row slots at or past P are stored but never read).
+    auto fetch = [&](int64_t s, float (&r)[V]) {
+        const float* src = gb + (j + s * J) * P;
+        if constexpr (VEC) {
 #pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-        const int n = tid + i * T;
-        pb[i] = n < N ? st[n] : 0;
-        pe[i] = n < N ? st[n + 1] : 0;
-    }
-    const float* src = g + b * g_batch + c * P;
-    for (int base = 0; base < P; base += 8 * T) {
-        float v[8];
-#pragma unroll
-        for (int u = 0; u < 8; ++u) v[u] = src[min(base + u * T + tid, P - 1)];
-#pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (base + u * T + tid < P) row[base + u * T + tid] = v[u];
-    }
-    int e0[NPT][F];
-#pragma unroll
-    for (int i = 0; i < NPT; ++i)
-#pragma unroll
-        for (int u = 0; u < F; ++u) e0[i][u] = ls[pe[i] > pb[i] ? min(pb[i] + u, pe[i] - 1) : 0];
-    __syncthreads();
-#pragma unroll
-    for (int i = 0; i < NPT; ++i) {
-        const int n = tid + i * T;
-        if (n >= N) break;
-        float acc = 0.f;
-#pragma unroll
-        for (int u = 0; u < F; ++u) {
-            const float t = row[e0[i][u]];
-            acc = pb[i] + u < pe[i] ? acc + t : acc;
-        }
-        // The rest of a long list: TB ids requested at once from L2.
-        for (int q = pb[i] + F; q < pe[i]; q += TB) {
-            int e[TB];
-#pragma unroll
-            for (int u = 0; u < TB; ++u) e[u] = ls[min(q + u, pe[i] - 1)];
-#pragma unroll
-            for (int u = 0; u < TB; ++u) {
-                const float t = row[e[u]];
-                acc = q + u < pe[i] ? acc + t : acc;
+            for (int u = 0; u < V / 4; ++u) {
+                const float4 v =
+                    *reinterpret_cast<const float4*>(src + min(4 * (u * T + tid), P - 4));
+                r[4 * u] = v.x;
+                r[4 * u + 1] = v.y;
+                r[4 * u + 2] = v.z;
+                r[4 * u + 3] = v.w;
             }
         }
-        gf[(b * C + c) * N + n] = acc;
+    };
+    float rv[V];
+    if (VEC && own > 0) fetch(0, rv);  // unaligned rows are read when needed instead
+    // This thread's list positions q0 .. q0 + qn - 1: ids and points
+    // (16-bit, two per register; id 0 past the end), the point just before
+    // q0 and the one just after my range.
+    const int q0 = tid * E;
+    const int qn = max(0, min(E, P - q0));
+    const int64_t lbase = b * csr.lstride + (q0 < P ? q0 : 0);  // lstride: whole 64-id blocks
+    uint32_t ids[E / 2], pts[E / 2];
+#pragma unroll
+    for (int u = 0; u < E / 8; ++u) {
+        const uint4 v = *reinterpret_cast<const uint4*>(csr.list + lbase + 8 * u);
+        const uint4 k = *reinterpret_cast<const uint4*>(csr.key + lbase + 8 * u);
+        ids[4 * u] = v.x;
+        ids[4 * u + 1] = v.y;
+        ids[4 * u + 2] = v.z;
+        ids[4 * u + 3] = v.w;
+        pts[4 * u] = k.x;
+        pts[4 * u + 1] = k.y;
+        pts[4 * u + 2] = k.z;
+        pts[4 * u + 3] = k.w;
+    }
+    const int before = q0 > 0 && q0 < P ? csr.key[b * csr.lstride + q0 - 1] : -1;
+    const int after = q0 + qn < P ? csr.key[b * csr.lstride + q0 + qn] : -1;
+    auto half = [](const uint32_t (&a)[E / 2], int u) {
+        return static_cast<int>((u & 1) ? a[u >> 1] >> 16 : a[u >> 1] & 0xFFFFu);
+    };
+#pragma unroll
+    for (int u = 0; u < E; ++u)  // positions past the end read row[0]
+        if (u >= qn) ids[u >> 1] &= (u & 1) ? 0x0000FFFFu : 0xFFFF0000u;
+    // Per position: does a piece start here (bit u of `fresh`), and where
+    // does the running sum go after it (dest, a slot index, two per
+    // register): the point's result slot where the point's list ends inside
+    // my range and began inside it, my continuation slot where my first
+    // piece (of a list begun before q0) ends, my head slot where my last
+    // piece (of a list going on past my range) ends, else my discard slot.
+    uint64_t fresh = 0;
+    uint32_t dest[E / 2];
+    int head_n = -1;  // the list my head piece begins (-1: none)
+    {
+        const int first_n = qn > 0 ? half(pts, 0) : -1;
+        const bool cont = qn > 0 && before == first_n;
+#pragma unroll
+        for (int u = 0; u < E; ++u) {
+            const int n = half(pts, u);
+            const int nn = u + 1 < qn ? half(pts, u + 1) : after;
+            if (u < qn && (u == 0 || n != half(pts, u - 1))) fresh |= uint64_t(1) << u;
+            const bool mine_first = cont && n == first_n;  // a list begun before q0
+            int d = kTrash + tid;
+            if (u < qn && n != nn) {  // the list ends here
+                d = mine_first ? kCont + tid : n;
+            } else if (u + 1 == qn) {  // the list goes on past my range
+                if (mine_first) {
+                    d = kCont + tid;  // a middle piece
+                } else {
+                    d = kHead + tid;
+                    head_n = n;
+                }
+            }
+            if (u & 1) dest[u >> 1] |= static_cast<uint32_t>(d) << 16;
+            else dest[u >> 1] = static_cast<uint32_t>(d);
+        }
+    }
+    // Following threads whose first pieces finish my head's list.
+    const int head_span =
+        head_n >= 0 ? (csr.start[b * csr.sstride + head_n + 1] - (q0 + qn) + E - 1) / E : 0;
+    // Every result slot starts at 0: a point with an empty list keeps it,
+    // the others are rewritten in every channel.
+#pragma unroll
+    for (int i = 0; i < NPT; ++i) {
+        const int n = tid + i * T;
+        if (n < N) slots[n] = 0.f;
+    }
+    for (int64_t s = 0; s < own; ++s) {
+        __syncthreads();  // previous channel: row and results read
+        if constexpr (VEC) {
+#pragma unroll
+            for (int u = 0; u < V / 4; ++u)
+                *reinterpret_cast<float4*>(row + 4 * (u * T + tid)) =
+                    make_float4(rv[4 * u], rv[4 * u + 1], rv[4 * u + 2], rv[4 * u + 3]);
+        } else {
+            const float* src = gb + (j + s * J) * P;
+            for (int at = tid; at < P; at += T) row[at] = src[at];
+        }
+        __syncthreads();  // row complete
+        if (VEC && s + 1 < own) fetch(s + 1, rv);
+        // The running sum in position order, restarted from +0 where a piece
+        // starts, stored after every position to that position's slot.
+        // Keeps the unpacked ids and slots from being hoisted out of the
+        // channel loop (twice the registers of the packed ones).
+#pragma unroll
+        for (int u = 0; u < E / 2; ++u) asm volatile("" : "+v"(ids[u]), "+v"(dest[u]));
+        float acc = 0.f;
+#pragma unroll
+        for (int u8 = 0; u8 < E; u8 += 8) {
+            float v[8];
+#pragma unroll
+            for (int u = u8; u < u8 + 8; ++u)
+                v[u - u8] = row[(u & 1) ? ids[u >> 1] >> 16 : ids[u >> 1] & 0xFFFFu];
+#pragma unroll
+            for (int u = u8; u < u8 + 8; ++u) {
+                acc = ((fresh >> u) & 1u ? 0.f : acc) + v[u - u8];  // +0 + x: a piece's first term
+                slots[(u & 1) ? dest[u >> 1] >> 16 : dest[u >> 1] & 0xFFFFu] = acc;
+            }
+            __builtin_amdgcn_sched_barrier(0);  // eight positions at a time: few live values
+        }
+        __syncthreads();  // pieces complete
+        if (head_span > 0) {
+            // The following threads' pieces, eight reads in flight at a time
+            // (past the span: the last piece again, not added).
+            float v = slots[kHead + tid];
+            for (int k0 = 1; k0 <= head_span; k0 += 8) {
+                float w[8];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) w[k] = slots[kCont + tid + min(k0 + k, head_span)];
+#pragma unroll
+                for (int k = 0; k < 8; ++k) v = k0 + k <= head_span ? v + w[k] : v;
+            }
+            slots[head_n] = v;
+        }
+        __syncthreads();  // results complete
+        const int64_t c = j + s * J;
+#pragma unroll
+        for (int i = 0; i < NPT; ++i) {
+            const int n = tid + i * T;
+            if (n < N) gf[(b * C + c) * N + n] = slots[n];
+        }
     }
 }
 
@@ -549,10 +668,21 @@ hipError_t pointops_group_points_backward(const float* grad_out, int64_t grad_ba
                                static_cast<const int64_t*>(idx), csr, n, p);
         const hipError_t err = hipGetLastError();
         if (err != hipSuccess) return err;
-        hipLaunchKernelGGL(group_csr_grad_kernel,
-                           dim3(static_cast<uint32_t>(C), static_cast<uint32_t>(B)),
-                           dim3(kGroupCsrThreads), static_cast<size_t>(P) * sizeof(float), stream,
-                           grad_out, grad_batch_stride, csr, grad_features, C, n, p);
+        // J workgroups per batch (every J-th channel each), enough to cover
+        // the CUs; LDS: a row and the result slots.
+        const int64_t J = std::min<int64_t>(C, std::max<int64_t>(1, (256 + B - 1) / B));
+        const size_t lds =
+            (kGroupCsrMaxP + kGroupCsrMaxN + 1 + 3 * kGroupGradThreads) * sizeof(float);
+        const dim3 ggrid(static_cast<uint32_t>(B * J));
+        const uint32_t uj = static_cast<uint32_t>(J);
+        const bool vec = P % 4 == 0 && grad_batch_stride % 4 == 0 &&
+                         reinterpret_cast<uintptr_t>(grad_out) % 16 == 0;
+        if (vec)
+            hipLaunchKernelGGL(group_csr_grad_kernel<true>, ggrid, dim3(kGroupGradThreads), lds,
+                               stream, grad_out, grad_batch_stride, csr, grad_features, C, n, p, uj);
+        else
+            hipLaunchKernelGGL(group_csr_grad_kernel<false>, ggrid, dim3(kGroupGradThreads), lds,
+                               stream, grad_out, grad_batch_stride, csr, grad_features, C, n, p, uj);
         return hipGetLastError();
     }
     dim3 pgrid, ngrid;

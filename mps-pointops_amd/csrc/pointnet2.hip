@@ -622,6 +622,146 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kerne
     }
 }
 
+// three_interp_csr_gather_kernel, the gather for M <= kTiCsrThreads known
+// points (thread m owns known point m): J workgroups per batch, each taking
+// every J-th group of 4 channels.  The batch's CSR is staged in LDS once
+// (the unknown index n = e / 3 of each entry, its weight, the starts) and
+// thread m keeps its first kTiRegEntries entries in registers; the 4 rows of
+// a channel group pass through one [N][4] LDS buffer (channels
+// interleaved, so one 16-byte read serves an entry's 4 channels), each
+// group's rows requested two groups ahead into registers.  Per channel the
+// sum is the sequential loop's: fl32(row * w) added in list order.
+constexpr int kTiRegEntries = 16;
+
+__global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_gather_kernel(
+    const float* __restrict__ grad_out, TiCsr csr, float* __restrict__ grad_features, int64_t C,
+    int M, int N, uint32_t J) {
+    constexpr int T = kTiCsrThreads;
+    constexpr int R = kTiRegEntries;
+    extern __shared__ float4 lds4[];
+    float4* const rows = lds4;                                  // [N]: 4 channels each
+    float* const wl = reinterpret_cast<float*>(lds4 + N);      // [3N] weights
+    uint16_t* const nl = reinterpret_cast<uint16_t*>(wl + 3 * N);  // [3N] unknown index
+    int* const st = reinterpret_cast<int*>(nl + ((3 * N + 1) & ~1));  // [M + 1]
+    const CloudBlock cb = cloud_block(J);  // a 1-D launch of B J workgroups
+    const int64_t b = cb.b;
+    const int64_t j = cb.x;
+    const int tid = threadIdx.x;
+    const int64_t groups = (C + 3) / 4;
+    const int64_t own = j < groups ? (groups - 1 - j) / J + 1 : 0;  // groups j, j + J, ...
+    // A group's rows, thread tid holding unknowns n = tid + k T (k < NK) of
+    // its 4 channels, so that the LDS stores below (one 16-byte [n][4]
+    // entry per lane) go to consecutive addresses.  Every lane loads from
+    // inside the batch (row and unknown clamped); what lies outside is
+    // replaced by zeros afterwards.
+    constexpr int NK = kTiCsrMaxN / T;
+    auto fetch = [&](int64_t s, float4 (&r)[NK]) {
+        const int64_t c0 = 4 * (j + s * J);
+        float v[4][NK];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+            const float* src = grad_out + (b * C + min(c0 + cc, C - 1)) * N;
+#pragma unroll
+            for (int k = 0; k < NK; ++k) v[cc][k] = src[min(tid + k * T, N - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < NK; ++k) {
+            r[k] = make_float4(c0 < C ? v[0][k] : 0.f, c0 + 1 < C ? v[1][k] : 0.f,
+                               c0 + 2 < C ? v[2][k] : 0.f, c0 + 3 < C ? v[3][k] : 0.f);
+        }
+    };
+    float4 ra[NK], rb[NK];
+    if (own > 0) fetch(0, ra);
+    if (own > 1) fetch(1, rb);
+    // The batch's CSR into LDS, every load issued before the first store.
+    {
+        constexpr int U = (3 * kTiCsrMaxN + T - 1) / T;  // entries per thread at most
+        constexpr int US = (kTiCsrThreads + 1 + T - 1) / T;  // starts per thread at most
+        const uint16_t* lsrc = csr.list + b * csr.lstride;
+        const float* wsrc = csr.weight + b * csr.wstride;
+        const int* ssrc = csr.start + b * csr.sstride;
+        uint32_t lv[U];
+        float wv[U];
+        int sv[US];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = min(tid + u * T, 3 * N - 1);
+            lv[u] = lsrc[q];
+            wv[u] = wsrc[q];
+        }
+#pragma unroll
+        for (int u = 0; u < US; ++u) sv[u] = ssrc[min(tid + u * T, M)];
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int q = tid + u * T;
+            if (q < 3 * N) {
+                nl[q] = static_cast<uint16_t>(lv[u] / 3);
+                wl[q] = wv[u];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < US; ++u)
+            if (tid + u * T <= M) st[tid + u * T] = sv[u];
+    }
+    __syncthreads();
+    const bool mine = tid < M;
+    const int pb = mine ? st[tid] : 0, pe = mine ? st[tid + 1] : 0;
+    int en[R];
+    float ew[R];
+#pragma unroll
+    for (int k = 0; k < R; ++k) {
+        const int q = min(pb + k, max(pe - 1, pb));  // an unused slot repeats a valid one
+        en[k] = pe > pb ? nl[q] : 0;
+        ew[k] = pe > pb ? wl[q] : 0.f;
+    }
+    for (int64_t s = 0; s < own; ++s) {
+        __syncthreads();  // every thread is done with the previous group's rows
+#pragma unroll
+        for (int k = 0; k < NK; ++k)
+            if (tid + k * T < N) rows[tid + k * T] = ra[k];
+#pragma unroll
+        for (int k = 0; k < NK; ++k) ra[k] = rb[k];
+        __syncthreads();
+        if (s + 2 < own) fetch(s + 2, rb);
+        if (!mine) continue;
+        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+        auto add = [&](const float4 v, float w, bool ok) {
+            const float t0 = v.x * w, t1 = v.y * w, t2 = v.z * w, t3 = v.w * w;
+            a0 = ok ? a0 + t0 : a0;
+            a1 = ok ? a1 + t1 : a1;
+            a2 = ok ? a2 + t2 : a2;
+            a3 = ok ? a3 + t3 : a3;
+        };
+#pragma unroll
+        for (int k = 0; k < R; ++k) add(rows[en[k]], ew[k], pb + k < pe);
+        // The rest of a long list: four entries' reads at once (past the
+        // end: the last entry again, not added), added in order.
+        for (int p = pb + R; p < pe; p += 4) {
+            float4 v[4];
+            float w[4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int q = min(p + u, pe - 1);
+                v[u] = rows[nl[q]];
+                w[u] = wl[q];
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u) add(v[u], w[u], p + u < pe);
+        }
+        const int64_t c0 = 4 * (j + s * J);
+        float* o = grad_features + (b * C + c0) * M + tid;
+        o[0] = a0;
+        if (c0 + 1 < C) o[M] = a1;
+        if (c0 + 2 < C) o[2 * static_cast<int64_t>(M)] = a2;
+        if (c0 + 3 < C) o[3 * static_cast<int64_t>(M)] = a3;
+    }
+}
+
+__host__ __device__ inline size_t csr_gather_lds_bytes(int64_t M, int64_t N) {
+    return static_cast<size_t>(16 * N + 4 * 3 * N + 2 * ((3 * N + 1) & ~int64_t(1)) + 4 * (M + 1));
+}
+
 // Channels per step of the CSR gather: the largest CG in {4, 2, 1} whose
 // LDS fits the budget (0: none).
 int csr_channel_group(int64_t M, int64_t N) {
@@ -713,20 +853,14 @@ size_t pointops_three_interpolate_backward_workspace_bytes(int64_t B, int64_t M,
     return ti_csr_bytes(B, M, N, nullptr, nullptr);
 }
 
-hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const int32_t* idx,
-                                                   const float* weights, float* grad_features,
-                                                   void* workspace, int64_t B, int64_t C, int64_t M,
-                                                   int64_t N, hipStream_t stream) {
-    if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
-    if (B == 0 || C == 0 || M == 0) return hipSuccess;
-    // grad_out rows are staged with 16-byte loads: N % 4 == 0, 16-byte aligned.
+hipError_t pointops_three_interpolate_csr_build(const int32_t* idx, const float* weights,
+                                               void* workspace, int64_t B, int64_t M, int64_t N,
+                                               hipStream_t stream) {
+    if (B < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
+    if (B == 0 || M == 0) return hipSuccess;
     if (N == 0 || M > kTiCsrMaxM || N > kTiCsrMaxN || N % 4 != 0 || workspace == nullptr ||
-        B > 65535 || (C + kTiCsrBlock - 1) / kTiCsrBlock > INT32_MAX ||
-        reinterpret_cast<uintptr_t>(grad_out) % 16 != 0 ||
-        reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        B > 65535 || reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
         return hipErrorInvalidValue;
-    const int cg = csr_channel_group(M, N);
-    if (cg == 0) return hipErrorInvalidValue;
     TiCsr csr;
     ti_csr_bytes(B, M, N, &csr, static_cast<char*>(workspace));
     // Workgroups per batch (a power of two, each owning the known indices of
@@ -736,27 +870,73 @@ hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const 
     hipLaunchKernelGGL(three_interp_csr_kernel, dim3(static_cast<uint32_t>(B), static_cast<uint32_t>(ranges)),
                        dim3(kTiCsrThreads), 0, stream, idx, weights, csr, static_cast<int>(M),
                        static_cast<int>(N));
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
+    return hipGetLastError();
+}
+
+hipError_t pointops_three_interpolate_backward_from_csr(const float* grad_out,
+                                                        const void* workspace,
+                                                        float* grad_features, int64_t B,
+                                                        int64_t C, int64_t M, int64_t N,
+                                                        hipStream_t stream) {
+    if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
+    if (B == 0 || C == 0 || M == 0) return hipSuccess;
+    // grad_out rows are staged with 16-byte loads: N % 4 == 0, 16-byte aligned.
+    if (N == 0 || M > kTiCsrMaxM || N > kTiCsrMaxN || N % 4 != 0 || workspace == nullptr ||
+        B > 65535 || (C + kTiCsrBlock - 1) / kTiCsrBlock > INT32_MAX ||
+        reinterpret_cast<uintptr_t>(grad_out) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
+        return hipErrorInvalidValue;
+    TiCsr csr;
+    ti_csr_bytes(B, M, N, &csr, static_cast<char*>(const_cast<void*>(workspace)));
+    const int m = static_cast<int>(M), n = static_cast<int>(N);
+    if (M <= kTiCsrThreads) {
+        // J workgroups per batch, enough to cover the CUs.
+        const int64_t groups = (C + 3) / 4;
+        const int64_t J = std::min<int64_t>(groups, std::max<int64_t>(1, (256 + B - 1) / B));
+        if (B * J <= INT32_MAX) {
+            hipLaunchKernelGGL(three_interp_csr_gather_kernel, dim3(static_cast<uint32_t>(B * J)),
+                               dim3(kTiCsrThreads), csr_gather_lds_bytes(M, N), stream, grad_out,
+                               csr, grad_features, C, m, n, static_cast<uint32_t>(J));
+            return hipGetLastError();
+        }
+    }
+    const int cg = csr_channel_group(M, N);
+    if (cg == 0) return hipErrorInvalidValue;
     const size_t shmem = static_cast<size_t>(csr_lds_bytes(cg, M, N));
     const dim3 grid(static_cast<uint32_t>((C + kTiCsrBlock - 1) / kTiCsrBlock),
                     static_cast<uint32_t>(B));
-    const int m = static_cast<int>(M), n = static_cast<int>(N);
     switch (cg) {
         case 4:
             hipLaunchKernelGGL((three_interp_backward_csr_kernel<4>), grid, dim3(kTiCsrThreads), shmem,
-                               stream, grad_out, weights, csr, grad_features, C, m, n);
+                               stream, grad_out, nullptr, csr, grad_features, C, m, n);
             break;
         case 2:
             hipLaunchKernelGGL((three_interp_backward_csr_kernel<2>), grid, dim3(kTiCsrThreads), shmem,
-                               stream, grad_out, weights, csr, grad_features, C, m, n);
+                               stream, grad_out, nullptr, csr, grad_features, C, m, n);
             break;
         default:
             hipLaunchKernelGGL((three_interp_backward_csr_kernel<1>), grid, dim3(kTiCsrThreads), shmem,
-                               stream, grad_out, weights, csr, grad_features, C, m, n);
-            break;
+                               stream, grad_out, nullptr, csr, grad_features, C, m, n);
     }
     return hipGetLastError();
+}
+
+hipError_t pointops_three_interpolate_backward_csr(const float* grad_out, const int32_t* idx,
+                                                   const float* weights, float* grad_features,
+                                                   void* workspace, int64_t B, int64_t C, int64_t M,
+                                                   int64_t N, hipStream_t stream) {
+    if (B < 0 || C < 0 || M < 0 || N < 0) return hipErrorInvalidValue;
+    if (B == 0 || C == 0 || M == 0) return hipSuccess;
+    if (N == 0 || M > kTiCsrMaxM || N > kTiCsrMaxN || N % 4 != 0 || workspace == nullptr ||
+        B > 65535 || (C + kTiCsrBlock - 1) / kTiCsrBlock > INT32_MAX ||
+        reinterpret_cast<uintptr_t>(grad_out) % 16 != 0 ||
+        reinterpret_cast<uintptr_t>(workspace) % 256 != 0 || csr_channel_group(M, N) == 0)
+        return hipErrorInvalidValue;
+    const hipError_t err =
+        pointops_three_interpolate_csr_build(idx, weights, workspace, B, M, N, stream);
+    if (err != hipSuccess) return err;
+    return pointops_three_interpolate_backward_from_csr(grad_out, workspace, grad_features, B, C,
+                                                        M, N, stream);
 }
 
 hipError_t pointops_three_interpolate_backward(const float* grad_out, const int32_t* idx,

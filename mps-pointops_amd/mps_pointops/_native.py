@@ -51,6 +51,8 @@ _SIGNATURES: dict[str, list] = {
     "pointops_three_interpolate_backward": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_three_interpolate_backward_csr": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
                                                 _vp],
+    "pointops_three_interpolate_csr_build": [_vp, _vp, _vp, _i64, _i64, _i64, _vp],
+    "pointops_three_interpolate_backward_from_csr": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_ball_query_pn2_f32": [_vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_ball_query_grid_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_ball_query_auto_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],

@@ -92,6 +92,12 @@ def _validate_interpolate(features: Tensor, indices: Tensor, weights: Tensor):
     return batch, channels, points, queries
 
 
+def _csr_eligible(points: int, queries: int, batch: int) -> bool:
+    """Shapes the CSR backward serves (pointops_three_interpolate_backward_csr)."""
+    return (0 < points <= _CSR_MAX_KNOWN and 0 < queries <= _CSR_MAX_UNKNOWN
+            and queries % 4 == 0 and batch <= 65535)
+
+
 class _ThreeInterpolate(torch.autograd.Function):
     """Native forward and backward; zero weight gradient
     (pointnet2.py:150-188)."""
@@ -102,13 +108,24 @@ class _ThreeInterpolate(torch.autograd.Function):
         queries = indices.shape[1]
         output = torch.empty((batch, channels, queries), dtype=torch.float32,
                              device=features.device)
+        stream = _native.stream(features.device)
         if output.numel():
             _native.call("pointops_three_interpolate", features.contiguous().data_ptr(),
                          indices.data_ptr(), weights.data_ptr(), output.data_ptr(),
-                         batch, channels, points, queries, _native.stream(features.device))
+                         batch, channels, points, queries, stream)
         ctx.save_for_backward(indices, weights)
         ctx.points = points
         ctx.channels = channels
+        # The backward's CSR of the entries depends only on the indices and
+        # weights: built here, behind the forward on the same stream, so the
+        # backward only gathers.
+        ctx.csr = None
+        if ctx.needs_input_grad[0] and batch * channels and _csr_eligible(points, queries, batch):
+            size = _native.size_query("pointops_three_interpolate_backward_workspace_bytes",
+                                      batch, points, queries)
+            ctx.csr = torch.empty(size, dtype=torch.uint8, device=features.device)
+            _native.call("pointops_three_interpolate_csr_build", indices.data_ptr(),
+                         weights.data_ptr(), ctx.csr.data_ptr(), batch, points, queries, stream)
         return output
 
     @staticmethod
@@ -122,20 +139,15 @@ class _ThreeInterpolate(torch.autograd.Function):
         if ctx.needs_input_grad[0]:
             shape = (batch, ctx.channels, ctx.points)
             stream = _native.stream(indices.device)
-            if (0 < ctx.points <= _CSR_MAX_KNOWN and 0 < queries <= _CSR_MAX_UNKNOWN
-                    and queries % 4 == 0 and batch <= 65535):
-                # Deterministic gather over a CSR of the entries; writes every
-                # element, so no zero fill.
+            if _csr_eligible(ctx.points, queries, batch):
+                # Deterministic gather over the CSR the forward built; writes
+                # every element, so no zero fill.
                 grad_features = torch.empty(shape, device=indices.device, dtype=torch.float32)
                 if batch * ctx.channels:
-                    size = _native.size_query("pointops_three_interpolate_backward_workspace_bytes",
-                                              batch, ctx.points, queries)
-                    workspace = torch.empty(size, dtype=torch.uint8, device=indices.device)
-                    _native.call("pointops_three_interpolate_backward_csr",
-                                 grad_output.contiguous().data_ptr(), indices.data_ptr(),
-                                 weights.data_ptr(), grad_features.data_ptr(),
-                                 workspace.data_ptr(), batch, ctx.channels, ctx.points, queries,
-                                 stream)
+                    _native.call("pointops_three_interpolate_backward_from_csr",
+                                 grad_output.contiguous().data_ptr(), ctx.csr.data_ptr(),
+                                 grad_features.data_ptr(), batch, ctx.channels, ctx.points,
+                                 queries, stream)
             else:
                 grad_features = torch.zeros(shape, device=indices.device, dtype=torch.float32)
                 if batch * ctx.channels * queries:

@@ -100,8 +100,9 @@ def test_csr_backward_rejects_out_of_range(cuda_device):
 
 
 def test_public_backward_uses_csr_path(cuda_device, monkeypatch):
-    """three_interpolate's autograd backward takes the CSR entry point for
-    config 2's shape and gives the sequential-loop gradient."""
+    """three_interpolate's autograd forward builds the CSR for config 2's
+    shape and its backward gathers over it, giving the sequential-loop
+    gradient."""
     from mps_pointops import _native, three_interpolate
 
     calls = []
@@ -113,7 +114,18 @@ def test_public_backward_uses_csr_path(cuda_device, monkeypatch):
     w = torch.rand(B, N, 3, generator=g)
     up = torch.randn(B, C, N, generator=g)
     f = torch.randn(B, C, M, generator=g).cuda().requires_grad_()
-    three_interpolate(f, idx.cuda(), w.cuda()).backward(up.cuda())
-    assert "pointops_three_interpolate_backward_csr" in calls
+    out = three_interpolate(f, idx.cuda(), w.cuda())
+    # The CSR is built right after the forward; the backward only gathers.
+    assert calls == ["pointops_three_interpolate", "pointops_three_interpolate_csr_build"]
+    out.backward(up.cuda(), retain_graph=True)
+    assert calls[2:] == ["pointops_three_interpolate_backward_from_csr"]
     want = sequential_f32(up.numpy(), idx.numpy(), w.numpy(), M)
     np.testing.assert_array_equal(host(f.grad).view(np.uint32), want.view(np.uint32))
+    # A second backward over the same graph reuses the CSR: the same bits again.
+    f.grad = None
+    out.backward(up.cuda())
+    np.testing.assert_array_equal(host(f.grad).view(np.uint32), want.view(np.uint32))
+    # Without a feature gradient no CSR is built.
+    calls.clear()
+    three_interpolate(f.detach(), idx.cuda(), w.cuda())
+    assert calls == ["pointops_three_interpolate"]
