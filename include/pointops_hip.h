@@ -267,9 +267,14 @@ hipError_t pointops_three_interpolate_backward(const float *grad_out, const int3
                                                const float *weights, float *grad_features,
                                                int64_t B, int64_t C, int64_t M, int64_t N,
                                                hipStream_t stream);
-/* The same gradient, always in (n, t) order (deterministic), for M <= 4096
- * known points and N <= 4096 unknowns with N % 4 == 0 (grad_out 16-byte
- * aligned), without atomics: a CSR of the entries by known index is built in
+/* The same gradient in a fixed order (deterministic), for M <= 4096 known
+ * points and N <= 4096 unknowns with N % 4 == 0 (grad_out 16-byte aligned),
+ * without atomics.  A known point's terms fl32(grad_out * w) are taken in
+ * (n, t) order; with M <= 1024 the batch's entries sorted by (known index,
+ * n, t) are cut into pieces at every 12th position, each piece summed from
+ * +0 in order and a point's pieces added in order (every lane of the kernel
+ * sums 12 entries however long the lists are); with more known points the
+ * terms are added one by one.  A CSR of the entries by known index is built in
  * `workspace` (256-byte aligned,
  * pointops_three_interpolate_backward_workspace_bytes(B, M, N) bytes, no
  * initialisation needed), then every element of grad_features is written

@@ -401,6 +401,7 @@ struct TiCsr {
     int* start;      // [B][sstride]: bucket starts, M+1 used
     float* weight;   // [B][wstride]: w[e] in list order, 3N used
     uint16_t* list;  // [B][lstride]: entry ids by known index, ascending, 3N used
+    uint16_t* key;   // [B][lstride]: the known index of each list position
     int sstride, wstride, lstride;
 };
 
@@ -411,15 +412,17 @@ __host__ __device__ inline size_t ti_csr_bytes(int64_t B, int64_t M, int64_t N, 
                   ls = (3 * N + 7) & ~int64_t(7);
     const size_t start_bytes = up(static_cast<size_t>(B * ss) * sizeof(int));
     const size_t weight_bytes = up(static_cast<size_t>(B * ws) * sizeof(float));
+    const size_t list_bytes = up(static_cast<size_t>(B * ls) * sizeof(uint16_t));
     if (out != nullptr) {
         out->start = reinterpret_cast<int*>(base);
         out->weight = reinterpret_cast<float*>(base + start_bytes);
         out->list = reinterpret_cast<uint16_t*>(base + start_bytes + weight_bytes);
+        out->key = reinterpret_cast<uint16_t*>(base + start_bytes + weight_bytes + list_bytes);
         out->sstride = static_cast<int>(ss);
         out->wstride = static_cast<int>(ws);
         out->lstride = static_cast<int>(ls);
     }
-    return start_bytes + weight_bytes + static_cast<size_t>(B * ls) * sizeof(uint16_t);
+    return start_bytes + weight_bytes + 2 * list_bytes;
 }
 
 __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
@@ -430,7 +433,7 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_kernel(
     csr_sort_class<kTiCsrThreads, kMaxE, kTiCsrMaxM, kMaxE, int32_t, true, false>(
         idx + b * 3 * N, weights + b * 3 * N, 3 * N, M, static_cast<int>(blockIdx.y),
         static_cast<int>(gridDim.y), csr.start + b * csr.sstride, csr.list + b * csr.lstride,
-        csr.weight + b * csr.wstride);
+        csr.weight + b * csr.wstride, csr.key + b * csr.lstride);
 }
 
 // Copies up to kTiCsrStage 16-byte chunks per thread from three consecutive
@@ -623,38 +626,116 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_backward_csr_kerne
 }
 
 // three_interp_csr_gather_kernel, the gather for M <= kTiCsrThreads known
-// points (thread m owns known point m): J workgroups per batch, each taking
-// every J-th group of 4 channels.  The batch's CSR is staged in LDS once
-// (the unknown index n = e / 3 of each entry, its weight, the starts) and
-// thread m keeps its first kTiRegEntries entries in registers; the 4 rows of
-// a channel group pass through one [N][4] LDS buffer (channels
-// interleaved, so one 16-byte read serves an entry's 4 channels), each
-// group's rows requested two groups ahead into registers.  Per channel the
-// sum is the sequential loop's: fl32(row * w) added in list order.
-constexpr int kTiRegEntries = 16;
+// points: J workgroups per batch, each taking every J-th group of 4
+// channels.  Thread t owns positions [12 t, 12 t + 12) of the batch's CSR
+// (kTiPiece = 3 * kTiCsrMaxN / kTiCsrThreads), the same work in every lane
+// however long the lists are, with each position's unknown index, weight
+// and slot in registers for all channel groups.  The 4 rows of a group pass
+// through one [N][4] LDS buffer (channels interleaved, so one 16-byte read
+// serves a position's 4 channels), each group's rows requested two groups
+// ahead into registers.  A thread sums the pieces of lists inside its
+// range in list order; a list that crosses ranges is summed piece by piece,
+// its first piece by the thread where it starts, which then adds the
+// following threads' pieces in order.  So a known point's gradient is the
+// sum of fl32(row * w) over its entries in (n, t) order, cut into pieces at
+// every 12th CSR position of the batch, each piece summed from +0 in order
+// and the pieces added in order.  The results go through LDS to coalesced
+// stores; every element of grad_features is written once.
+constexpr int kTiPiece = 3 * kTiCsrMaxN / kTiCsrThreads;
 
 __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_gather_kernel(
     const float* __restrict__ grad_out, TiCsr csr, float* __restrict__ grad_features, int64_t C,
     int M, int N, uint32_t J) {
     constexpr int T = kTiCsrThreads;
-    constexpr int R = kTiRegEntries;
+    constexpr int E = kTiPiece;
+    constexpr int NK = kTiCsrMaxN / T;  // unknowns per thread when staging rows
+    static_assert(E % 4 == 0 && E <= 32, "whole 8-byte id loads, one mask word");
     extern __shared__ float4 lds4[];
-    float4* const rows = lds4;                                  // [N]: 4 channels each
-    float* const wl = reinterpret_cast<float*>(lds4 + N);      // [3N] weights
-    uint16_t* const nl = reinterpret_cast<uint16_t*>(wl + 3 * N);  // [3N] unknown index
-    int* const st = reinterpret_cast<int*>(nl + ((3 * N + 1) & ~1));  // [M + 1]
+    // LDS: the rows [kTiCsrMaxN], then the slots: results [T] (M <= T),
+    // continuation pieces [T], head pieces [T], a discard slot per thread [T].
+    float4* const rows = lds4;
+    float4* const slots = lds4 + kTiCsrMaxN;
+    constexpr int kCont = T, kHead = 2 * T, kTrash = 3 * T;
     const CloudBlock cb = cloud_block(J);  // a 1-D launch of B J workgroups
     const int64_t b = cb.b;
     const int64_t j = cb.x;
     const int tid = threadIdx.x;
     const int64_t groups = (C + 3) / 4;
     const int64_t own = j < groups ? (groups - 1 - j) / J + 1 : 0;  // groups j, j + J, ...
+    // This thread's positions q0 .. q0 + qn - 1 (the batch's CSR holds the
+    // entries whose index lies in [0, M): start[M] of them).
+    const int* st = csr.start + b * csr.sstride;
+    const int total = st[M];
+    const int q0 = tid * E;
+    const int qn = max(0, min(E, total - q0));
+    const int base = q0 < total ? q0 : 0;  // 3N % 12 == 0: the loads stay inside the list
+    uint32_t ids[E / 2], pts[E / 2];
+    float w[E];
+    {
+        const uint2* lp = reinterpret_cast<const uint2*>(csr.list + b * csr.lstride + base);
+        const uint2* kp = reinterpret_cast<const uint2*>(csr.key + b * csr.lstride + base);
+        const float4* wp = reinterpret_cast<const float4*>(csr.weight + b * csr.wstride + base);
+#pragma unroll
+        for (int u = 0; u < E / 4; ++u) {
+            const uint2 l = lp[u], k = kp[u];
+            const float4 v = wp[u];
+            ids[2 * u] = l.x;
+            ids[2 * u + 1] = l.y;
+            pts[2 * u] = k.x;
+            pts[2 * u + 1] = k.y;
+            w[4 * u] = v.x;
+            w[4 * u + 1] = v.y;
+            w[4 * u + 2] = v.z;
+            w[4 * u + 3] = v.w;
+        }
+    }
+    const int before = q0 > 0 && q0 < total ? csr.key[b * csr.lstride + q0 - 1] : -1;
+    const int after = q0 + qn < total ? csr.key[b * csr.lstride + q0 + qn] : -1;
+    auto half = [](const uint32_t (&a)[E / 2], int u) {
+        return static_cast<int>((u & 1) ? a[u >> 1] >> 16 : a[u >> 1] & 0xFFFFu);
+    };
+    // Entry ids become unknown indices (n = e / 3), 0 past my positions
+    // (weight 0, never stored).
+#pragma unroll
+    for (int u = 0; u < E / 2; ++u) {
+        const uint32_t lo = u * 2 < qn ? (ids[u] & 0xFFFFu) / 3 : 0;
+        const uint32_t hi = u * 2 + 1 < qn ? (ids[u] >> 16) / 3 : 0;
+        ids[u] = lo | (hi << 16);
+    }
+    // Per position: does a piece start here (bit u of `fresh`), and the slot
+    // its running sum goes to (as in the grouping gather).
+    uint32_t fresh = 0;
+    uint32_t dest[E / 2];
+    int head_m = -1;
+    {
+        const int first_m = qn > 0 ? half(pts, 0) : -1;
+        const bool cont = qn > 0 && before == first_m;
+#pragma unroll
+        for (int u = 0; u < E; ++u) {
+            const int m = half(pts, u);
+            const int mm = u + 1 < qn ? half(pts, u + 1) : after;
+            if (u < qn && (u == 0 || m != half(pts, u - 1))) fresh |= 1u << u;
+            const bool mine_first = cont && m == first_m;  // a list begun before q0
+            int d = kTrash + tid;
+            if (u < qn && m != mm) {  // the list ends here
+                d = mine_first ? kCont + tid : m;
+            } else if (u + 1 == qn) {  // the list goes on past my range
+                if (mine_first) {
+                    d = kCont + tid;  // a middle piece
+                } else {
+                    d = kHead + tid;
+                    head_m = m;
+                }
+            }
+            if (u & 1) dest[u >> 1] |= static_cast<uint32_t>(d) << 16;
+            else dest[u >> 1] = static_cast<uint32_t>(d);
+        }
+    }
+    const int head_span = head_m >= 0 ? (st[head_m + 1] - (q0 + qn) + E - 1) / E : 0;
     // A group's rows, thread tid holding unknowns n = tid + k T (k < NK) of
-    // its 4 channels, so that the LDS stores below (one 16-byte [n][4]
-    // entry per lane) go to consecutive addresses.  Every lane loads from
-    // inside the batch (row and unknown clamped); what lies outside is
-    // replaced by zeros afterwards.
-    constexpr int NK = kTiCsrMaxN / T;
+    // its 4 channels, so that the LDS stores (one 16-byte [n][4] entry per
+    // lane) go to consecutive addresses.  Every lane loads from inside the
+    // batch (row and unknown clamped); what lies outside is zeroed.
     auto fetch = [&](int64_t s, float4 (&r)[NK]) {
         const int64_t c0 = 4 * (j + s * J);
         float v[4][NK];
@@ -673,93 +754,70 @@ __global__ __launch_bounds__(kTiCsrThreads) void three_interp_csr_gather_kernel(
     float4 ra[NK], rb[NK];
     if (own > 0) fetch(0, ra);
     if (own > 1) fetch(1, rb);
-    // The batch's CSR into LDS, every load issued before the first store.
-    {
-        constexpr int U = (3 * kTiCsrMaxN + T - 1) / T;  // entries per thread at most
-        constexpr int US = (kTiCsrThreads + 1 + T - 1) / T;  // starts per thread at most
-        const uint16_t* lsrc = csr.list + b * csr.lstride;
-        const float* wsrc = csr.weight + b * csr.wstride;
-        const int* ssrc = csr.start + b * csr.sstride;
-        uint32_t lv[U];
-        float wv[U];
-        int sv[US];
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int q = min(tid + u * T, 3 * N - 1);
-            lv[u] = lsrc[q];
-            wv[u] = wsrc[q];
-        }
-#pragma unroll
-        for (int u = 0; u < US; ++u) sv[u] = ssrc[min(tid + u * T, M)];
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-            const int q = tid + u * T;
-            if (q < 3 * N) {
-                nl[q] = static_cast<uint16_t>(lv[u] / 3);
-                wl[q] = wv[u];
-            }
-        }
-#pragma unroll
-        for (int u = 0; u < US; ++u)
-            if (tid + u * T <= M) st[tid + u * T] = sv[u];
-    }
-    __syncthreads();
-    const bool mine = tid < M;
-    const int pb = mine ? st[tid] : 0, pe = mine ? st[tid + 1] : 0;
-    int en[R];
-    float ew[R];
-#pragma unroll
-    for (int k = 0; k < R; ++k) {
-        const int q = min(pb + k, max(pe - 1, pb));  // an unused slot repeats a valid one
-        en[k] = pe > pb ? nl[q] : 0;
-        ew[k] = pe > pb ? wl[q] : 0.f;
-    }
+    // Every result slot starts at 0: a known point with an empty list keeps
+    // it, the others are rewritten for every group.
+    if (tid < M) slots[tid] = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int64_t s = 0; s < own; ++s) {
-        __syncthreads();  // every thread is done with the previous group's rows
+        __syncthreads();  // every thread is done with the previous group's rows and slots
 #pragma unroll
         for (int k = 0; k < NK; ++k)
             if (tid + k * T < N) rows[tid + k * T] = ra[k];
 #pragma unroll
         for (int k = 0; k < NK; ++k) ra[k] = rb[k];
-        __syncthreads();
+        __syncthreads();  // rows complete
         if (s + 2 < own) fetch(s + 2, rb);
-        if (!mine) continue;
-        float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-        auto add = [&](const float4 v, float w, bool ok) {
-            const float t0 = v.x * w, t1 = v.y * w, t2 = v.z * w, t3 = v.w * w;
-            a0 = ok ? a0 + t0 : a0;
-            a1 = ok ? a1 + t1 : a1;
-            a2 = ok ? a2 + t2 : a2;
-            a3 = ok ? a3 + t3 : a3;
-        };
+        // Keeps the unpacked indices and slots from being hoisted out of the
+        // group loop.
 #pragma unroll
-        for (int k = 0; k < R; ++k) add(rows[en[k]], ew[k], pb + k < pe);
-        // The rest of a long list: four entries' reads at once (past the
-        // end: the last entry again, not added), added in order.
-        for (int p = pb + R; p < pe; p += 4) {
-            float4 v[4];
-            float w[4];
+        for (int u = 0; u < E / 2; ++u) asm volatile("" : "+v"(ids[u]), "+v"(dest[u]));
+        float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-            for (int u = 0; u < 4; ++u) {
-                const int q = min(p + u, pe - 1);
-                v[u] = rows[nl[q]];
-                w[u] = wl[q];
-            }
-#pragma unroll
-            for (int u = 0; u < 4; ++u) add(v[u], w[u], p + u < pe);
+        for (int u = 0; u < E; ++u) {
+            const float4 v = rows[half(ids, u)];
+            const bool f = (fresh >> u) & 1u;
+            // +0 + fl(row * w): a piece's first term, as the sequential loop
+            // adds it to a zero-filled gradient.
+            acc.x = (f ? 0.f : acc.x) + v.x * w[u];
+            acc.y = (f ? 0.f : acc.y) + v.y * w[u];
+            acc.z = (f ? 0.f : acc.z) + v.z * w[u];
+            acc.w = (f ? 0.f : acc.w) + v.w * w[u];
+            slots[half(dest, u)] = acc;
         }
-        const int64_t c0 = 4 * (j + s * J);
-        float* o = grad_features + (b * C + c0) * M + tid;
-        o[0] = a0;
-        if (c0 + 1 < C) o[M] = a1;
-        if (c0 + 2 < C) o[2 * static_cast<int64_t>(M)] = a2;
-        if (c0 + 3 < C) o[3 * static_cast<int64_t>(M)] = a3;
+        __syncthreads();  // pieces complete
+        if (head_span > 0) {
+            // The following threads' pieces, four reads in flight at a time
+            // (past the span: the last piece again, not added).
+            float4 v = slots[kHead + tid];
+            for (int k0 = 1; k0 <= head_span; k0 += 4) {
+                float4 c[4];
+#pragma unroll
+                for (int k = 0; k < 4; ++k) c[k] = slots[kCont + tid + min(k0 + k, head_span)];
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k0 + k <= head_span) {
+                        v.x = v.x + c[k].x;
+                        v.y = v.y + c[k].y;
+                        v.z = v.z + c[k].z;
+                        v.w = v.w + c[k].w;
+                    }
+            }
+            slots[head_m] = v;
+        }
+        __syncthreads();  // results complete
+        if (tid < M) {
+            const int64_t c0 = 4 * (j + s * J);
+            const float4 r = slots[tid];
+            float* o = grad_features + (b * C + c0) * M + tid;
+            o[0] = r.x;
+            if (c0 + 1 < C) o[M] = r.y;
+            if (c0 + 2 < C) o[2 * static_cast<int64_t>(M)] = r.z;
+            if (c0 + 3 < C) o[3 * static_cast<int64_t>(M)] = r.w;
+        }
     }
 }
 
-__host__ __device__ inline size_t csr_gather_lds_bytes(int64_t M, int64_t N) {
-    return static_cast<size_t>(16 * N + 4 * 3 * N + 2 * ((3 * N + 1) & ~int64_t(1)) + 4 * (M + 1));
+__host__ __device__ inline size_t csr_gather_lds_bytes() {
+    return static_cast<size_t>(16 * (kTiCsrMaxN + 4 * kTiCsrThreads));
 }
 
 // Channels per step of the CSR gather: the largest CG in {4, 2, 1} whose
@@ -895,7 +953,7 @@ hipError_t pointops_three_interpolate_backward_from_csr(const float* grad_out,
         const int64_t J = std::min<int64_t>(groups, std::max<int64_t>(1, (256 + B - 1) / B));
         if (B * J <= INT32_MAX) {
             hipLaunchKernelGGL(three_interp_csr_gather_kernel, dim3(static_cast<uint32_t>(B * J)),
-                               dim3(kTiCsrThreads), csr_gather_lds_bytes(M, N), stream, grad_out,
+                               dim3(kTiCsrThreads), csr_gather_lds_bytes(), stream, grad_out,
                                csr, grad_features, C, m, n, static_cast<uint32_t>(J));
             return hipGetLastError();
         }

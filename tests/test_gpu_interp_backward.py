@@ -1,8 +1,11 @@
 """GPU parity of the CSR three_interpolate backward
 (pointops_three_interpolate_backward_csr): bit for bit, on every call, equal
-to a float32 scatter loop over (n, t) in order (numpy's unbuffered add.at,
-which applies the updates in index order), and within 1e-5 of the oracle's
-three_interpolate_backward (the same loop accumulated in double,
+to its documented float32 order -- for up to 1024 known points, a known
+point's terms fl32(grad_out * w) in (n, t) order summed in pieces cut at
+every 12th position of the batch's CSR (emulated in numpy here); for more,
+the float32 scatter loop over (n, t) in order (numpy's unbuffered add.at,
+which applies the updates in index order) -- and within 1e-5 of the
+oracle's three_interpolate_backward (the same loop accumulated in double,
 kernels/pointnet2.metal:85-103)."""
 
 from __future__ import annotations
@@ -32,6 +35,40 @@ def sequential_f32(up: np.ndarray, idx: np.ndarray, w: np.ndarray, m: int) -> np
     return out
 
 
+def pieces_f32(up: np.ndarray, idx: np.ndarray, w: np.ndarray, m: int, piece: int = 12) -> np.ndarray:
+    """The CSR gather's order for M <= 1024 known points: per batch the
+    entries e = 3n + t sorted by (known index, e) are cut into pieces at
+    every `piece`-th position; each piece sums fl32(up[c, n] * w[e]) from +0
+    in order and a known point's pieces are added in order."""
+    B, C, _ = up.shape
+    out = np.zeros((B, C, m), np.float32)
+    for b in range(B):
+        keys = idx[b].reshape(-1).astype(np.int64)
+        valid = np.nonzero((keys >= 0) & (keys < m))[0]
+        order = valid[np.argsort(keys[valid], kind="stable")]
+        sk = keys[order]
+        starts = np.searchsorted(sk, np.arange(m + 1))
+        terms = (up[b][:, order // 3] * w[b].reshape(-1)[order]).astype(np.float32)  # (C, E)
+        for k in range(m):
+            q, e = int(starts[k]), int(starts[k + 1])
+            total = None
+            while q < e:
+                cut = min(e, (q // piece + 1) * piece)
+                part = np.zeros(C, np.float32)
+                for i in range(q, cut):
+                    part = (part + terms[:, i]).astype(np.float32)
+                total = part if total is None else (total + part).astype(np.float32)
+                q = cut
+            if total is not None:
+                out[b, :, k] = total
+    return out
+
+
+def expected_bits(up, idx, w, m):
+    """Known points <= 1024: the piece order; more: the sequential loop."""
+    return pieces_f32(up, idx, w, m) if m <= 1024 else sequential_f32(up, idx, w, m)
+
+
 def backward_csr(grad_out: torch.Tensor, idx: torch.Tensor, w: torch.Tensor, m: int,
                  fill: float = float("nan")) -> np.ndarray:
     """The CSR entry point through the C ABI into an output pre-filled with
@@ -59,7 +96,7 @@ def test_csr_backward_matches_sequential_loop(cuda_device, m, n, c):
     idx[:, : n // 3, :] = idx[:, :1, :]  # a hot bucket, repeated within one n
     w = torch.rand(B, n, 3, generator=g)
     up = torch.randn(B, c, n, generator=g)
-    want = sequential_f32(up.numpy(), idx.numpy(), w.numpy(), m)
+    want = expected_bits(up.numpy(), idx.numpy(), w.numpy(), m)
     first = backward_csr(up, idx, w, m)
     np.testing.assert_array_equal(first.view(np.uint32), want.view(np.uint32))
     # float32 against double accumulation; the hot bucket sums up to 4096 terms.
@@ -119,7 +156,7 @@ def test_public_backward_uses_csr_path(cuda_device, monkeypatch):
     assert calls == ["pointops_three_interpolate", "pointops_three_interpolate_csr_build"]
     out.backward(up.cuda(), retain_graph=True)
     assert calls[2:] == ["pointops_three_interpolate_backward_from_csr"]
-    want = sequential_f32(up.numpy(), idx.numpy(), w.numpy(), M)
+    want = pieces_f32(up.numpy(), idx.numpy(), w.numpy(), M)
     np.testing.assert_array_equal(host(f.grad).view(np.uint32), want.view(np.uint32))
     # A second backward over the same graph reuses the CSR: the same bits again.
     f.grad = None
