@@ -749,6 +749,21 @@ def probe() -> None:
           "QueryAndGroup fwd+bwd, 256 MiB copy) done", flush=True)
 
 
+def pipeline_trace(calls: int = 20) -> None:
+    """The timed step alone (mps_pointops.fps_ball_knn at config 2, chunk
+    256, as the benchmark times it) `calls` times after two warm-up calls,
+    for a kernel trace of the overlapped front end."""
+    import mps_pointops as mp
+
+    xyz = make_c2().cuda()
+    radii = [r for r, _ in C2_RADII]
+    ks = [k for _, k in C2_RADII]
+    for _ in range(2 + calls):
+        mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
+    torch.cuda.synchronize()
+    print(f"pipeline: {2 + calls} x fps_ball_knn (chunk 256) done", flush=True)
+
+
 def main() -> None:
     parser = argparse.ArgumentParser()
     parser.add_argument("--gpus", type=int, default=1)
@@ -760,6 +775,9 @@ def main() -> None:
     parser.add_argument("--cpu-repeats", type=int, default=20)
     parser.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                         help="workload; the headline metric (and the default) is c2")
+    parser.add_argument("--pipeline-trace", action="store_true",
+                        help="run only the timed step (fps_ball_knn, chunk 256) 22 times, "
+                             "for a kernel trace")
     parser.add_argument("--probe", action="store_true",
                         help="run each config-2 kernel 3 times (for rocprofv3 counter passes)")
     args = parser.parse_args()
@@ -770,6 +788,9 @@ def main() -> None:
         sys.exit(2)
     if args.probe:
         probe()
+        return
+    if args.pipeline_trace:
+        pipeline_trace()
         return
     result = run(args) if args.config == "c2" else run_other(args)
     if args.config != "c2" and not args.no_cpu_baseline:

@@ -396,13 +396,15 @@ hipError_t pointops_chamfer_backward_f64(const double *query, const double *ref,
  * events per host thread and device are created on first use and kept.
  * `workspace` (pointops_fps_query_pipeline_workspace_bytes bytes, no
  * initialisation needed) and `status` (one word) belong to one call until
- * fps_stream has passed it: calls that overlap need distinct ones.  The
- * gates read the progress words at most 2^24 times per thread (or
- * POINTOPS_PIPELINE_SPIN_LIMIT times, read per call; 0 makes them give up at
- * once).  A gate that gives up sets `status` non-zero and writes NaN centres
- * for its chunk and every later chunk, whose queries then return the
- * results for a NaN query (ball query (0, -1), kNN (inf, 2^32 - 1)); the
- * samples stay exact.  No counterpart in the
+ * fps_stream has passed it: calls that overlap need distinct ones.  FPS
+ * stores each centre in the workspace before publishing it and a gate (one
+ * wave per cloud) copies the chunk's centres out.  A gate wave reads its
+ * cloud's progress word at most 2^24 times (or POINTOPS_PIPELINE_SPIN_LIMIT
+ * times, read per call; 0 makes it give up at once).  A wave that gives up,
+ * and every wave of a later gate, sets `status` non-zero and writes NaN
+ * centres for its cloud's chunk, whose queries then return the results for
+ * a NaN query (ball query (0, -1), kNN (inf, 2^32 - 1)); the samples stay
+ * exact.  No counterpart in the
  * reference, which runs these steps one after another. */
 size_t pointops_fps_query_pipeline_workspace_bytes(int64_t B, int64_t N, int64_t npoint,
                                                    int64_t chunk);

@@ -157,7 +157,7 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
                                                       const int64_t* __restrict__ starts,
                                                       int64_t* __restrict__ out, int64_t N,
                                                       int64_t npoint, int64_t start, int skip,
-    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk) {
+    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk, float* __restrict__ centres) {
     constexpr int NW = T / kWave;
     constexpr int KC = kWave / NW;  // candidates per wave
     constexpr int CAP = P * T;      // points per cloud at most
@@ -191,7 +191,17 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     const int wave = tid / kWave;
     const int lane = tid % kWave;
     const int far0 = static_cast<int>(seg.start);
-    if (tid == 0) o[0] = seg.base + far0;
+    // With `centres` set, sample s's coordinates also go to
+    // centres[3 (out_lo + s) ..], copied from the cloud.
+    float* const oc = centres != nullptr ? centres + 3 * seg.out_lo : nullptr;
+    if (tid == 0) {
+        o[0] = seg.base + far0;
+        if (oc != nullptr && n > 0) {
+            oc[0] = p[3 * far0];
+            oc[1] = p[3 * far0 + 1];
+            oc[2] = p[3 * far0 + 2];
+        }
+    }
     // With `progress` set, wave 0 publishes, once the samples [0, done) are
     // stored, tag + the number of whole `chunk`s among them (all of them once
     // done == seg.cnt) in word blockIdx.x: an agent-scope release fence over
@@ -514,7 +524,14 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
             take(wv);
         }
         if (pend) apply_pending();
-        if (wave == 0 && when >= 0) o[step + when] = seg.base + cidx;
+        if (wave == 0 && when >= 0) {
+            o[step + when] = seg.base + cidx;
+            if (oc != nullptr) {
+                oc[3 * (step + when)] = ccx;
+                oc[3 * (step + when) + 1] = ccy;
+                oc[3 * (step + when) + 2] = ccz;
+            }
+        }
         step += taken;
         publish(step - taken, step);
     }
@@ -564,7 +581,7 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     const float* __restrict__ xyz, const int64_t* __restrict__ ptr,
     const int64_t* __restrict__ out_ptr, const int64_t* __restrict__ starts,
     int64_t* __restrict__ out, int64_t N, int64_t npoint, int64_t start, int skip,
-    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk) {
+    uint64_t* __restrict__ progress, uint64_t tag, int64_t chunk, float* __restrict__ centres) {
     constexpr int NS = kLeadFollowers;  // followers; they also run the setup's sort
     constexpr int TS = NS * kWave;      // threads of the sort
     constexpr int NF = kLeadFollowers;
@@ -620,7 +637,17 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     const bool follower = !leader;
     constexpr int kOutWave = 0;  // the first follower stores the samples
     const int far0 = static_cast<int>(seg.start);
-    if (wave == kOutWave && lane == 0) o[0] = seg.base + far0;
+    // With `centres` set, sample s's coordinates also go to
+    // centres[3 (out_lo + s) ..], copied from the cloud.
+    float* const oc = centres != nullptr ? centres + 3 * seg.out_lo : nullptr;
+    if (wave == kOutWave && lane == 0) {
+        o[0] = seg.base + far0;
+        if (oc != nullptr && n > 0) {
+            oc[0] = p[3 * far0];
+            oc[1] = p[3 * far0 + 1];
+            oc[2] = p[3 * far0 + 2];
+        }
+    }
     auto publish = [&](int64_t before, int64_t done_steps) {
         if (progress == nullptr || wave != kOutWave) return;
         const int64_t whole = (seg.cnt + chunk - 1) / chunk;
@@ -1088,6 +1115,17 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
                     const int wl = reinterpret_cast<const uint8_t*>(ring[si >> 2])[si & 3];
                     const int idx = __builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.w));
                     if (c0 + lane < a) o[run_start + c0 + lane] = seg.base + idx;
+                    if (oc != nullptr) {
+                        const int x = __builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.x));
+                        const int y = __builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.y));
+                        const int z = __builtin_amdgcn_ds_bpermute(wl << 2, f2i(mine.z));
+                        if (c0 + lane < a) {
+                            float* c = oc + 3 * (run_start + c0 + lane);
+                            c[0] = i2f(x);
+                            c[1] = i2f(y);
+                            c[2] = i2f(z);
+                        }
+                    }
                 }
             }
             step = run_start + a;
@@ -1749,15 +1787,15 @@ hipError_t launch_regs(const float* xyz, const int64_t* ptr, const int64_t* out_
                        const int64_t* starts, int64_t* out, int64_t blocks, int64_t N,
                        int64_t npoint, int64_t start, int skip, hipStream_t stream,
                        uint64_t* progress = nullptr, uint64_t tag = 0, int64_t chunk = 1,
-                       size_t reserve = 0) {
+                       size_t reserve = 0, float* centres = nullptr) {
     if constexpr (P > 8) {
         hipLaunchKernelGGL((fps_tiled_kernel<P, kRegsThreads, kTilesFirstHalf<P>>), dim3(static_cast<uint32_t>(blocks)),
                            dim3(kRegsThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                           start, skip, progress, tag, chunk);
+                           start, skip, progress, tag, chunk, centres);
     } else {
         hipLaunchKernelGGL((fps_lead_kernel<P>), dim3(static_cast<uint32_t>(blocks)),
                            dim3(kLeadThreads), reserve, stream, xyz, ptr, out_ptr, starts, out, N, npoint,
-                           start, skip, progress, tag, chunk);
+                           start, skip, progress, tag, chunk, centres);
     }
     return hipGetLastError();
 }
@@ -1885,9 +1923,12 @@ int large_capacity(int device) {
 
 namespace pointops {
 
-// Dense FPS of B clouds of N <= 8192 points (the tiled kernel) that publishes
-// per-cloud progress words: progress[b] = tag + the whole `chunk`s of samples
-// of cloud b stored so far (all ceil(npoint / chunk) of them at the end).
+// Dense FPS of B clouds of N <= 8192 points (fps_lead_kernel, or
+// fps_tiled_kernel above 4096 points) that publishes per-cloud progress
+// words: progress[b] = tag + the whole `chunk`s of samples of cloud b stored
+// so far (all ceil(npoint / chunk) of them at the end).  With `centres` set,
+// each sample's coordinates are stored too (B, npoint, 3), before the
+// progress word that covers them.
 // Dynamic LDS that, added to fps_tiled_kernel<P>'s own, takes all of a CU's
 // LDS: no workgroup that uses LDS (every kernel queued beside a pipelined
 // FPS does) can then share a CU with an FPS workgroup and take issue slots
@@ -1914,24 +1955,24 @@ size_t fps_reserve_lds() {
 
 hipError_t fps_dense_progress(const float* xyz, int64_t* out, int64_t B, int64_t N,
                               int64_t npoint, int64_t start, int skip, uint64_t* progress,
-                              uint64_t tag, int64_t chunk, hipStream_t stream) {
+                              uint64_t tag, int64_t chunk, float* centres, hipStream_t stream) {
     if (B < 1 || B > INT32_MAX || N < 1 || N > kRegsMaxPoints || npoint < 1 || npoint > N ||
         start < 0 || start >= N || chunk < 1 || progress == nullptr)
         return hipErrorInvalidValue;
     if (N <= 1 * kRegsThreads)
-        return launch_regs<1>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
-                               fps_reserve_lds<1>());
+        return launch_regs<1>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream,
+                              progress, tag, chunk, fps_reserve_lds<1>(), centres);
     if (N <= 2 * kRegsThreads)
-        return launch_regs<2>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
-                               fps_reserve_lds<2>());
+        return launch_regs<2>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream,
+                              progress, tag, chunk, fps_reserve_lds<2>(), centres);
     if (N <= 4 * kRegsThreads)
-        return launch_regs<4>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
-                               fps_reserve_lds<4>());
+        return launch_regs<4>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream,
+                              progress, tag, chunk, fps_reserve_lds<4>(), centres);
     if (N <= 8 * kRegsThreads)
-        return launch_regs<8>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
-                               fps_reserve_lds<8>());
-    return launch_regs<16>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream, progress, tag, chunk,
-                               fps_reserve_lds<16>());
+        return launch_regs<8>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream,
+                              progress, tag, chunk, fps_reserve_lds<8>(), centres);
+    return launch_regs<16>(xyz, nullptr, nullptr, nullptr, out, B, N, npoint, start, skip, stream,
+                           progress, tag, chunk, fps_reserve_lds<16>(), centres);
 }
 
 }  // namespace pointops

@@ -6,17 +6,19 @@
 // radius and knn (ops.py:144-205).  Single-cloud FPS is sequential in its
 // samples and occupies one CU per cloud (B CUs of 256), while the queries of
 // a centre need only that centre.  Here FPS runs on `fps_stream` and
-// publishes per-cloud progress every `chunk` samples; on `query_stream`, for
-// each chunk of centres a one-workgroup gate kernel waits until every cloud
-// has published the chunk, gathers its centres, and the ball queries of that
-// chunk follow on the free CUs while FPS goes on.  kNN runs once, over all
+// stores each sample's index, and its coordinates in the workspace,
+// publishing per-cloud progress every `chunk` samples; on `query_stream`,
+// for each chunk of centres a gate kernel (one wave per cloud) waits until
+// its cloud has published the chunk and copies the cloud's centres of the
+// chunk (contiguous rows, not a gather through the indices), and the ball
+// queries of that chunk follow on the free CUs while FPS goes on.  kNN runs once, over all
 // centres, after the last chunk: its lane kernel gives each workgroup 64
 // queries against the whole cloud, so its duration does not shrink with the
 // number of queries (measured at config 2: about 62 us for 128 centres per
 // cloud, 86 us for 1024), and per-chunk launches would serialise that cost.  Results are those
 // of the separate calls, bit for bit: the same kernels compute each query.
 //
-// The only waiting is the gate's bounded poll of the progress words; FPS
+// The only waiting is the gates' bounded poll of the progress words; FPS
 // waits on nothing, and its workgroups are resident before any chunk can be
 // published, so the query kernels queued behind a gate cannot keep FPS from
 // running.
@@ -26,11 +28,12 @@
 // that clear before its first gate, so a gate can only be satisfied by its
 // own call's FPS.  Overlapping calls (on other streams, or queued back to
 // back) need distinct workspaces; the Python wrapper allocates one per call.
-// A gate that gives up (its poll budget spent, or an earlier gate of the call
-// gave up) sets *status and writes NaN centres for its chunk, so the chunk's
-// queries run on NaN centres: ball-query rows (0, -1) and kNN rows
-// (inf, 2^32 - 1), the reference's results for a NaN query.  Every launch
-// ends.
+// A gate wave that gives up (its poll budget spent, or a gate of the call
+// gave up before it started) sets *status and writes NaN centres for its
+// cloud's chunk, so those queries run on NaN centres: ball-query rows
+// (0, -1) and kNN rows (inf, 2^32 - 1), the reference's results for a NaN
+// query.  FPS only ever writes the workspace's copy, so nothing overwrites
+// the NaN.  Every launch ends.
 #include <cstdlib>
 
 #include "pointops_common.hpp"
@@ -40,7 +43,7 @@ namespace pointops {
 
 hipError_t fps_dense_progress(const float* xyz, int64_t* out, int64_t B, int64_t N,
                               int64_t npoint, int64_t start, int skip, uint64_t* progress,
-                              uint64_t tag, int64_t chunk, hipStream_t stream);
+                              uint64_t tag, int64_t chunk, float* centres, hipStream_t stream);
 hipError_t ball_query_rows_f32(const float* q, const float* p, int64_t* idx, float* dist2,
                                int64_t B, int64_t Q, int64_t QS, int64_t P, int64_t K, float r2,
                                hipStream_t stream);
@@ -51,8 +54,8 @@ hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist,
 namespace {
 
 constexpr int kGateThreads = 256;
-// Reads of the progress words per gate thread (over all of its clouds)
-// before the gate gives up, each after a sleep of about 0.5 us: several
+// Reads of its cloud's progress word per gate wave before it gives up,
+// each after a sleep of about 0.5 us: several
 // seconds, against well under a second for the longest FPS this path takes
 // (65535 clouds of 8192 points).
 constexpr uint32_t kGateSpinLimit = 1u << 24;
@@ -112,57 +115,44 @@ __global__ __launch_bounds__(kGateThreads) void pipeline_clear_kernel(
     if (i == 0) status[0] = 0;
 }
 
-// Waits until progress[b] >= target for every cloud b, then writes the
-// centres of samples [m0, m1) of every cloud: centres[b, m] = xyz[b, samples[b, m]].
-// A thread reads the words at most `spin_limit` times in all; once any
-// thread gives up (or an earlier gate has: *status set), every thread stops
-// waiting and the chunk's centres are NaN.
-__global__ __launch_bounds__(kGateThreads) void pipeline_gate_kernel(
-    const uint64_t* __restrict__ progress, uint64_t target, const float* __restrict__ xyz,
-    const int64_t* samples, float* __restrict__ centres, uint32_t* __restrict__ status,
-    int64_t B, int64_t N, int64_t npoint, int64_t m0, int64_t m1, uint32_t spin_limit) {
-    __shared__ int gave_up;
-    if (threadIdx.x == 0)
-        gave_up = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
-    __syncthreads();
-    volatile int* const flag = &gave_up;
-    uint32_t polls = 0;
-    for (int64_t b = threadIdx.x; b < B; b += kGateThreads) {
-        for (;;) {
-            if (*flag) break;
-            if (polls >= spin_limit) {
-                *flag = 1;
-                break;
-            }
-            ++polls;
-            if (__hip_atomic_load(progress + b, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= target)
-                break;
-            __builtin_amdgcn_s_sleep(16);
+// One wave per cloud b: waits until progress[b] >= target, then writes the
+// centres of samples [m0, m1) of cloud b, copied from the coordinates FPS
+// stored in `staged` (B, npoint, 3) before publishing them (contiguous
+// rows, every load in flight at once).  The wave reads the word at most
+// `spin_limit` times; if it gives up, or an earlier gate of the call has
+// (*status set), it sets *status and the cloud's chunk of centres is NaN.
+constexpr int kGateRowFloats = 12;  // floats per lane per copy round
+
+__global__ __launch_bounds__(kWave) void pipeline_gate_kernel(
+    const uint64_t* __restrict__ progress, uint64_t target, const float* staged,
+    float* __restrict__ centres, uint32_t* __restrict__ status, int64_t npoint, int64_t m0,
+    int64_t m1, uint32_t spin_limit) {
+    const int64_t b = blockIdx.x;
+    const int lane = threadIdx.x;
+    bool gave_up = __hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0u;
+    for (uint32_t polls = 0; !gave_up; ++polls) {
+        if (polls >= spin_limit) {
+            gave_up = true;
+            break;
         }
-        if (*flag) break;
+        if (__hip_atomic_load(progress + b, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) >= target)
+            break;
+        __builtin_amdgcn_s_sleep(16);
     }
-    __syncthreads();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-    const bool poisoned = gave_up != 0;
-    if (poisoned && threadIdx.x == 0)
+    if (gave_up && lane == 0)
         __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t mc = m1 - m0;
-    for (int64_t i = threadIdx.x; i < B * mc; i += kGateThreads) {
-        const int64_t b = i / mc, m = m0 + i % mc;
-        float* dst = centres + (b * npoint + m) * 3;
-        if (poisoned) {
-            dst[0] = dst[1] = dst[2] = __builtin_nanf("");
-            continue;
-        }
-        // Samples are read with agent-scope atomic loads: they were stored by
-        // workgroups still running on other XCDs.
-        int64_t j = __hip_atomic_load(samples + b * npoint + m, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-        j = j < 0 ? 0 : (j >= N ? N - 1 : j);
-        const float* src = xyz + (b * N + j) * 3;
-        dst[0] = src[0];
-        dst[1] = src[1];
-        dst[2] = src[2];
+    const int64_t row = (m1 - m0) * 3;  // floats of the cloud's chunk
+    const float* src = staged + (b * npoint + m0) * 3;
+    float* dst = centres + (b * npoint + m0) * 3;
+    for (int64_t i0 = lane; i0 < row; i0 += kGateRowFloats * kWave) {
+        float v[kGateRowFloats];
+#pragma unroll
+        for (int u = 0; u < kGateRowFloats; ++u)
+            v[u] = gave_up ? __builtin_nanf("") : src[min(i0 + u * kWave, row - 1)];
+#pragma unroll
+        for (int u = 0; u < kGateRowFloats; ++u)
+            if (i0 + u * kWave < row) dst[i0 + u * kWave] = v[u];
     }
 }
 
@@ -177,6 +167,7 @@ size_t pointops_fps_query_pipeline_workspace_bytes(int64_t B, int64_t N, int64_t
                                                    int64_t chunk) {
     if (B <= 0 || N <= 0 || npoint <= 0 || chunk <= 0) return 0;
     return align_up(static_cast<size_t>(B) * sizeof(uint64_t)) +
+           align_up(static_cast<size_t>(B * npoint * 3) * sizeof(float)) +
            pointops_knn3_windowed_workspace_bytes(B, npoint, N);
 }
 
@@ -198,7 +189,10 @@ hipError_t pointops_fps_query_pipeline_f32(
             return hipErrorInvalidValue;
     const int64_t chunks = (npoint + chunk - 1) / chunk;
     uint64_t* progress = static_cast<uint64_t*>(workspace);
-    char* knn_ws = static_cast<char*>(workspace) + align_up(static_cast<size_t>(B) * sizeof(uint64_t));
+    float* staged = reinterpret_cast<float*>(static_cast<char*>(workspace) +
+                                             align_up(static_cast<size_t>(B) * sizeof(uint64_t)));
+    char* knn_ws = reinterpret_cast<char*>(staged) +
+                   align_up(static_cast<size_t>(B * npoint * 3) * sizeof(float));
     CallEvents* ev = nullptr;
     hipError_t err = call_events(fps_stream, &ev);
     if (err != hipSuccess) return err;
@@ -210,15 +204,15 @@ hipError_t pointops_fps_query_pipeline_f32(
     if ((err = hipEventRecord(ev->cleared, fps_stream)) != hipSuccess) return err;
     if ((err = hipStreamWaitEvent(query_stream, ev->cleared, 0)) != hipSuccess) return err;
     err = fps_dense_progress(xyz, samples, B, N, npoint, start_idx, skip_near_origin != 0,
-                             progress, 0, chunk, fps_stream);
+                             progress, 0, chunk, staged, fps_stream);
     if (err != hipSuccess) return err;
     for (int64_t c = 0; c < chunks; ++c) {
         const int64_t m0 = c * chunk;
         const int64_t m1 = m0 + chunk < npoint ? m0 + chunk : npoint;
         const int64_t mc = m1 - m0;
-        hipLaunchKernelGGL(pipeline_gate_kernel, dim3(1), dim3(kGateThreads), 0, query_stream,
-                           progress, static_cast<uint64_t>(c + 1), xyz, samples, centres,
-                           status, B, N, npoint, m0, m1, limit);
+        hipLaunchKernelGGL(pipeline_gate_kernel, dim3(static_cast<uint32_t>(B)), dim3(kWave), 0,
+                           query_stream, progress, static_cast<uint64_t>(c + 1), staged, centres,
+                           status, npoint, m0, m1, limit);
         if ((err = hipGetLastError()) != hipSuccess) return err;
         for (int64_t r = 0; r < nball; ++r) {
             err = ball_query_rows_f32(centres + 3 * m0, xyz, ball_idx[r] + m0 * ball_k[r],
