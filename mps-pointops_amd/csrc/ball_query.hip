@@ -360,21 +360,149 @@ hipError_t ball_query_f32_unless(const float* queries, const float* points, int6
 
 namespace pointops {
 
-// Ball query (float32, no lengths, LDS-staged kernel) over Q query rows per
-// cloud whose rows -- queries and both outputs -- lie QS rows apart: Q
-// consecutive centres of a (B, QS, 3) tensor and of its (B, QS, K) outputs.
-hipError_t ball_query_rows_f32(const float* q, const float* p, int64_t* idx, float* dist2,
-                               int64_t B, int64_t Q, int64_t QS, int64_t P, int64_t K, float r2,
-                               hipStream_t stream) {
+// Ball queries of several radii around the same centres in one scan (the
+// multi-scale grouping of a PointNet++ layer): the LDS-staged search of
+// ball_query_lds_kernel, each pair's distance computed once and tested
+// against every radius still short of its K hits.  A radius keeps its own
+// first-K list in index order, so every output equals that radius's own
+// search, bit for bit; the scan ends when every radius is done (or the
+// cloud is).  Float32, no lengths; Q query rows per cloud lying QS rows
+// apart, as in ball_query_rows_f32.
+template <int NR>
+__global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel(
+    const float* __restrict__ queries, const float* __restrict__ points, BallMulti out,
+    int64_t Q, int64_t P, int64_t QS) {
+    constexpr int NWQ = kBqLdsQueries;
+    constexpr int kTile = kBqLdsDepth * kWave;
+    constexpr int kPer = kTile / (NWQ * kWave);
+    static_assert(kPer * NWQ * kWave == kTile && kBqLdsDepth % 2 == 0 && NR <= kBqMulti, "shape");
+    __shared__ float4 tile[kTile];
+    __shared__ int done_flags[NWQ];
+    const int tid = threadIdx.x;
+    const int lane = lane_id();
+    const int wave = uniform(tid / kWave);
+    const int64_t b = blockIdx.y;
+    const int64_t qi = static_cast<int64_t>(blockIdx.x) * NWQ + wave;
+    const int n = static_cast<int>(P);
+    const bool live = qi < Q;
+    const int64_t row = b * QS + (live ? qi : 0);
+    float qx = 0.f, qy = 0.f, qz = 0.f;
+    if (live) {
+        qx = queries[3 * row];
+        qy = queries[3 * row + 1];
+        qz = queries[3 * row + 2];
+    }
+    int found[NR];
+    bool fin[NR];  // wave-uniform: this radius needs no more points
+    bool done = true;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        found[r] = 0;
+        // d < r2 is impossible for r2 <= 0 (d is never negative) or NaN r2.
+        fin[r] = !live || !(out.r2[r] > 0.f);
+        done = done && fin[r];
+    }
+    const float* pp = points + 3 * b * P;
+    float4 pf[kPer];
+    auto fetch = [&](int base) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const float* pt = pp + 3 * static_cast<int64_t>(min(base + k * NWQ * kWave + tid, n - 1));
+            pf[k] = make_float4(pt[0], pt[1], pt[2], 0.f);
+        }
+    };
+    if (n > 0) fetch(0);
+    for (int base = 0; base < n; base += kTile) {
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) tile[k * NWQ * kWave + tid] = pf[k];
+        __syncthreads();
+        if (base + kTile < n) fetch(base + kTile);  // in flight during the scan
+        auto scan = [&](auto full) {
+#pragma unroll
+            for (int c = 0; c < kBqLdsDepth; c += 2) {
+                const float4 p0 = tile[c * kWave + lane];
+                const float4 p1 = tile[(c + 1) * kWave + lane];
+                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
+                const float d0 = sqdist3(qx, qy, qz, p0.x, p0.y, p0.z);
+                const float d1 = sqdist3(qx, qy, qz, p1.x, p1.y, p1.z);
+                const bool in0 = decltype(full)::value || j0 < n;
+                const bool in1 = decltype(full)::value || j1 < n;
+                bool all = true;
+#pragma unroll
+                for (int r = 0; r < NR; ++r) {
+                    if (fin[r]) continue;
+                    const bool h0 = in0 && d0 < out.r2[r];
+                    const bool h1 = in1 && d1 < out.r2[r];
+                    const uint64_t m0 = ballot(h0), m1 = ballot(h1);
+                    if ((m0 | m1) != 0) {
+                        const uint32_t s0 = static_cast<uint32_t>(found[r] + lanes_below(m0));
+                        const uint32_t s1 =
+                            static_cast<uint32_t>(found[r] + __popcll(m0) + lanes_below(m1));
+                        const uint32_t uk = static_cast<uint32_t>(out.k[r]);
+                        int64_t* oi = out.idx[r] + row * out.k[r];
+                        float* od = out.dist[r] + row * out.k[r];
+                        if (h0 && s0 < uk) {
+                            oi[s0] = static_cast<int64_t>(static_cast<uint32_t>(j0));
+                            od[s0] = d0;
+                        }
+                        if (h1 && s1 < uk) {
+                            oi[s1] = static_cast<int64_t>(static_cast<uint32_t>(j1));
+                            od[s1] = d1;
+                        }
+                        found[r] += __popcll(m0) + __popcll(m1);
+                        fin[r] = found[r] >= out.k[r];
+                    }
+                    all = all && fin[r];
+                }
+                if (all) break;
+            }
+        };
+        if (!done) {
+            if (base + kTile <= n) scan(std::true_type{});
+            else scan(std::false_type{});
+            done = true;
+#pragma unroll
+            for (int r = 0; r < NR; ++r) done = done && fin[r];
+        }
+        if (lane == 0) done_flags[wave] = done ? 1 : 0;
+        __syncthreads();  // flags written; every wave is past its reads of this tile
+        bool all_done = true;
+#pragma unroll
+        for (int w = 0; w < NWQ; ++w) all_done = all_done && done_flags[w] != 0;
+        if (all_done) break;
+    }
+    if (!live) return;
+#pragma unroll
+    for (int r = 0; r < NR; ++r) {
+        int64_t* oi = out.idx[r] + row * out.k[r];
+        float* od = out.dist[r] + row * out.k[r];
+        for (int s = min(found[r], out.k[r]) + lane; s < out.k[r]; s += kWave) {
+            oi[s] = -1;
+            od[s] = 0.f;
+        }
+    }
+}
+
+// The multi-radius search over Q query rows per cloud lying QS rows apart
+// (1 <= nr <= kBqMulti radii; every k >= 1).
+hipError_t ball_query_multi_rows_f32(const float* q, const float* p, const BallMulti& out, int nr,
+                                     int64_t B, int64_t Q, int64_t QS, int64_t P,
+                                     hipStream_t stream) {
     constexpr int NWQ = kBqLdsQueries;
     const int64_t qblocks = (Q + NWQ - 1) / NWQ;
-    if (B < 1 || B > 65535 || Q < 1 || QS < Q || P < 0 || K < 1 || K > INT32_MAX ||
+    if (nr < 1 || nr > kBqMulti || B < 1 || B > 65535 || Q < 1 || QS < Q || P < 0 ||
         P > INT32_MAX - kBqDepth * kWave || qblocks > INT32_MAX)
         return hipErrorInvalidValue;
-    hipLaunchKernelGGL((ball_query_lds_kernel<float, NWQ, false>),
-                       dim3(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B)),
-                       dim3(NWQ * kWave), 0, stream, q, p, nullptr, nullptr, idx, dist2, Q, P,
-                       static_cast<int>(K), r2, nullptr, QS);
+    for (int r = 0; r < nr; ++r)
+        if (out.k[r] < 1 || out.idx[r] == nullptr || out.dist[r] == nullptr) return hipErrorInvalidValue;
+    const dim3 grid(static_cast<uint32_t>(qblocks), static_cast<uint32_t>(B));
+    const dim3 block(NWQ * kWave);
+    switch (nr) {
+        case 1: hipLaunchKernelGGL(ball_query_multi_kernel<1>, grid, block, 0, stream, q, p, out, Q, P, QS); break;
+        case 2: hipLaunchKernelGGL(ball_query_multi_kernel<2>, grid, block, 0, stream, q, p, out, Q, P, QS); break;
+        case 3: hipLaunchKernelGGL(ball_query_multi_kernel<3>, grid, block, 0, stream, q, p, out, Q, P, QS); break;
+        default: hipLaunchKernelGGL(ball_query_multi_kernel<4>, grid, block, 0, stream, q, p, out, Q, P, QS); break;
+    }
     return hipGetLastError();
 }
 

@@ -11,12 +11,15 @@
 // for each chunk of centres a gate kernel (one wave per cloud) waits until
 // its cloud has published the chunk and copies the cloud's centres of the
 // chunk (contiguous rows, not a gather through the indices), and the ball
-// queries of that chunk follow on the free CUs while FPS goes on.  kNN runs once, over all
-// centres, after the last chunk: its lane kernel gives each workgroup 64
-// queries against the whole cloud, so its duration does not shrink with the
-// number of queries (measured at config 2: about 62 us for 128 centres per
-// cloud, 86 us for 1024), and per-chunk launches would serialise that cost.  Results are those
-// of the separate calls, bit for bit: the same kernels compute each query.
+// queries of that chunk follow on the free CUs while FPS goes on, every
+// radius in one scan (ball_query_multi_kernel: each distance computed once,
+// each radius's first-K list as its own search would build it).  kNN runs
+// once, over all centres, after the last chunk: its lane kernel gives each
+// workgroup 64 queries against the whole cloud, so its duration does not
+// shrink with the number of queries (measured at config 2: about 62 us for
+// 128 centres per cloud, 86 us for 1024), and per-chunk launches would
+// serialise that cost.  Results are those of the separate calls, bit for
+// bit: each query's distances and tests are the same.
 //
 // The only waiting is the gates' bounded poll of the progress words; FPS
 // waits on nothing, and its workgroups are resident before any chunk can be
@@ -44,9 +47,6 @@ namespace pointops {
 hipError_t fps_dense_progress(const float* xyz, int64_t* out, int64_t B, int64_t N,
                               int64_t npoint, int64_t start, int skip, uint64_t* progress,
                               uint64_t tag, int64_t chunk, float* centres, hipStream_t stream);
-hipError_t ball_query_rows_f32(const float* q, const float* p, int64_t* idx, float* dist2,
-                               int64_t B, int64_t Q, int64_t QS, int64_t P, int64_t K, float r2,
-                               hipStream_t stream);
 hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist, int64_t* idx,
                               void* workspace, int64_t B, int64_t M, int64_t QS, int64_t N,
                               int64_t K, hipStream_t stream);
@@ -185,7 +185,8 @@ hipError_t pointops_fps_query_pipeline_f32(
         (knn_k > 0 && (knn_dist == nullptr || knn_idx == nullptr)))
         return hipErrorInvalidValue;
     for (int64_t r = 0; r < nball; ++r)
-        if (ball_k[r] < 1 || ball_idx[r] == nullptr || ball_dist2[r] == nullptr)
+        if (ball_k[r] < 1 || ball_k[r] > INT32_MAX || ball_idx[r] == nullptr ||
+            ball_dist2[r] == nullptr)
             return hipErrorInvalidValue;
     const int64_t chunks = (npoint + chunk - 1) / chunk;
     uint64_t* progress = static_cast<uint64_t*>(workspace);
@@ -214,10 +215,18 @@ hipError_t pointops_fps_query_pipeline_f32(
                            query_stream, progress, static_cast<uint64_t>(c + 1), staged, centres,
                            status, npoint, m0, m1, limit);
         if ((err = hipGetLastError()) != hipSuccess) return err;
-        for (int64_t r = 0; r < nball; ++r) {
-            err = ball_query_rows_f32(centres + 3 * m0, xyz, ball_idx[r] + m0 * ball_k[r],
-                                      ball_dist2[r] + m0 * ball_k[r], B, mc, npoint, N, ball_k[r],
-                                      radii_sq[r], query_stream);
+        // The radii in groups of up to kBqMulti, each group in one scan.
+        for (int64_t r0 = 0; r0 < nball; r0 += kBqMulti) {
+            const int nr = static_cast<int>(nball - r0 < kBqMulti ? nball - r0 : kBqMulti);
+            BallMulti out{};
+            for (int r = 0; r < nr; ++r) {
+                out.idx[r] = ball_idx[r0 + r] + m0 * ball_k[r0 + r];
+                out.dist[r] = ball_dist2[r0 + r] + m0 * ball_k[r0 + r];
+                out.k[r] = static_cast<int>(ball_k[r0 + r]);
+                out.r2[r] = radii_sq[r0 + r];
+            }
+            err = ball_query_multi_rows_f32(centres + 3 * m0, xyz, out, nr, B, mc, npoint, N,
+                                            query_stream);
             if (err != hipSuccess) return err;
         }
     }

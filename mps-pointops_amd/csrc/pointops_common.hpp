@@ -221,6 +221,20 @@ __device__ __forceinline__ CloudBlock cloud_block(uint32_t per_cloud) {
     return {blk % per_cloud, blk / per_cloud};
 }
 
+// ball_query.hip: up to kBqMulti ball queries around the same centres in one
+// scan (radius r: r2[r] as pointops_ball_query_f32 takes it, k[r] slots,
+// outputs (B, QS, k[r]) written at the query rows).
+constexpr int kBqMulti = 4;
+struct BallMulti {
+    int64_t* idx[kBqMulti];
+    float* dist[kBqMulti];
+    int k[kBqMulti];
+    float r2[kBqMulti];
+};
+hipError_t ball_query_multi_rows_f32(const float* q, const float* p, const BallMulti& out, int nr,
+                                     int64_t B, int64_t Q, int64_t QS, int64_t P,
+                                     hipStream_t stream);
+
 // ball_query.hip: the index-order float32 ball query without lengths (the
 // LDS-staged kernel, B <= 65535), every workgroup returning at once when
 // `skip` is non-null and *skip != 0 at launch time.

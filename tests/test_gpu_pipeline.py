@@ -48,6 +48,8 @@ C2 = (bench.C2_NPOINT, tuple(r for r, _ in bench.C2_RADII), tuple(k for _, k in 
     (2, 1000, 8, 1000, 4096, (0.2, 0.5), (4, 64), 32, 0, True),   # one chunk, every point
     (5, 8192, 9, 300, 64, (0.05,), (32,), 0, 3, False),   # no kNN, the largest cloud
     (4, 2048, 10, 1, 1, (), (), 1, 0, False),              # one sample, no ball query
+    # Six radii (two multi-radius scans), K above 128, a zero and a huge radius.
+    (3, 3000, 12, 200, 64, (0.1, 0.0, 0.3, 0.05, 2.0, 0.2), (16, 8, 200, 1, 3, 65), 8, 0, False),
 ])
 def test_fps_ball_knn_matches_separate_calls(B, N, seed, npoint, chunk, radii, ks, knn_k, start,
                                              skip):
