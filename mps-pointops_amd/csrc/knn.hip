@@ -363,9 +363,11 @@ __device__ __forceinline__ void lane_publish_and_merge(
 //
 // knn_window_prep_kernel (one workgroup per cloud) counting-sorts the
 // references by a 16 x 16 x 16 Morton cell of the finite references'
-// bounding box and writes their coordinates in that order, and gives every
-// query a "home": the middle of its cell's range in the sorted order (or where
-// the cell would start).  knn3_lane_kernel then takes, per query, the window
+// bounding box and writes their coordinates in that order, with the grid
+// (box and cell starts); it reads no query, so it can run before the queries
+// exist.  In knn3_lane_kernel every query takes a "home": the middle of its
+// cell's range in the sorted order (or where the cell would start), and
+// then, per query, the window
 // of r*K sorted references around its home (r = min(8, N/K)) in K strided
 // groups {w0 + g + j*K : j < r}; wave w takes the c groups g = w mod NW and
 // the c-th smallest key among their c*r references, and the limit is the
@@ -382,19 +384,25 @@ constexpr int kWindowCells = 4096;  // 16^3 Morton cells
 constexpr int kWindowGroups = 8;    // window references per group (r <= 8)
 constexpr int kWindowChunk = 8;     // of which loaded at once
 
+// Per cloud, the Morton grid of the sort: lo[3] and scale[3] (the first
+// 8 words, as floats), then the cells' starts in the sorted order
+// (kWindowCells + 1 ints).
+constexpr int kWindowGridWords = 8 + ((kWindowCells + 1 + 63) & ~63);
+
 struct WindowLayout {
     float4* sorted;  // [B][N]: coordinates in Morton order (w unused)
-    int* home;       // [B][M]: per query row, a position in the sorted order
+    int* grid;       // [B][kWindowGridWords]
 };
 
 __host__ __device__ inline size_t window_layout_bytes(int64_t B, int64_t M, int64_t N,
                                                       WindowLayout* out, char* base) {
+    (void)M;
     const size_t sorted_bytes = (static_cast<size_t>(B * N) * sizeof(float4) + 255) & ~size_t(255);
     if (out != nullptr) {
         out->sorted = reinterpret_cast<float4*>(base);
-        out->home = reinterpret_cast<int*>(base + sorted_bytes);
+        out->grid = reinterpret_cast<int*>(base + sorted_bytes);
     }
-    return sorted_bytes + static_cast<size_t>(B * M) * sizeof(int);
+    return sorted_bytes + static_cast<size_t>(B * kWindowGridWords) * sizeof(int);
 }
 
 __device__ __forceinline__ uint32_t window_cell(float x, float y, float z, const float (&lo)[3],
@@ -410,10 +418,8 @@ __device__ __forceinline__ uint32_t window_cell(float x, float y, float z, const
 }
 
 __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
-    const float* __restrict__ query, const float* __restrict__ ref, WindowLayout L, int M, int N,
-    int64_t QS) {
+    const float* __restrict__ ref, WindowLayout L, int N) {
     constexpr int RPT = kWindowMaxRefs / kWindowPrepThreads;
-    constexpr int QPT = kWindowMaxQueries / kWindowPrepThreads;
     constexpr int CPT = kWindowCells / kWindowPrepThreads;  // cells per thread in the scan
     constexpr int NWV = kWindowPrepThreads / kWave;
     __shared__ int cell_off[kWindowCells + 1];
@@ -423,13 +429,12 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
     const int lane = tid % kWave, wave = tid / kWave;
     const int64_t b = blockIdx.x;
     const float* rp = ref + 3 * b * N;
-    const float* qp = query + 3 * b * QS;  // QS: query rows between clouds
 
     for (int c = tid; c <= kWindowCells; c += kWindowPrepThreads) cell_off[c] = 0;
-    // References and queries are requested together, without branches (an
-    // index past the end reads the last point again), so that every load is
-    // in flight before the first wait.
-    float px[RPT], py[RPT], pz[RPT], qx[QPT], qy[QPT], qz[QPT];
+    // The references are requested together, without branches (an index
+    // past the end reads the last point again), so that every load is in
+    // flight before the first wait.
+    float px[RPT], py[RPT], pz[RPT];
     // Rounds k with no point at all are skipped (a uniform branch).
 #pragma unroll
     for (int k = 0; k < RPT; ++k) {
@@ -439,15 +444,6 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
         px[k] = rp[3 * j];
         py[k] = rp[3 * j + 1];
         pz[k] = rp[3 * j + 2];
-    }
-#pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        qx[k] = qy[k] = qz[k] = 0.f;
-        if (k * kWindowPrepThreads >= M) continue;
-        const int m = min(tid + k * kWindowPrepThreads, M - 1);
-        qx[k] = qp[3 * m];
-        qy[k] = qp[3 * m + 1];
-        qz[k] = qp[3 * m + 2];
     }
     float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
@@ -523,22 +519,20 @@ __global__ __launch_bounds__(kWindowPrepThreads) void knn_window_prep_kernel(
         const int j = tid + k * kWindowPrepThreads;
         if (j < N) sorted[cell_off[cell[k]] + rank[k]] = make_float4(px[k], py[k], pz[k], 0.f);
     }
-    int* home = L.home + b * M;
-#pragma unroll
-    for (int k = 0; k < QPT; ++k) {
-        const int m = tid + k * kWindowPrepThreads;
-        if (m < M) {
-            const int c = static_cast<int>(window_cell(qx[k], qy[k], qz[k], lo, scale));
-            home[m] = min((cell_off[c] + cell_off[c + 1]) / 2, N - 1);
-        }
+    // The grid, from which each query finds its home in the lane kernel.
+    int* grid = L.grid + b * kWindowGridWords;
+    if (tid < 3) {
+        grid[tid] = f2i(lo[tid]);
+        grid[3 + tid] = f2i(scale[tid]);
     }
+    for (int c = tid; c <= kWindowCells; c += kWindowPrepThreads) grid[8 + c] = cell_off[c];
 }
 
 template <int KMAX, int NW, int CAP>
 __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
     const float* __restrict__ query, const float* __restrict__ ref, float* __restrict__ out_dist,
     int64_t* __restrict__ out_idx, int64_t M, int64_t N, int K, const float4* __restrict__ sorted,
-    const int* __restrict__ home, int64_t QS) {
+    const int* __restrict__ grid, int64_t QS) {
     // Per wave: the candidate buffer during the scan, then the final list.
     __shared__ uint2 lds[NW][KMAX > CAP ? KMAX : CAP][kWave];
     __shared__ uint32_t window_max[kWave];  // per lane: the Morton-window limit
@@ -590,7 +584,16 @@ __global__ __launch_bounds__(NW * kWave) void knn3_lane_kernel(
         const float4* sp = sorted + b * N;
         const int n = static_cast<int>(N);
         const int r = min(kWindowGroups, n / K);
-        const int h = active ? home[b * M + m] : 0;
+        // The query's home: the middle of its Morton cell's range in the
+        // sorted order.
+        int h = 0;
+        if (active) {
+            const int* g = grid + b * kWindowGridWords;
+            const float glo[3] = {i2f(g[0]), i2f(g[1]), i2f(g[2])};
+            const float gsc[3] = {i2f(g[3]), i2f(g[4]), i2f(g[5])};
+            const int c = static_cast<int>(window_cell(qx, qy, qz, glo, gsc));
+            h = min((g[8 + c] + g[8 + c + 1]) / 2, n - 1);
+        }
         const int w0 = min(max(h - r * K / 2, 0), n - r * K);
         // This wave's groups g = wave mod NW (c of them) hold c x r distinct
         // references; the c-th smallest of their keys bounds c of them, so
@@ -856,7 +859,7 @@ hipError_t launch_lane(const float* query, const float* ref, float* dist, int64_
     constexpr int CAP = KMAX <= 16 ? 16 : 32;
     hipLaunchKernelGGL((knn3_lane_kernel<KMAX, NW, CAP>), grid, dim3(NW * kWave), 0, stream, query,
                        ref, dist, idx, M, N, K, window ? window->sorted : nullptr,
-                       window ? window->home : nullptr, QS > 0 ? QS : M);
+                       window ? window->grid : nullptr, QS > 0 ? QS : M);
     return hipGetLastError();
 }
 
@@ -925,6 +928,22 @@ namespace pointops {
 // queries and both outputs -- lie QS rows apart (M consecutive centres of a
 // (B, QS, 3) tensor and of its (B, QS, K) outputs).  `workspace` holds
 // pointops_knn3_windowed_workspace_bytes(B, M, N) bytes.
+// The windowed search in two launches: knn3_window_sort (the references of
+// every cloud in Morton order, and the grid, into `workspace`; it depends on
+// the references only) and knn3_windowed_rows (the queries -- M rows per
+// cloud lying QS rows apart -- over a workspace the sort has filled for the
+// same references, B and N).
+hipError_t knn3_window_sort(const float* ref, void* workspace, int64_t B, int64_t M, int64_t N,
+                            hipStream_t stream) {
+    if (B < 1 || B > INT32_MAX || N < 1 || N > kWindowMaxRefs || workspace == nullptr)
+        return hipErrorInvalidValue;
+    WindowLayout L;
+    window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
+    hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
+                       dim3(kWindowPrepThreads), 0, stream, ref, L, static_cast<int>(N));
+    return hipGetLastError();
+}
+
 hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist, int64_t* idx,
                               void* workspace, int64_t B, int64_t M, int64_t QS, int64_t N,
                               int64_t K, hipStream_t stream) {
@@ -934,11 +953,6 @@ hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist,
         return hipErrorInvalidValue;
     WindowLayout L;
     window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
-    hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
-                       dim3(kWindowPrepThreads), 0, stream, query, ref, L, static_cast<int>(M),
-                       static_cast<int>(N), QS);
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
     const int k = static_cast<int>(K);
     if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, k, stream, &L, QS);
     if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, k, stream, &L, QS);
@@ -972,17 +986,9 @@ hipError_t pointops_knn3_windowed(const float* query, const float* ref, float* d
     if (N > kWindowMaxRefs || M > kWindowMaxQueries || workspace == nullptr || B > INT32_MAX ||
         (M + kWave - 1) / kWave * B > INT32_MAX)
         return hipErrorInvalidValue;
-    WindowLayout L;
-    window_layout_bytes(B, M, N, &L, static_cast<char*>(workspace));
-    hipLaunchKernelGGL(knn_window_prep_kernel, dim3(static_cast<uint32_t>(B)),
-                       dim3(kWindowPrepThreads), 0, stream, query, ref, L, static_cast<int>(M),
-                       static_cast<int>(N), M);
-    const hipError_t err = hipGetLastError();
+    const hipError_t err = knn3_window_sort(ref, workspace, B, M, N, stream);
     if (err != hipSuccess) return err;
-    const int k = static_cast<int>(K);
-    if (K <= 8) return launch_lane<8>(query, ref, dist, idx, B, M, N, k, stream, &L);
-    if (K <= 16) return launch_lane<16>(query, ref, dist, idx, B, M, N, k, stream, &L);
-    return launch_lane<32>(query, ref, dist, idx, B, M, N, k, stream, &L);
+    return knn3_windowed_rows(query, ref, dist, idx, workspace, B, M, M, N, K, stream);
 }
 
 hipError_t pointops_knn_feat(const float* query, const float* ref, float* dist, int64_t* idx,

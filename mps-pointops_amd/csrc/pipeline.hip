@@ -47,6 +47,8 @@ namespace pointops {
 hipError_t fps_dense_progress(const float* xyz, int64_t* out, int64_t B, int64_t N,
                               int64_t npoint, int64_t start, int skip, uint64_t* progress,
                               uint64_t tag, int64_t chunk, float* centres, hipStream_t stream);
+hipError_t knn3_window_sort(const float* ref, void* workspace, int64_t B, int64_t M, int64_t N,
+                            hipStream_t stream);
 hipError_t knn3_windowed_rows(const float* query, const float* ref, float* dist, int64_t* idx,
                               void* workspace, int64_t B, int64_t M, int64_t QS, int64_t N,
                               int64_t K, hipStream_t stream);
@@ -207,6 +209,12 @@ hipError_t pointops_fps_query_pipeline_f32(
     err = fps_dense_progress(xyz, samples, B, N, npoint, start_idx, skip_near_origin != 0,
                              progress, 0, chunk, staged, fps_stream);
     if (err != hipSuccess) return err;
+    // kNN's sort of the references needs the cloud only: it runs first on
+    // the query stream, beside FPS.
+    if (knn_k > 0) {
+        err = knn3_window_sort(xyz, knn_ws, B, npoint, N, query_stream);
+        if (err != hipSuccess) return err;
+    }
     for (int64_t c = 0; c < chunks; ++c) {
         const int64_t m0 = c * chunk;
         const int64_t m1 = m0 + chunk < npoint ? m0 + chunk : npoint;
