@@ -158,12 +158,13 @@ class KernelTimer:
 
 
 def fps_kernel_name(n: int) -> str:
-    """Template instance fps_tiled_kernel<P,512,PO> that a cloud of n points
-    uses (PO: tiles per wave of the first half, 9 for P = 8)."""
+    """Template instance of the dense FPS kernel that a cloud of n points
+    uses: fps_lead_kernel<P> up to 4096 points (P points per follower lane),
+    fps_tiled_kernel<16,512,16> up to 8192."""
     p = 1
     while p * 512 < n:
         p *= 2
-    return f"fps_tiled_kernel<{p},512,{9 if p == 8 else p}>"
+    return f"fps_lead_kernel<{p}>" if p <= 8 else f"fps_tiled_kernel<{p},512,{p}>"
 
 
 def profiled_traffic(kernel: str, workload: str):
@@ -549,8 +550,8 @@ def run(args) -> dict:
         "ops": {"fps": op(t_fps, fps_ops), "ball_query_x3": op(t_ball, ball_ops),
                 "knn": op(t_knn, knn_ops)},
         "step": "mps_pointops.fps_ball_knn: FPS, centre gather, 3 ball queries and kNN of one "
-                "batch, the ball queries of each 256-centre chunk overlapped with the rest of FPS, "
-                "kNN once after the last chunk",
+                "batch, the ball queries of each 256-centre chunk (all 3 radii in one scan) "
+                "overlapped with the rest of FPS, kNN once after the last chunk",
         "sequential_not_in_value": {
             "what": "the same batch as separate calls on one stream (FPS, then the ball queries "
                     "and kNN on centres gathered beforehand, outside the timed region)",
