@@ -423,6 +423,13 @@ def run(args) -> dict:
     t_fps = timer.time(fps, reps)
     t_ball = timer.time(balls, reps)
     t_knn = timer.time(knn, reps)
+    # The same three ball queries as one multi-radius scan (not in value).
+    multi = mp.ball_query_multi(centres, xyz, radii, ks)
+    for (radius, k), (d, i) in zip(C2_RADII, multi):
+        rd, ri = mp.ball_query(centres, xyz, radius, k)
+        if not (torch.equal(i, ri) and torch.equal(d, rd)):
+            raise SystemExit("bench: ball_query_multi differs from the separate ball queries")
+    t_ball_multi = timer.time(lambda: mp.ball_query_multi(centres, xyz, radii, ks), reps)
 
     # Algorithmic work (FP32 ops): FPS 9 per point-step; ball query 8 per
     # scanned pair (up to the K-th hit); kNN 8 per pair (all pairs).
@@ -549,6 +556,11 @@ def run(args) -> dict:
         },
         "ops": {"fps": op(t_fps, fps_ops), "ball_query_x3": op(t_ball, ball_ops),
                 "knn": op(t_knn, knn_ops)},
+        "ball_query_x3_one_scan_not_in_value": {
+            "what": "mps_pointops.ball_query_multi: the 3 radii over all 1024 centres in one "
+                    "scan (each pair's distance computed once), the same outputs bit for bit",
+            **op(t_ball_multi, ball_ops),
+        },
         "step": "mps_pointops.fps_ball_knn: FPS, centre gather, 3 ball queries and kNN of one "
                 "batch, the ball queries of each 256-centre chunk (all 3 radii in one scan) "
                 "overlapped with the rest of FPS, kNN once after the last chunk",
@@ -711,8 +723,8 @@ def run_other(args) -> dict:
 
 
 def probe() -> None:
-    """One pass of each config-2 kernel (the metric's FPS, ball queries and
-    kNN, then three_nn and three_interpolate forward and backward of C=128
+    """One pass of each config-2 kernel (the metric's FPS, ball queries --
+    separately and in one multi-radius scan -- and kNN, then three_nn and three_interpolate forward and backward of C=128
     features, and the set-abstraction layer: the pointnet2-form ball query
     (0.2, 32) and the grouping of C=64 features forward and backward) plus a
     256 MiB device copy, three times, for hardware-counter runs (the copy's
@@ -736,6 +748,7 @@ def probe() -> None:
         centres = xyz.gather(1, idx[..., None].expand(-1, -1, 3)).contiguous()
         for radius, k in C2_RADII:
             mp.ball_query(centres, xyz, radius, k)
+        mp.ball_query_multi(centres, xyz, [r for r, _ in C2_RADII], [k for _, k in C2_RADII])
         mp.knn(centres, xyz, C2_KNN_K)
         tn_d, tn_i = mp.three_nn(xyz, centres)
         inv = 1.0 / (tn_d + 1e-8)
@@ -746,7 +759,7 @@ def probe() -> None:
         sa_layer(xyz, centres, sa_feats).backward(sa_up)
         dst.copy_(src)
     torch.cuda.synchronize()
-    print("probe: 3 x (fps, 3 ball queries, knn, three_nn, three_interpolate fwd+bwd, "
+    print("probe: 3 x (fps, 3 ball queries, their one-scan form, knn, three_nn, three_interpolate fwd+bwd, "
           "QueryAndGroup fwd+bwd, 256 MiB copy) done", flush=True)
 
 

@@ -168,6 +168,22 @@ hipError_t pointops_ball_query_f16(const uint16_t *queries, const uint16_t *poin
                                    const int64_t *query_lengths, const int64_t *point_lengths,
                                    int64_t *idx, float *dist2, int64_t B, int64_t Q, int64_t P,
                                    int64_t K, float radius_sq, hipStream_t stream);
+/* Ball queries of nball (<= 8) radii around the same queries in one scan
+ * per kBqMulti = 4 radii: each radius r's (idx[r], dist2[r]) of shape
+ * (B,Q,ks[r]) equals pointops_ball_query_f32(queries, points, NULL, NULL,
+ * idx[r], dist2[r], B, Q, P, ks[r], radii_sq[r]) bit for bit (first ks[r]
+ * hits in index order, d < radius_sq, -1 / 0 padding); a radius with
+ * ks[r] == 0 writes nothing.  Each pair's distance is computed once for all
+ * radii, and a scan stops when every radius has its hits.  The arrays
+ * radii_sq, ks, idx and dist2 are host arrays of nball entries; B <= 65535.
+ * A multi-scale-grouping layer asks several radii around one set of centres
+ * (the config-2 workload: r = 0.1, 0.2, 0.4 with K = 16, 32, 128): this
+ * replaces its per-radius ops.ball_query calls (ops.py:208-227, one
+ * _ball_query_mps.py:139-162 call each). */
+hipError_t pointops_ball_query_multi_f32(const float *queries, const float *points, int64_t nball,
+                                         const float *radii_sq, const int64_t *ks,
+                                         int64_t *const *idx, float *const *dist2, int64_t B,
+                                         int64_t Q, int64_t P, hipStream_t stream);
 /* The same float32 query without lengths in pointnet2_ops' form: int32
  * indices only, (B,Q,K), slots past the hits repeating the query's first hit
  * and all 0 for a query without one.  Replaces compat.py:76-85 (the ball

@@ -520,6 +520,38 @@ hipError_t pointops_ball_query_f32(const float* queries, const float* points,
                               radius_sq, nullptr, stream);
 }
 
+hipError_t pointops_ball_query_multi_f32(const float* queries, const float* points, int64_t nball,
+                                         const float* radii_sq, const int64_t* ks,
+                                         int64_t* const* idx, float* const* dist2, int64_t B,
+                                         int64_t Q, int64_t P, hipStream_t stream) {
+    if (nball < 0 || nball > 8 || B < 0 || Q < 0 || P < 0 || P > INT32_MAX - kBqDepth * kWave ||
+        (nball > 0 && (radii_sq == nullptr || ks == nullptr || idx == nullptr || dist2 == nullptr)))
+        return hipErrorInvalidValue;
+    for (int64_t r = 0; r < nball; ++r)
+        if (ks[r] < 0 || ks[r] > INT32_MAX || (ks[r] > 0 && (idx[r] == nullptr || dist2[r] == nullptr)))
+            return hipErrorInvalidValue;
+    if (B == 0 || Q == 0) return hipSuccess;
+    if (queries == nullptr || points == nullptr || B > 65535) return hipErrorInvalidValue;
+    // The radii with K >= 1 in order, kBqMulti to a scan.
+    BallMulti out{};
+    int nr = 0;
+    for (int64_t r = 0; r <= nball; ++r) {
+        if (r < nball && ks[r] > 0) {
+            out.idx[nr] = idx[r];
+            out.dist[nr] = dist2[r];
+            out.k[nr] = static_cast<int>(ks[r]);
+            out.r2[nr] = radii_sq[r];
+            ++nr;
+        }
+        if (nr == kBqMulti || (r == nball && nr > 0)) {
+            const hipError_t err = ball_query_multi_rows_f32(queries, points, out, nr, B, Q, Q, P, stream);
+            if (err != hipSuccess) return err;
+            nr = 0;
+        }
+    }
+    return hipSuccess;
+}
+
 hipError_t pointops_ball_query_pn2_f32(const float* queries, const float* points, int32_t* idx,
                                        int64_t B, int64_t Q, int64_t P, int64_t K, float radius_sq,
                                        hipStream_t stream) {

@@ -9,11 +9,11 @@ gfx950 kernel from libpointops_hip.so.
 
 from . import flat
 from .chamfer import chamfer_distance
-from .ops import ball_query, fps_ball_knn, furthest_point_sample, knn
+from .ops import ball_query, ball_query_multi, fps_ball_knn, furthest_point_sample, knn
 from .pointnet2 import three_interpolate, three_nn
 
 __all__ = [
-    "ball_query", "chamfer_distance", "flat", "fps_ball_knn", "furthest_point_sample", "knn",
+    "ball_query", "ball_query_multi", "chamfer_distance", "flat", "fps_ball_knn", "furthest_point_sample", "knn",
     "three_interpolate", "three_nn",
 ]
 __version__ = "1.0.0"

@@ -39,6 +39,7 @@ _SIGNATURES: dict[str, list] = {
     "pointops_knn_feat": [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _vp],
     "pointops_knn_flat": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp],
     "pointops_ball_query_f32": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
+    "pointops_ball_query_multi_f32": [_vp, _vp, _i64, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp],
     "pointops_ball_query_f16": [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _f32, _vp],
     "pointops_radius_flat_f32": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],
     "pointops_radius_flat_f16": [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _f32, _i32, _vp],

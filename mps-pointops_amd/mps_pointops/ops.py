@@ -196,6 +196,45 @@ def ball_query(query: Tensor, ref: Tensor, radius: float, K: int) -> tuple[Tenso
     return result.distances, result.indices
 
 
+def ball_query_multi(query: Tensor, ref: Tensor, radii, nsamples) -> list[tuple[Tensor, Tensor]]:
+    """Ball queries of several radii around the same queries in one scan:
+    ``[ball_query(query, ref, r, k) for r, k in zip(radii, nsamples)]``, the
+    same tensors bit for bit (ops.py:208-227 per radius), each pair's
+    distance computed once for up to four radii.  float32 (B, M, 3) and
+    (B, N, 3), at most 8 radii, B <= 65535; no autograd (the distances do
+    not require grad)."""
+    radii, nsamples = list(radii), list(nsamples)
+    if len(radii) != len(nsamples) or len(radii) > 8:
+        raise ValueError("radii and nsamples must have the same length, at most 8")
+    if query.dim() != 3 or ref.dim() != 3 or query.shape[-1] != 3 or ref.shape[-1] != 3:
+        raise ValueError("query and ref must have shapes (B, M, 3) and (B, N, 3)")
+    if query.shape[0] != ref.shape[0]:
+        raise ValueError("query and ref must have the same batch size")
+    if query.device != ref.device:
+        raise ValueError(f"query and ref are on different devices: {query.device} and {ref.device}")
+    if query.dtype != torch.float32 or ref.dtype != torch.float32:
+        raise TypeError("ball_query_multi takes float32 coordinates")
+    radii_sq = [_checked_radius_and_k(r, k)[1] for r, k in zip(radii, nsamples)]
+    B, M, _ = query.shape
+    N = ref.shape[1]
+    if B > 65_535:
+        raise ValueError(f"ball_query_multi takes at most 65535 clouds, got {B}")
+    _native.require_device(query.device)
+    q, r = query.detach().contiguous(), ref.detach().contiguous()
+    dev = q.device
+    outs = [(torch.empty(B, M, k, dtype=torch.float32, device=dev),
+             torch.empty(B, M, k, dtype=torch.long, device=dev)) for k in nsamples]
+    n = len(radii)
+    c_radii = (ctypes.c_float * max(n, 1))(*radii_sq)
+    c_ks = (ctypes.c_int64 * max(n, 1))(*nsamples)
+    c_idx = (ctypes.c_void_p * max(n, 1))(*[i.data_ptr() for _, i in outs])
+    c_d2 = (ctypes.c_void_p * max(n, 1))(*[d.data_ptr() for d, _ in outs])
+    with torch.cuda.device(dev):
+        _native.call("pointops_ball_query_multi_f32", q.data_ptr(), r.data_ptr(), n, c_radii,
+                     c_ks, c_idx, c_d2, B, M, N, _native.stream(dev))
+    return outs
+
+
 # Streams beside the caller's stream for fps_ball_knn, one per (device,
 # caller stream), default priority: calls issued from different streams keep
 # independent query queues.

@@ -64,6 +64,50 @@ def test_capi_rejects_bad_arguments_before_any_launch():
     assert lib.pointops_three_interpolate(None, None, None, None, 1, 2, 0, 4, None) == 1  # M == 0
 
 
+def test_ball_query_multi_rejects_bad_arguments():
+    """The multi-radius entry checks every radius before any launch: at most
+    8 radii, K in [0, 2^31), an output pair for each radius with K >= 1;
+    empty work succeeds."""
+    from mps_pointops import _native
+
+    lib = _native.library()
+    r2 = (ctypes.c_float * 9)(*([0.01] * 9))
+    ks = (ctypes.c_int64 * 9)(*([4] * 9))
+    ptrs = (ctypes.c_void_p * 9)(*([8] * 9))
+    nul = (ctypes.c_void_p * 9)()
+    f = lib.pointops_ball_query_multi_f32
+    assert f(None, None, 9, r2, ks, ptrs, ptrs, 1, 1, 1, None) == 1            # > 8 radii
+    assert f(None, None, 2, None, ks, ptrs, ptrs, 1, 1, 1, None) == 1          # no radii array
+    assert f(None, None, 2, r2, ks, nul, ptrs, 1, 1, 1, None) == 1             # no idx output
+    bad = (ctypes.c_int64 * 2)(4, -1)
+    assert f(None, None, 2, r2, bad, ptrs, ptrs, 1, 1, 1, None) == 1           # K < 0
+    big = (ctypes.c_int64 * 1)(1 << 31)
+    assert f(None, None, 1, r2, big, ptrs, ptrs, 1, 1, 1, None) == 1           # K >= 2^31
+    assert f(None, None, 2, r2, ks, ptrs, ptrs, 0, 5, 5, None) == 0            # B == 0
+    assert f(None, None, 2, r2, ks, ptrs, ptrs, 3, 0, 5, None) == 0            # Q == 0
+    assert f(None, None, 2, r2, ks, ptrs, ptrs, 65536, 1, 5, None) == 1        # B > 65535
+    zero = (ctypes.c_int64 * 2)(0, 0)
+    assert f(None, None, 2, r2, zero, nul, nul, 2, 3, 5, None) == 1            # no coordinates
+
+
+def test_ball_query_multi_python_validation():
+    import mps_pointops as mp
+
+    q, r = torch.zeros(1, 4, 3), torch.zeros(1, 8, 3)
+    with pytest.raises(ValueError, match="same length"):
+        mp.ball_query_multi(q, r, [0.1, 0.2], [4])
+    with pytest.raises(ValueError, match="at most 8"):
+        mp.ball_query_multi(q, r, [0.1] * 9, [4] * 9)
+    with pytest.raises(ValueError, match="radius"):
+        mp.ball_query_multi(q, r, [-1.0], [4])
+    with pytest.raises(ValueError, match="shapes"):
+        mp.ball_query_multi(q[..., :2], r, [0.1], [4])
+    with pytest.raises(TypeError, match="float32"):
+        mp.ball_query_multi(q.double(), r.double(), [0.1], [4])
+    with pytest.raises(ValueError, match="ROCm"):
+        mp.ball_query_multi(q, r, [0.1], [4])  # CPU tensors are not computed
+
+
 def test_scratch_size_queries():
     from mps_pointops import _native
 
