@@ -122,6 +122,7 @@ def make_c5(seed: int = 5, B: int = 32, P: int = 8192) -> tuple[torch.Tensor, to
 C2_RADII = ((0.1, 16), (0.2, 32), (0.4, 128))
 C2_NPOINT = 1024
 C2_KNN_K = 16
+C2_CHUNK = 128  # centres per chunk of the overlapped step (mps_pointops.fps_ball_knn)
 
 # ---------------------------------------------------------------- timing
 
@@ -395,7 +396,7 @@ def run(args) -> dict:
     wall_sequential = timed_steps(step, args.steps, args.warmup)
 
     # The same batch's FPS, centre gather, ball queries and kNN in one call
-    # (mps_pointops.fps_ball_knn): the ball queries of each 256-centre chunk
+    # (mps_pointops.fps_ball_knn): the ball queries of each C2_CHUNK-centre chunk
     # run as soon as FPS has sampled it, on the CUs FPS leaves free, and kNN
     # once after the last chunk.  Same outputs,
     # bit for bit (tests/test_gpu_pipeline.py); this is the timed step.
@@ -403,7 +404,7 @@ def run(args) -> dict:
     ks = [k for _, k in C2_RADII]
 
     def fused_step():
-        state["fused"] = mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
+        state["fused"] = mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=C2_CHUNK)
 
     wall = timed_steps(fused_step, args.steps, args.warmup)
     # The last timed call's outputs against the separate calls, bit for bit
@@ -562,7 +563,7 @@ def run(args) -> dict:
             **op(t_ball_multi, ball_ops),
         },
         "step": "mps_pointops.fps_ball_knn: FPS, centre gather, 3 ball queries and kNN of one "
-                "batch, the ball queries of each 256-centre chunk (all 3 radii in one scan) "
+                f"batch, the ball queries of each {C2_CHUNK}-centre chunk (all 3 radii in one scan) "
                 "overlapped with the rest of FPS, kNN once after the last chunk",
         "sequential_not_in_value": {
             "what": "the same batch as separate calls on one stream (FPS, then the ball queries "
@@ -765,7 +766,7 @@ def probe() -> None:
 
 def pipeline_trace(calls: int = 20) -> None:
     """The timed step alone (mps_pointops.fps_ball_knn at config 2, chunk
-    256, as the benchmark times it) `calls` times after two warm-up calls,
+    C2_CHUNK, as the benchmark times it) `calls` times after two warm-up calls,
     for a kernel trace of the overlapped front end."""
     import mps_pointops as mp
 
@@ -773,9 +774,9 @@ def pipeline_trace(calls: int = 20) -> None:
     radii = [r for r, _ in C2_RADII]
     ks = [k for _, k in C2_RADII]
     for _ in range(2 + calls):
-        mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=256)
+        mp.fps_ball_knn(xyz, C2_NPOINT, radii, ks, C2_KNN_K, chunk=C2_CHUNK)
     torch.cuda.synchronize()
-    print(f"pipeline: {2 + calls} x fps_ball_knn (chunk 256) done", flush=True)
+    print(f"pipeline: {2 + calls} x fps_ball_knn (chunk {C2_CHUNK}) done", flush=True)
 
 
 def main() -> None:
@@ -790,7 +791,7 @@ def main() -> None:
     parser.add_argument("--config", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
                         help="workload; the headline metric (and the default) is c2")
     parser.add_argument("--pipeline-trace", action="store_true",
-                        help="run only the timed step (fps_ball_knn, chunk 256) 22 times, "
+                        help=f"run only the timed step (fps_ball_knn, chunk {C2_CHUNK}) 22 times, "
                              "for a kernel trace")
     parser.add_argument("--probe", action="store_true",
                         help="run each config-2 kernel 3 times (for rocprofv3 counter passes)")

@@ -251,7 +251,7 @@ def fps_ball_knn(
     start_idx: int = 0,
     skip_near_origin: bool = False,
     *,
-    chunk: int = 256,
+    chunk: int = 128,
     check: bool = False,
 ) -> tuple[Tensor, Tensor, list[tuple[Tensor, Tensor]], tuple[Tensor, Tensor]]:
     """A multi-scale set-abstraction front end in one call: samples =
@@ -264,9 +264,10 @@ def fps_ball_knn(
     The ball queries of each ``chunk`` of centres start as soon as FPS has
     sampled it in every cloud, on the CUs FPS leaves free (FPS uses one per
     cloud), and kNN runs once after the last chunk, on a side stream that
-    the library joins back to the current one before returning (256:
-    0.560 ms at B=32, N=4096, npoint 1024, three radii and kNN16, against
-    0.600 ms for the separate calls; 128: 0.590, 512: 0.606).  Each call has
+    the library joins back to the current one before returning (128:
+    0.475 ms per call at B=32, N=4096, npoint 1024, three radii and kNN16,
+    against 0.557 ms for the separate calls; 96: 0.479, 192: 0.488, 256:
+    0.484: a smaller last chunk leaves less after FPS).  Each call has
     its own workspace, so calls may overlap (queued back to back, or issued
     from several streams or host threads).
 
