@@ -265,9 +265,12 @@ __global__ __launch_bounds__(kGroupThreads) void group_gather_grad_kernel(
 // group_csr_grad_kernel (a few workgroups per batch, each taking every
 // J-th channel): thread t owns positions [32 t, 32 t + 32) of the batch's
 // CSR list -- the same amount of work in every lane, however long the
-// lists are -- with their ids and point indices in registers for all
-// channels.  A channel's grad_out row of P floats is staged in LDS (the
-// next row requested into registers meanwhile); each thread sums the
+// lists are -- with, for all channels, one register per position holding
+// the LDS byte offsets of the row element it reads and of the slot its
+// running sum goes to.  A channel's grad_out row of P floats is staged in
+// LDS (the next row requested into registers meanwhile, with non-temporal
+// loads: each element is read once, and the rows -- larger than the
+// caches -- would otherwise displace reused data); each thread sums the
 // pieces of lists inside its range in list order, and a list that crosses
 // ranges is summed piece by piece: its first piece by the thread where it
 // starts, which then adds the following threads' pieces in order.  So a
@@ -281,8 +284,13 @@ constexpr int kGroupCsrMaxP = 32768;
 constexpr int kGroupCsrMaxN = 4096;
 constexpr int kGroupCsrRanges = 8;       // build workgroups per batch at most
 constexpr int kGroupCsrSorted = 256;     // lists up to this long are in ascending p
-constexpr int kGroupGradThreads = 1024;  // the gather's workgroup
-constexpr int kGroupCsrPiece = kGroupCsrMaxP / kGroupGradThreads;  // list positions per thread
+constexpr int kGroupGradThreads = 1024;  // the gather's workgroup: 32 list positions per thread
+// The gather's LDS result slots, in floats: a channel's results, a
+// continuation and a head piece per thread, and a padding slot (4 floats,
+// so the row after them is 16-byte aligned).
+__host__ __device__ constexpr int group_grad_slots(int threads) {
+    return kGroupCsrMaxN + 2 * threads + 4;
+}
 
 struct GroupCsr {
     int* start;      // [B][sstride]: list starts, N + 1 used
@@ -321,22 +329,24 @@ __global__ __launch_bounds__(kGroupCsrThreads) void group_csr_kernel(const I* __
         csr.key + b * csr.lstride);
 }
 
-template <bool VEC>
-__global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
+template <int T, bool VEC>
+__global__ __launch_bounds__(T) void group_csr_grad_kernel(
     const float* __restrict__ g, int64_t g_batch, GroupCsr csr, float* __restrict__ gf, int64_t C,
     int N, int P, uint32_t J) {
-    constexpr int T = kGroupGradThreads;
-    constexpr int E = kGroupCsrPiece;       // list positions per thread
+    constexpr int E = kGroupCsrMaxP / T;    // list positions per thread
     constexpr int NPT = kGroupCsrMaxN / T;  // output points per thread
     constexpr int V = kGroupCsrMaxP / T;    // row floats per thread
-    static_assert(E % 8 == 0 && V % 4 == 0 && E <= 64, "whole 16-byte loads, one mask");
-    extern __shared__ __align__(16) unsigned char group_lds[];
-    // LDS: the row [kGroupCsrMaxP], then the result slots: a channel's
-    // results [N], continuation pieces [T], head pieces [T], and a discard
-    // slot per thread [T].
-    float* const row = reinterpret_cast<float*>(group_lds);
-    float* const slots = row + kGroupCsrMaxP;
-    const int kCont = kGroupCsrMaxN, kHead = kCont + T, kTrash = kHead + T;
+    constexpr int B8 = 8;                   // positions per batch of LDS reads
+    constexpr int kCont = kGroupCsrMaxN, kHead = kCont + T, kPad = kHead + T;
+    constexpr uint32_t kRowByte = 4u * group_grad_slots(T);  // the row after the slots
+    static_assert(E % B8 == 0 && V % 4 == 0 && E <= 64, "whole 16-byte loads");
+    static_assert(kRowByte < 32768u && kRowByte % 16 == 0, "15-bit slot offsets, aligned row");
+    __shared__ __align__(16) unsigned char group_lds[kRowByte + 4 * kGroupCsrMaxP];
+    // LDS: the result slots -- a channel's results [N], continuation pieces
+    // [T], head pieces [T] and a padding slot [4] -- then the row
+    // [kGroupCsrMaxP].
+    float* const slots = reinterpret_cast<float*>(group_lds);
+    float* const row = reinterpret_cast<float*>(group_lds + kRowByte);
     const CloudBlock cb = cloud_block(J);  // a 1-D launch of B J workgroups
     const int64_t b = cb.b;
     const int64_t j = cb.x;
@@ -351,7 +361,7 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
 #pragma unroll
             for (int u = 0; u < V / 4; ++u) {
                 const float4 v =
-                    *reinterpret_cast<const float4*>(src + min(4 * (u * T + tid), P - 4));
+                    load_once(reinterpret_cast<const float4*>(src + min(4 * (u * T + tid), P - 4)));
                 r[4 * u] = v.x;
                 r[4 * u + 1] = v.y;
                 r[4 * u + 2] = v.z;
@@ -362,8 +372,8 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
     float rv[V];
     if (VEC && own > 0) fetch(0, rv);  // unaligned rows are read when needed instead
     // This thread's list positions q0 .. q0 + qn - 1: ids and points
-    // (16-bit, two per register; id 0 past the end), the point just before
-    // q0 and the one just after my range.
+    // (16-bit, two per register), the point just before q0 and the one just
+    // after my range.
     const int q0 = tid * E;
     const int qn = max(0, min(E, P - q0));
     const int64_t lbase = b * csr.lstride + (q0 < P ? q0 : 0);  // lstride: whole 64-id blocks
@@ -386,18 +396,20 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
     auto half = [](const uint32_t (&a)[E / 2], int u) {
         return static_cast<int>((u & 1) ? a[u >> 1] >> 16 : a[u >> 1] & 0xFFFFu);
     };
-#pragma unroll
-    for (int u = 0; u < E; ++u)  // positions past the end read row[0]
-        if (u >= qn) ids[u >> 1] &= (u & 1) ? 0x0000FFFFu : 0xFFFF0000u;
-    // Per position: does a piece start here (bit u of `fresh`), and where
-    // does the running sum go after it (dest, a slot index, two per
-    // register): the point's result slot where the point's list ends inside
-    // my range and began inside it, my continuation slot where my first
-    // piece (of a list begun before q0) ends, my head slot where my last
-    // piece (of a list going on past my range) ends, else my discard slot.
-    uint64_t fresh = 0;
-    uint32_t dest[E / 2];
+    // Per position, two LDS byte offsets in one register: bits 15-31 the
+    // row element it reads (4 x its id; row[0] past the end), bits 0-14
+    // the slot its running sum goes to: the point's result slot where the
+    // point's list ends inside my range and began inside it, my
+    // continuation slot where my first piece (of a list begun before q0)
+    // ends, my head slot where my last piece (of a list going on past my
+    // range) ends -- my last position --, the padding slot past the end.
+    // Positions inside a list also write my head slot: they come before my
+    // head piece's write, if there is one, and the slot is read only then.
+    // So a piece starts at position u exactly where position u - 1 wrote a
+    // slot other than my head slot (or u = 0).
+    uint32_t pos[E];
     int head_n = -1;  // the list my head piece begins (-1: none)
+    const uint32_t head_byte = 4u * static_cast<uint32_t>(kHead + tid);
     {
         const int first_n = qn > 0 ? half(pts, 0) : -1;
         const bool cont = qn > 0 && before == first_n;
@@ -405,21 +417,21 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
         for (int u = 0; u < E; ++u) {
             const int n = half(pts, u);
             const int nn = u + 1 < qn ? half(pts, u + 1) : after;
-            if (u < qn && (u == 0 || n != half(pts, u - 1))) fresh |= uint64_t(1) << u;
             const bool mine_first = cont && n == first_n;  // a list begun before q0
-            int d = kTrash + tid;
-            if (u < qn && n != nn) {  // the list ends here
+            int d = kHead + tid;  // inside a list
+            if (u >= qn) {
+                d = kPad;
+            } else if (n != nn) {  // the list ends here
                 d = mine_first ? kCont + tid : n;
             } else if (u + 1 == qn) {  // the list goes on past my range
                 if (mine_first) {
                     d = kCont + tid;  // a middle piece
                 } else {
-                    d = kHead + tid;
                     head_n = n;
                 }
             }
-            if (u & 1) dest[u >> 1] |= static_cast<uint32_t>(d) << 16;
-            else dest[u >> 1] = static_cast<uint32_t>(d);
+            const uint32_t id = u < qn ? static_cast<uint32_t>(half(ids, u)) : 0u;
+            pos[u] = (4u * id) << 15 | 4u * static_cast<uint32_t>(d);
         }
     }
     // Following threads whose first pieces finish my head's list.
@@ -441,28 +453,40 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
                     make_float4(rv[4 * u], rv[4 * u + 1], rv[4 * u + 2], rv[4 * u + 3]);
         } else {
             const float* src = gb + (j + s * J) * P;
-            for (int at = tid; at < P; at += T) row[at] = src[at];
+            for (int at = tid; at < P; at += T) row[at] = load_once(src + at);
         }
         __syncthreads();  // row complete
         if (VEC && s + 1 < own) fetch(s + 1, rv);
+        // Keeps the unpacked offsets from being hoisted out of the channel
+        // loop (twice the registers of the packed ones).
+#pragma unroll
+        for (int u = 0; u < E; ++u) asm volatile("" : "+v"(pos[u]));
         // The running sum in position order, restarted from +0 where a piece
-        // starts, stored after every position to that position's slot.
-        // Keeps the unpacked ids and slots from being hoisted out of the
-        // channel loop (twice the registers of the packed ones).
-#pragma unroll
-        for (int u = 0; u < E / 2; ++u) asm volatile("" : "+v"(ids[u]), "+v"(dest[u]));
+        // starts, stored after every position to that position's slot.  The
+        // next eight row reads are issued before the current eight are
+        // summed (the row is not written in this phase).
+        auto rd = [&](int u) {
+            return *reinterpret_cast<const float*>(group_lds + kRowByte + (pos[u] >> 15));
+        };
         float acc = 0.f;
+        float va[B8], vb[B8];
 #pragma unroll
-        for (int u8 = 0; u8 < E; u8 += 8) {
-            float v[8];
+        for (int u = 0; u < B8; ++u) va[u] = rd(u);
 #pragma unroll
-            for (int u = u8; u < u8 + 8; ++u)
-                v[u - u8] = row[(u & 1) ? ids[u >> 1] >> 16 : ids[u >> 1] & 0xFFFFu];
+        for (int u8 = 0; u8 < E; u8 += B8) {
+            if (u8 + B8 < E) {
 #pragma unroll
-            for (int u = u8; u < u8 + 8; ++u) {
-                acc = ((fresh >> u) & 1u ? 0.f : acc) + v[u - u8];  // +0 + x: a piece's first term
-                slots[(u & 1) ? dest[u >> 1] >> 16 : dest[u >> 1] & 0xFFFFu] = acc;
+                for (int u = 0; u < B8; ++u) vb[u] = rd(u8 + B8 + u);
             }
+#pragma unroll
+            for (int u = 0; u < B8; ++u) {
+                const int q = u8 + u;
+                const bool keep = q > 0 && (pos[q - 1] & 0x7FFFu) == head_byte;
+                acc = (keep ? acc : 0.f) + va[u];  // +0 + x: a piece's first term
+                *reinterpret_cast<float*>(group_lds + (pos[q] & 0x7FFFu)) = acc;
+            }
+#pragma unroll
+            for (int u = 0; u < B8; ++u) va[u] = vb[u];
             __builtin_amdgcn_sched_barrier(0);  // eight positions at a time: few live values
         }
         __syncthreads();  // pieces complete
@@ -495,8 +519,10 @@ __global__ __launch_bounds__(kGroupGradThreads) void group_csr_grad_kernel(
 // coordinates for channels 0-2 -- with coalesced loads, then walks its
 // columns: each column's index is read once (four columns per thread in
 // flight) and its CG values come from LDS, so the gathers never touch L2;
-// stores along p are coalesced.  HBM traffic: the output, the source rows
-// once per slice (L2 after the first) and the index once per channel group.
+// stores along p are coalesced and non-temporal (the output, S times the
+// features, is larger than the caches and would displace the source rows).
+// HBM traffic: the output, the source rows once per slice (L2 after the
+// first) and the index once per channel group.
 constexpr int kGroupLdsThreads = 512;
 // Rows per workgroup: up to 32 KiB (measured at config 2's shape: 8 KiB
 // rows, 2 per workgroup, 83 us; 1 row 104 us, 4 rows 94 us, 8 rows 134 us),
@@ -562,7 +588,7 @@ __global__ __launch_bounds__(kGroupLdsThreads) void group_lds_kernel(
                 if (k >= nc) break;
                 float v = rows[static_cast<int64_t>(k) * N + j[u]];
                 if (REL && c0 + k < 3) v = v - ctr[c0 + k];
-                ob[static_cast<int64_t>(k) * P + p] = v;
+                store_once(ob + static_cast<int64_t>(k) * P + p, v);
             }
         }
     }
@@ -671,17 +697,16 @@ hipError_t pointops_group_points_backward(const float* grad_out, int64_t grad_ba
         // J workgroups per batch (every J-th channel each), enough to cover
         // the CUs; LDS: a row and the result slots.
         const int64_t J = std::min<int64_t>(C, std::max<int64_t>(1, (256 + B - 1) / B));
-        const size_t lds =
-            (kGroupCsrMaxP + kGroupCsrMaxN + 1 + 3 * kGroupGradThreads) * sizeof(float);
+        constexpr int T = kGroupGradThreads;  // LDS: a row and the result slots (static)
         const dim3 ggrid(static_cast<uint32_t>(B * J));
         const uint32_t uj = static_cast<uint32_t>(J);
         const bool vec = P % 4 == 0 && grad_batch_stride % 4 == 0 &&
                          reinterpret_cast<uintptr_t>(grad_out) % 16 == 0;
         if (vec)
-            hipLaunchKernelGGL(group_csr_grad_kernel<true>, ggrid, dim3(kGroupGradThreads), lds,
+            hipLaunchKernelGGL((group_csr_grad_kernel<T, true>), ggrid, dim3(T), 0,
                                stream, grad_out, grad_batch_stride, csr, grad_features, C, n, p, uj);
         else
-            hipLaunchKernelGGL(group_csr_grad_kernel<false>, ggrid, dim3(kGroupGradThreads), lds,
+            hipLaunchKernelGGL((group_csr_grad_kernel<T, false>), ggrid, dim3(T), 0,
                                stream, grad_out, grad_batch_stride, csr, grad_features, C, n, p, uj);
         return hipGetLastError();
     }

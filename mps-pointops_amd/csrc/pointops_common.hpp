@@ -39,6 +39,18 @@ __device__ __forceinline__ float sqdist3(float ax, float ay, float az, float bx,
 __device__ __forceinline__ int f2i(float v) { return __float_as_int(v); }
 __device__ __forceinline__ float i2f(int v) { return __int_as_float(v); }
 
+// Loads of data read exactly once (gradient rows streamed through LDS),
+// marked non-temporal: they do not displace reused data from the caches.
+__device__ __forceinline__ float4 load_once(const float4* p) {
+    typedef float f4 __attribute__((ext_vector_type(4)));
+    const f4 v = __builtin_nontemporal_load(reinterpret_cast<const f4*>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+__device__ __forceinline__ float load_once(const float* p) { return __builtin_nontemporal_load(p); }
+// Stores of outputs larger than the caches (the set-abstraction layer's
+// grouped features), marked non-temporal for the same reason.
+__device__ __forceinline__ void store_once(float* p, float v) { __builtin_nontemporal_store(v, p); }
+
 // ---------------------------------------------------------------- DPP / SALU
 // GFX9 DPP controls (row = 16 lanes).
 constexpr int kDppQuadXor1 = 0xB1;      // quad_perm [1,0,3,2]
