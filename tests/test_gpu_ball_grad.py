@@ -121,6 +121,8 @@ def test_c2_radii_closed_form(radius, k):
     (3, 77, 1000, 16, 0.5, 2),    # one partial tile
     (1, 9, 2048, 128, 2.0, 3),    # every row full, K > 64
     (2, 64, 1, 4, 1.0, 4),        # a one-point cloud
+    (1, 5, 300, 8, 0.5, 5),       # fewer rows than segments: empty segments
+    (1, 2100, 600, 128, 0.5, 6),  # many rows per segment, K > 64
 ])
 def test_fixed_order_bits_and_repeatability(B, Q, P, K, radius, seed):
     import mps_pointops as mp
