@@ -42,6 +42,7 @@ constexpr int kGradBatch = 8;    // (row, chunk) units per wave loaded before th
 constexpr int kGradWaves = 8;
 constexpr int kGradThreads = kGradWaves * kWave;
 constexpr int kGradTile = 512;  // points per workgroup: 48 KiB of accumulators
+constexpr int kGradDenseTiles = 16;  // tiles per cloud up to which every tile reads every row
 
 template <typename S>
 __device__ __forceinline__ float widen(S v);
@@ -121,7 +122,7 @@ __global__ __launch_bounds__(kGradRowThreads) void ball_grad_rows_kernel(
     range[row] = make_int2(slo, shi);
 }
 
-template <typename S>
+template <typename S, bool DENSE>
 __global__ __launch_bounds__(kGradThreads) void ball_grad_points_kernel(
     const S* __restrict__ queries, const S* __restrict__ points, const int64_t* __restrict__ idx,
     const float* __restrict__ grad, const int2* __restrict__ range, float* __restrict__ grad_points,
@@ -148,50 +149,102 @@ __global__ __launch_bounds__(kGradThreads) void ball_grad_points_kernel(
     // At least one chunk per row, so the unit walk advances (for K = 0 every
     // slot is masked).
     const int64_t chunks = K > kWave ? (K + kWave - 1) / kWave : 1;
-    // Units (row q, slots [c * 64, c * 64 + 64)) in row order; kGradBatch of
-    // them are loaded, then added in order.
-    int64_t q = r0, c = 0;
-    while (q < r1) {
-        int64_t rows[kGradBatch], ks[kGradBatch];
-        bool use[kGradBatch];
-        float ux[kGradBatch], uy[kGradBatch], uz[kGradBatch];
-        // The units' range records and query rows (wave-uniform loads), all
-        // requested before any is used; then the slots of the units in use.
+    if constexpr (DENSE) {
+        // Few tiles per cloud: every row is read by every tile anyway, so the
+        // range records are not consulted.  Units (row q, slots [c * 64,
+        // c * 64 + 64)) in row order, kGradBatch at a time; the next batch's
+        // loads (from clamped addresses, masked at use) are in flight while
+        // this batch is added.
+        int64_t q = r0, c = 0;
+        struct Batch {
+            int64_t j[kGradBatch];
+            float g[kGradBatch], x[kGradBatch], y[kGradBatch], z[kGradBatch];
+            uint32_t live;  // bit d: unit d holds a slot of this lane
+        };
+        auto load = [&](Batch& t) {
+            t.live = 0;
 #pragma unroll
-        for (int d = 0; d < kGradBatch; ++d) {
-            use[d] = q < r1;
-            rows[d] = b * Q + min(q, r1 - 1);
-            ks[d] = c * kWave + lane;
-            if (++c == chunks) {
-                c = 0;
-                ++q;
+            for (int d = 0; d < kGradBatch; ++d) {
+                const int64_t row = b * Q + min(q, r1 - 1);
+                const int64_t k = c * kWave + lane;
+                if (q < r1 && k < K) t.live |= 1u << d;
+                const int64_t slot = row * K + min<int64_t>(k, K - 1);
+                t.j[d] = idx[slot];
+                t.g[d] = grad[slot];
+                t.x[d] = widen(queries[3 * row]);
+                t.y[d] = widen(queries[3 * row + 1]);
+                t.z[d] = widen(queries[3 * row + 2]);
+                if (q < r1 && ++c == chunks) {
+                    c = 0;
+                    ++q;
+                }
+            }
+        };
+        const int64_t batches = ((r1 - r0) * chunks + kGradBatch - 1) / kGradBatch;
+        if (batches > 0 && K > 0) {
+            Batch cur, nxt;
+            load(cur);
+            for (int64_t bt = 0; bt < batches; ++bt) {
+                if (bt + 1 < batches) load(nxt);
+#pragma unroll
+                for (int d = 0; d < kGradBatch; ++d) {
+                    const int64_t jd = (cur.live >> d) & 1u ? cur.j[d] : -1;
+                    if (jd < tlo || jd >= thi) continue;
+                    const int t = static_cast<int>(jd) - tlo;
+                    const float g2 = 2.f * cur.g[d];
+                    acc[wave][0][t] += g2 * (cur.x[d] - tile[0][t]);
+                    acc[wave][1][t] += g2 * (cur.y[d] - tile[1][t]);
+                    acc[wave][2][t] += g2 * (cur.z[d] - tile[2][t]);
+                }
+                cur = nxt;
             }
         }
-        int2 rr[kGradBatch];
-#pragma unroll
-        for (int d = 0; d < kGradBatch; ++d) {
-            rr[d] = range[rows[d]];
-            ux[d] = widen(queries[3 * rows[d]]);
-            uy[d] = widen(queries[3 * rows[d] + 1]);
-            uz[d] = widen(queries[3 * rows[d] + 2]);
-        }
-        int64_t jj[kGradBatch];
-        float gg[kGradBatch];
-#pragma unroll
-        for (int d = 0; d < kGradBatch; ++d) {
-            // Some slot of the row in the tile (wave-uniform), and a slot for this lane.
-            const bool live = use[d] && !(rr[d].y < tlo || rr[d].x >= thi) && ks[d] < K;
-            jj[d] = live ? idx[rows[d] * K + ks[d]] : -1;
-            gg[d] = live ? grad[rows[d] * K + ks[d]] : 0.f;
-        }
-#pragma unroll
-        for (int d = 0; d < kGradBatch; ++d) {
-            if (jj[d] < tlo || jj[d] >= thi) continue;
-            const int t = static_cast<int>(jj[d]) - tlo;
-            const float g2 = 2.f * gg[d];
-            acc[wave][0][t] += g2 * (ux[d] - tile[0][t]);
-            acc[wave][1][t] += g2 * (uy[d] - tile[1][t]);
-            acc[wave][2][t] += g2 * (uz[d] - tile[2][t]);
+    } else {
+        // Units (row q, slots [c * 64, c * 64 + 64)) in row order; kGradBatch of
+        // them are loaded, then added in order.
+        int64_t q = r0, c = 0;
+        while (q < r1) {
+            int64_t rows[kGradBatch], ks[kGradBatch];
+            bool use[kGradBatch];
+            float ux[kGradBatch], uy[kGradBatch], uz[kGradBatch];
+            // The units' range records and query rows (wave-uniform loads), all
+            // requested before any is used; then the slots of the units in use.
+    #pragma unroll
+            for (int d = 0; d < kGradBatch; ++d) {
+                use[d] = q < r1;
+                rows[d] = b * Q + min(q, r1 - 1);
+                ks[d] = c * kWave + lane;
+                if (++c == chunks) {
+                    c = 0;
+                    ++q;
+                }
+            }
+            int2 rr[kGradBatch];
+    #pragma unroll
+            for (int d = 0; d < kGradBatch; ++d) {
+                rr[d] = range[rows[d]];
+                ux[d] = widen(queries[3 * rows[d]]);
+                uy[d] = widen(queries[3 * rows[d] + 1]);
+                uz[d] = widen(queries[3 * rows[d] + 2]);
+            }
+            int64_t jj[kGradBatch];
+            float gg[kGradBatch];
+    #pragma unroll
+            for (int d = 0; d < kGradBatch; ++d) {
+                // Some slot of the row in the tile (wave-uniform), and a slot for this lane.
+                const bool live = use[d] && !(rr[d].y < tlo || rr[d].x >= thi) && ks[d] < K;
+                jj[d] = live ? idx[rows[d] * K + ks[d]] : -1;
+                gg[d] = live ? grad[rows[d] * K + ks[d]] : 0.f;
+            }
+    #pragma unroll
+            for (int d = 0; d < kGradBatch; ++d) {
+                if (jj[d] < tlo || jj[d] >= thi) continue;
+                const int t = static_cast<int>(jj[d]) - tlo;
+                const float g2 = 2.f * gg[d];
+                acc[wave][0][t] += g2 * (ux[d] - tile[0][t]);
+                acc[wave][1][t] += g2 * (uy[d] - tile[1][t]);
+                acc[wave][2][t] += g2 * (uz[d] - tile[2][t]);
+            }
         }
     }
     __syncthreads();
@@ -235,9 +288,17 @@ hipError_t launch_ball_grad(const S* queries, const S* points, const int64_t* id
         if (err != hipSuccess) return err;
     }
     if (grad_points == nullptr || tiles == 0) return hipSuccess;
-    hipLaunchKernelGGL(ball_grad_points_kernel<S>, dim3(static_cast<uint32_t>(B * tiles)),
-                       dim3(kGradThreads), 0, stream, queries, points, idx, grad, range,
-                       grad_points, Q, P, K, static_cast<uint32_t>(tiles));
+    // Up to kGradDenseTiles tiles per cloud: every tile reads every row
+    // (the dense loop, loads pipelined); beyond, rows missing a tile are
+    // skipped after their range record.
+    if (tiles <= kGradDenseTiles)
+        hipLaunchKernelGGL((ball_grad_points_kernel<S, true>), dim3(static_cast<uint32_t>(B * tiles)),
+                           dim3(kGradThreads), 0, stream, queries, points, idx, grad, range,
+                           grad_points, Q, P, K, static_cast<uint32_t>(tiles));
+    else
+        hipLaunchKernelGGL((ball_grad_points_kernel<S, false>), dim3(static_cast<uint32_t>(B * tiles)),
+                           dim3(kGradThreads), 0, stream, queries, points, idx, grad, range,
+                           grad_points, Q, P, K, static_cast<uint32_t>(tiles));
     return hipGetLastError();
 }
 

@@ -123,6 +123,7 @@ def test_c2_radii_closed_form(radius, k):
     (2, 64, 1, 4, 1.0, 4),        # a one-point cloud
     (1, 5, 300, 8, 0.5, 5),       # fewer rows than segments: empty segments
     (1, 2100, 600, 128, 0.5, 6),  # many rows per segment, K > 64
+    (1, 40, 9000, 16, 0.3, 7),    # more than 16 tiles: rows missing a tile skipped
 ])
 def test_fixed_order_bits_and_repeatability(B, Q, P, K, radius, seed):
     import mps_pointops as mp
