@@ -21,10 +21,13 @@
 //     rows and adds the contributions of its rows, in row order, into its own
 //     LDS accumulators (a point occurs at most once per row, so the lanes of
 //     one row never collide); the segments' sums are then added in segment
-//     order.  A row whose index range misses the tile is skipped after its
-//     8-byte range record, so large clouds do not re-read every row per tile.
-//     Each wave loads kGradBatch (row, 64-slot chunk) units before it adds
-//     the first, so one memory round trip covers several rows.
+//     order.  In clouds of more than kGradDenseTiles tiles a row whose
+//     index range misses the tile is skipped after its 8-byte range record,
+//     so large clouds do not re-read every row per tile, and each wave loads
+//     kGradBatch (row, 64-slot chunk) units before it adds the first; in
+//     smaller clouds (where first-K hits span the whole index range) every
+//     row is read and the next batch's loads are in flight while a batch is
+//     added.
 // Inputs are float32 or float16 coordinates (widened to float32, as the
 // reference's .float()); gradients are float32.
 #include <hip/hip_fp16.h>
