@@ -32,6 +32,8 @@ constexpr int kBqDepth = 8;  // 64-point blocks in flight per wave (even)
 // LDS-staged dense kernel: queries (waves) per workgroup and 64-point blocks
 // per LDS tile (measured best of 2-16 waves and 8-48 blocks per tile).
 constexpr int kBqLdsQueries = 8;
+constexpr uint64_t kBqAllDone = 0x0101010101010101ull;  // every wave's done byte set
+static_assert(kBqLdsQueries == 8, "the done bytes of a workgroup fill one 64-bit word");
 constexpr int kBqLdsDepth = 32;
 
 template <typename S>
@@ -132,7 +134,7 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
     constexpr int kPer = kTile / (NWQ * kWave);  // points each thread stages per tile
     static_assert(kPer * NWQ * kWave == kTile && kBqLdsDepth % 2 == 0, "tile shape");
     __shared__ float4 tile[kTile];
-    __shared__ int done_flags[NWQ];
+    __shared__ __align__(8) uint8_t done_flags[NWQ];  // one byte per wave, read as one word
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = uniform(tid / kWave);
@@ -180,13 +182,14 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
             for (int c = 0; c < kBqLdsDepth; c += 2) {
                 const float4 p0 = tile[c * kWave + lane];
                 const float4 p1 = tile[(c + 1) * kWave + lane];
-                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
                 const float d0 = sqdist3(qx, qy, qz, p0.x, p0.y, p0.z);
                 const float d1 = sqdist3(qx, qy, qz, p1.x, p1.y, p1.z);
-                const bool h0 = (decltype(full)::value || j0 < n) && d0 < r2;
-                const bool h1 = (decltype(full)::value || j1 < n) && d1 < r2;
+                // A full tile needs the point indices only where a hit is stored.
+                const bool h0 = (decltype(full)::value || base + c * kWave + lane < n) && d0 < r2;
+                const bool h1 = (decltype(full)::value || base + (c + 1) * kWave + lane < n) && d1 < r2;
                 const uint64_t m0 = ballot(h0), m1 = ballot(h1);
                 if ((m0 | m1) == 0) continue;
+                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
                 // Slots and indices are non-negative: unsigned, so that the
                 // 64-bit addresses and index values need no sign extension.
                 const uint32_t s0 = static_cast<uint32_t>(found + lanes_below(m0));
@@ -219,10 +222,7 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
         }
         if (lane == 0) done_flags[wave] = done ? 1 : 0;
         __syncthreads();  // flags written; every wave is past its reads of this tile
-        bool all_done = true;
-#pragma unroll
-        for (int w = 0; w < NWQ; ++w) all_done = all_done && done_flags[w] != 0;
-        if (all_done) break;
+        if (*reinterpret_cast<const uint64_t*>(done_flags) == kBqAllDone) break;
     }
     if (qi >= Q) return;
     found = min(found, K);
@@ -377,7 +377,7 @@ __global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel
     constexpr int kPer = kTile / (NWQ * kWave);
     static_assert(kPer * NWQ * kWave == kTile && kBqLdsDepth % 2 == 0 && NR <= kBqMulti, "shape");
     __shared__ float4 tile[kTile];
-    __shared__ int done_flags[NWQ];
+    __shared__ __align__(8) uint8_t done_flags[NWQ];  // one byte per wave, read as one word
     const int tid = threadIdx.x;
     const int lane = lane_id();
     const int wave = uniform(tid / kWave);
@@ -422,11 +422,10 @@ __global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel
             for (int c = 0; c < kBqLdsDepth; c += 2) {
                 const float4 p0 = tile[c * kWave + lane];
                 const float4 p1 = tile[(c + 1) * kWave + lane];
-                const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
                 const float d0 = sqdist3(qx, qy, qz, p0.x, p0.y, p0.z);
                 const float d1 = sqdist3(qx, qy, qz, p1.x, p1.y, p1.z);
-                const bool in0 = decltype(full)::value || j0 < n;
-                const bool in1 = decltype(full)::value || j1 < n;
+                const bool in0 = decltype(full)::value || base + c * kWave + lane < n;
+                const bool in1 = decltype(full)::value || base + (c + 1) * kWave + lane < n;
                 bool all = true;
 #pragma unroll
                 for (int r = 0; r < NR; ++r) {
@@ -435,6 +434,8 @@ __global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel
                     const bool h1 = in1 && d1 < out.r2[r];
                     const uint64_t m0 = ballot(h0), m1 = ballot(h1);
                     if ((m0 | m1) != 0) {
+                        // A full tile needs the point indices only here.
+                        const int j0 = base + c * kWave + lane, j1 = j0 + kWave;
                         const uint32_t s0 = static_cast<uint32_t>(found[r] + lanes_below(m0));
                         const uint32_t s1 =
                             static_cast<uint32_t>(found[r] + __popcll(m0) + lanes_below(m1));
@@ -466,10 +467,7 @@ __global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel
         }
         if (lane == 0) done_flags[wave] = done ? 1 : 0;
         __syncthreads();  // flags written; every wave is past its reads of this tile
-        bool all_done = true;
-#pragma unroll
-        for (int w = 0; w < NWQ; ++w) all_done = all_done && done_flags[w] != 0;
-        if (all_done) break;
+        if (*reinterpret_cast<const uint64_t*>(done_flags) == kBqAllDone) break;
     }
     if (!live) return;
 #pragma unroll
