@@ -34,6 +34,13 @@ constexpr int kBqDepth = 8;  // 64-point blocks in flight per wave (even)
 constexpr int kBqLdsQueries = 8;
 constexpr uint64_t kBqAllDone = 0x0101010101010101ull;  // every wave's done byte set
 static_assert(kBqLdsQueries == 8, "the done bytes of a workgroup fill one 64-bit word");
+// Element `slot` of a wave's output row, addressed by a 32-bit byte offset
+// from the row's (wave-uniform) base, so that the store needs no 64-bit
+// address arithmetic per lane.
+template <typename T>
+__device__ __forceinline__ T& row_at(T* base, uint32_t slot) {
+    return *reinterpret_cast<T*>(reinterpret_cast<char*>(base) + slot * static_cast<uint32_t>(sizeof(T)));
+}
 constexpr int kBqLdsDepth = 32;
 
 template <typename S>
@@ -199,16 +206,16 @@ __global__ __launch_bounds__(NWQ * kWave) void ball_query_lds_kernel(
                     if (found == 0)
                         first = m0 != 0 ? base + c * kWave + static_cast<int>(__builtin_ctzll(m0))
                                         : base + (c + 1) * kWave + static_cast<int>(__builtin_ctzll(m1));
-                    if (h0 && s0 < uk) oi32[s0] = j0;
-                    if (h1 && s1 < uk) oi32[s1] = j1;
+                    if (h0 && s0 < uk) row_at(oi32, s0) = j0;
+                    if (h1 && s1 < uk) row_at(oi32, s1) = j1;
                 } else {
                     if (h0 && s0 < uk) {
-                        oi[s0] = static_cast<int64_t>(static_cast<uint32_t>(j0));
-                        od[s0] = d0;
+                        row_at(oi, s0) = static_cast<int64_t>(static_cast<uint32_t>(j0));
+                        row_at(od, s0) = d0;
                     }
                     if (h1 && s1 < uk) {
-                        oi[s1] = static_cast<int64_t>(static_cast<uint32_t>(j1));
-                        od[s1] = d1;
+                        row_at(oi, s1) = static_cast<int64_t>(static_cast<uint32_t>(j1));
+                        row_at(od, s1) = d1;
                     }
                 }
                 found += __popcll(m0) + __popcll(m1);
@@ -443,12 +450,12 @@ __global__ __launch_bounds__(kBqLdsQueries * kWave) void ball_query_multi_kernel
                         int64_t* oi = out.idx[r] + row * out.k[r];
                         float* od = out.dist[r] + row * out.k[r];
                         if (h0 && s0 < uk) {
-                            oi[s0] = static_cast<int64_t>(static_cast<uint32_t>(j0));
-                            od[s0] = d0;
+                            row_at(oi, s0) = static_cast<int64_t>(static_cast<uint32_t>(j0));
+                            row_at(od, s0) = d0;
                         }
                         if (h1 && s1 < uk) {
-                            oi[s1] = static_cast<int64_t>(static_cast<uint32_t>(j1));
-                            od[s1] = d1;
+                            row_at(oi, s1) = static_cast<int64_t>(static_cast<uint32_t>(j1));
+                            row_at(od, s1) = d1;
                         }
                         found[r] += __popcll(m0) + __popcll(m1);
                         fin[r] = found[r] >= out.k[r];
