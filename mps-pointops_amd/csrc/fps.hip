@@ -537,6 +537,74 @@ __global__ __launch_bounds__(T) void fps_tiled_kernel(const float* __restrict__ 
     }
 }
 
+// The boxes of a wave's PO tiles of 64 points (lane l holds point l of each
+// tile, pcode 0x7FFFFFFF where it holds none), reduced together: the 6 PO
+// minima (x, y, z and -x, -y, -z of every tile) are halved at each exchange
+// 32, 16, ... lanes apart while their count is even (a lane keeps the half
+// that its lane bit selects and folds in the partner's copy of it), and the
+// 3 left are folded over the remaining exchanges.  Lane l then holds values
+// 3 g .. 3 g + 2 of group g = l >> (5 - log2 PO): tile t's minima in group
+// 2t, its negated maxima in group 2t + 1.  For PO = 8 that is 51 exchanges
+// in place of 48 separate wave reductions.  Per lane, the box of tile
+// lane % 16, or [+inf, +inf] where that tile does not exist or holds no
+// point.
+template <int V, int S>
+__device__ __forceinline__ void fold_min(float* v, int lane) {
+    if constexpr (S > 0) {
+        if constexpr (V % 2 == 0 && V > 3) {
+            constexpr int H = V / 2;
+            const bool upper = (lane & S) != 0;
+#pragma unroll
+            for (int i = 0; i < H; ++i) {
+                const float send = upper ? v[i] : v[H + i];
+                const float keep = upper ? v[H + i] : v[i];
+                v[i] = fminf(keep, __shfl_xor(send, S, kWave));
+            }
+            fold_min<H, S / 2>(v, lane);
+        } else {
+#pragma unroll
+            for (int i = 0; i < V; ++i) v[i] = fminf(v[i], __shfl_xor(v[i], S, kWave));
+            fold_min<V, S / 2>(v, lane);
+        }
+    }
+}
+
+template <int PO>
+__device__ __forceinline__ void tile_boxes(const float (&px)[PO], const float (&py)[PO],
+                                           const float (&pz)[PO], const int (&pcode)[PO], int lane,
+                                           float (&tlo)[3], float (&thi)[3]) {
+    static_assert(PO == 1 || PO == 2 || PO == 4 || PO == 8, "tiles per wave: 1, 2, 4 or 8");
+    float v[6 * PO];
+#pragma unroll
+    for (int k = 0; k < PO; ++k) {
+        const bool valid = pcode[k] != 0x7FFFFFFF;
+        v[6 * k] = valid ? px[k] : INFINITY;
+        v[6 * k + 1] = valid ? py[k] : INFINITY;
+        v[6 * k + 2] = valid ? pz[k] : INFINITY;
+        v[6 * k + 3] = valid ? -px[k] : INFINITY;
+        v[6 * k + 4] = valid ? -py[k] : INFINITY;
+        v[6 * k + 5] = valid ? -pz[k] : INFINITY;
+    }
+    fold_min<6 * PO, kWave / 2>(v, lane);
+    constexpr int shift = PO == 8 ? 2 : PO == 4 ? 3 : PO == 2 ? 4 : 5;
+    const int t = lane & 15;
+    const int src_lo = ((2 * t) << shift) & (kWave - 1);
+    const int src_hi = ((2 * t + 1) << shift) & (kWave - 1);
+    float lo[3], hi[3];
+    bool has = t < PO;
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        lo[a] = __shfl(v[a], src_lo, kWave);
+        hi[a] = -__shfl(v[a], src_hi, kWave);
+        has = has && lo[a] <= hi[a];
+    }
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+        tlo[a] = has ? lo[a] : INFINITY;
+        thi[a] = has ? hi[a] : INFINITY;
+    }
+}
+
 // fps_lead_kernel<P>: the tiled FPS above with the step chain taken by one
 // wave instead of all of them.
 //
@@ -591,12 +659,11 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     constexpr int kCells = 4096;
     static_assert(KC * NF == kWave && KC + 1 <= kWave && P <= 16 && CAP <= 8192, "shape");
     static_assert(kCells % TS == 0, "cells per thread");
-    constexpr int kSortInts = kCells + CAP;
-    constexpr int kBufVec = (kSortInts * 4 > CAP * 16 ? kSortInts * 4 : CAP * 16) / 16;
-    __shared__ float4 buf[kBufVec];
-    int* const cell_count = reinterpret_cast<int*>(buf);
-    int* const sorted_index = cell_count + kCells;
-    float4* const spts = buf;
+    // The sort's cell counts (then offsets), and the points by sorted
+    // position (xyz, and the point's index in w), which the sort's scatter
+    // writes directly.
+    __shared__ int cell_count[kCells];
+    __shared__ float4 spts[CAP];
     __shared__ float red[6][NS];
     __shared__ int wave_sum[NS];
     // The candidates: coordinates with the point index in w, and keys;
@@ -759,7 +826,8 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     if (sorter) {
 #pragma unroll
         for (int k = 0; k < P; ++k)
-            if (tid * P + k < n) sorted_index[cell_count[cell[k]] + rank[k]] = tid * P + k;
+            if (tid * P + k < n)
+                spts[cell_count[cell[k]] + rank[k]] = make_float4(lx[k], ly[k], lz[k], i2f(tid * P + k));
     }
     __syncthreads();  // permutation complete
 
@@ -774,7 +842,6 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
         pcode[k] = 0x7FFFFFFF;
         md[k] = -INFINITY;
     }
-    float blo[3] = {INFINITY, INFINITY, INFINITY}, bhi[3] = {INFINITY, INFINITY, INFINITY};
     if (follower) {
         float cx, cy, cz;
         {
@@ -785,45 +852,24 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
         }
 #pragma unroll
         for (int k = 0; k < PO; ++k) {
-            const int q = (tile0 + k) * kWave + lane;
+            const int q = (tile0 + k) * kWave + lane;  // < NF PO kWave = CAP
             const bool valid = k < my_tiles && q < n;
-            const int j = valid ? sorted_index[q] : 0;
-            px[k] = valid ? p[3 * j] : 0.f;
-            py[k] = valid ? p[3 * j + 1] : 0.f;
-            pz[k] = valid ? p[3 * j + 2] : 0.f;
-            pcode[k] = valid ? (j << 13) | q : 0x7FFFFFFF;
+            const float4 s = spts[q];
+            px[k] = valid ? s.x : 0.f;
+            py[k] = valid ? s.y : 0.f;
+            pz[k] = valid ? s.z : 0.f;
+            pcode[k] = valid ? (f2i(s.w) << 13) | q : 0x7FFFFFFF;
             md[k] = !valid ? -INFINITY : initial_running(skip, px[k], py[k], pz[k]);
             md[k] = running_min(md[k], sqdist3(px[k], py[k], pz[k], cx, cy, cz));
-            const float tlx = wave_min(valid ? px[k] : INFINITY), thx = wave_max(valid ? px[k] : -INFINITY);
-            const float tly = wave_min(valid ? py[k] : INFINITY), thy = wave_max(valid ? py[k] : -INFINITY);
-            const float tlz = wave_min(valid ? pz[k] : INFINITY), thz = wave_max(valid ? pz[k] : -INFINITY);
-            if (lane == k && tlx <= thx && tly <= thy && tlz <= thz) {
-                blo[0] = tlx; bhi[0] = thx;
-                blo[1] = tly; bhi[1] = thy;
-                blo[2] = tlz; bhi[2] = thz;
-            }
         }
     }
-    // Per lane, the box of tile lane % 16 (the follower's tile boxes sit in
-    // lanes 0..PO-1; lanes without a tile hold [+inf, +inf], which no test
-    // selects), and the shift of step lane / 16's byte in a block's lanes.
+    // Per lane, the box of tile lane % 16 ([+inf, +inf] where that tile does
+    // not exist or holds no point, which no test selects), and the shift of
+    // step lane / 16's byte in a block's lanes.
     static_assert(PO <= 16, "a follower holds at most 16 tiles");
     float tlo[3], thi[3];
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-        tlo[a] = __shfl(blo[a], lane & 15, kWave);
-        thi[a] = __shfl(bhi[a], lane & 15, kWave);
-    }
+    tile_boxes<PO>(px, py, pz, pcode, lane, tlo, thi);
     const uint32_t lane_shift = 8u * static_cast<uint32_t>(lane >> 4);
-    __syncthreads();  // every sorted index has been read
-    if (follower) {
-#pragma unroll
-        for (int k = 0; k < PO; ++k) {
-            const int q = (tile0 + k) * kWave + lane;
-            if (k < my_tiles && q < n) spts[q] = make_float4(px[k], py[k], pz[k], 0.f);
-        }
-    }
-    __syncthreads();  // coordinates by sorted position
 
     if (leader) __builtin_amdgcn_s_setprio(3);
     int64_t step = 1;
