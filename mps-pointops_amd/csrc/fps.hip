@@ -733,40 +733,59 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     // ---- setup: the sort by waves 0-7
     if (sorter)
         for (int c = tid; c < kCells; c += TS) cell_count[c] = 0;
-    float lx[P], ly[P], lz[P];
-#pragma unroll
-    for (int k = 0; k < P; ++k) {
-        const int j = min(tid * P + k, n - 1);
-        lx[k] = sorter ? p[3 * j] : 0.f;
-        ly[k] = sorter ? p[3 * j + 1] : 0.f;
-        lz[k] = sorter ? p[3 * j + 2] : 0.f;
-    }
+    // The cloud's coordinates, staged through the LDS (in the space that the
+    // sorted points take later) by coalesced loads; sorting thread t then
+    // takes points t, t + TS, ..., t + (P - 1) TS.
+    float* const stage = reinterpret_cast<float*>(spts);
+    static_assert(3 * CAP * sizeof(float) <= CAP * sizeof(float4), "the staged cloud fits");
     if (sorter) {
-        float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+        float raw[3 * P];
 #pragma unroll
-        for (int k = 0; k < P; ++k) {
-            mn[0] = fminf(mn[0], lx[k]); mx[0] = fmaxf(mx[0], lx[k]);
-            mn[1] = fminf(mn[1], ly[k]); mx[1] = fmaxf(mx[1], ly[k]);
-            mn[2] = fminf(mn[2], lz[k]); mx[2] = fmaxf(mx[2], lz[k]);
+        for (int m = 0; m < 3 * P; ++m) {
+            const int f = tid + m * TS;
+            raw[m] = f < 3 * n ? p[f] : 0.f;
         }
 #pragma unroll
-        for (int a = 0; a < 3; ++a) {
-            mn[a] = wave_min(mn[a]);
-            mx[a] = wave_max(mx[a]);
-        }
-        if (lane == 0) {
-#pragma unroll
-            for (int a = 0; a < 3; ++a) {
-                red[a][wave] = mn[a];
-                red[3 + a][wave] = mx[a];
-            }
+        for (int m = 0; m < 3 * P; ++m) {
+            const int f = tid + m * TS;
+            if (f < 3 * n) stage[f] = raw[m];
         }
     }
     if (tid == 0) {
         marks[0] = marks[1] = 1u;
         done[0] = done[1] = 0;
     }
-    __syncthreads();  // box partials, cleared counters, marks
+    __syncthreads();  // staged coordinates, cleared counters, marks
+    float lx[P], ly[P], lz[P];
+#pragma unroll
+    for (int k = 0; k < P; ++k) {
+        const int j = min(tid + k * TS, n - 1);
+        lx[k] = sorter ? stage[3 * j] : 0.f;
+        ly[k] = sorter ? stage[3 * j + 1] : 0.f;
+        lz[k] = sorter ? stage[3 * j + 2] : 0.f;
+    }
+    if (sorter) {
+        // Minima of x, y, z and of -x, -y, -z, folded together: the minima
+        // end in lane 0, the negated maxima in lane 32.
+        float v[6];
+        v[0] = v[1] = v[2] = v[3] = v[4] = v[5] = INFINITY;
+#pragma unroll
+        for (int k = 0; k < P; ++k) {
+            v[0] = fminf(v[0], lx[k]); v[3] = fminf(v[3], -lx[k]);
+            v[1] = fminf(v[1], ly[k]); v[4] = fminf(v[4], -ly[k]);
+            v[2] = fminf(v[2], lz[k]); v[5] = fminf(v[5], -lz[k]);
+        }
+        fold_min<6, kWave / 2>(v, lane);
+        if (lane == 0) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) red[a][wave] = v[a];
+        }
+        if (lane == kWave / 2) {
+#pragma unroll
+            for (int a = 0; a < 3; ++a) red[3 + a][wave] = -v[a];
+        }
+    }
+    __syncthreads();  // box partials
     float lo[3], scale[3];
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -793,7 +812,7 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
             for (int b = 0; b < 4; ++b) key |= ((q >> b) & 1u) << (3 * b + a);
         }
         cell[k] = static_cast<int>(key);
-        rank[k] = (sorter && tid * P + k < n) ? atomicAdd(&cell_count[key], 1) : 0;
+        rank[k] = (sorter && tid + k * TS < n) ? atomicAdd(&cell_count[key], 1) : 0;
     }
     __syncthreads();  // counts complete
     {
@@ -826,8 +845,8 @@ __global__ __launch_bounds__(kLeadThreads) void fps_lead_kernel(
     if (sorter) {
 #pragma unroll
         for (int k = 0; k < P; ++k)
-            if (tid * P + k < n)
-                spts[cell_count[cell[k]] + rank[k]] = make_float4(lx[k], ly[k], lz[k], i2f(tid * P + k));
+            if (tid + k * TS < n)
+                spts[cell_count[cell[k]] + rank[k]] = make_float4(lx[k], ly[k], lz[k], i2f(tid + k * TS));
     }
     __syncthreads();  // permutation complete
 
